@@ -1,0 +1,217 @@
+#!/usr/bin/env python
+"""Benchmark of the MI355X selective-scan engine (one JSON line on stdout).
+
+Metric: selective-scan fwd+bwd Mtok/s and % HBM peak at B16 L512 D512 N16
+fp32 (config 1: z gate + D skip, upstream grad dy ~ N(0,1)).  A step is one forward and one
+backward of the fused scan over the batch, inputs resident in HBM.  W untimed warmup steps,
+then exactly K steps between two torch.cuda.synchronize() calls.
+
+Per-entry device times come from HIP events recorded on the launch stream around every
+C-ABI call (ssm_scan.KernelTimer); the dominant entry (ssm_bwd: the backward kernel plus its
+small fixed-order reduction kernel) gives the roofline: algorithmic bytes per launch /
+average duration, against 8 TB/s.  The CPU baseline is the torch-CPU restatement of the
+reference's CPU path (oracle/cpu_chunked.py), timed on a bounded sample of the same workload.
+
+Other workloads (--workload): c0 (forward, B1 L512), c2 (long-sequence forward), c4 (decode
+step), copy (a plain device copy of known size, for PMC counter calibration).
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "mamba-ssm-benchmark_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "selective-scan fwd+bwd Mtok/s and % HBM peak, B16 L512 D512 N16 fp32"
+
+
+def alg_bytes(B, L, D, N, s=4, gate=True, skip=True, last=True):
+    """Algorithmic HBM bytes per pass: every tensor read or written once (workspace excluded).
+    fwd: x, delta, B, C, z read; y written; A, D read; last written.
+    bwd: x, delta, B, C, z, A, D re-read; dy read; dx, ddelta, dz, dB, dC, dA, dD written."""
+    BL = B * L
+    fwd = s * BL * (2 * D + 2 * N) + (s * BL * D if gate else 0) + s * BL * D + 4 * D * N \
+        + (4 * D if skip else 0) + (4 * B * D * N if last else 0)
+    bwd = s * BL * (2 * D + 2 * N) + (s * BL * D if gate else 0) + 4 * D * N + (4 * D if skip else 0) \
+        + s * BL * D + (3 if gate else 2) * s * BL * D + 2 * s * BL * N + 4 * D * N + (4 * D if skip else 0)
+    return fwd, bwd
+
+
+def load_traffic(name):
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def cpu_baseline_c1(t, budget_s=12.0):
+    """Time oracle/cpu_chunked.fwd_bwd on batch row 0 (1 x 512 tokens) of config 1."""
+    from oracle import cpu_chunked
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    rows = slice(0, 1)
+    args = [t[k][rows].contiguous().float() for k in ("u", "delta")] + [t["A"]] + \
+        [t[k][rows].contiguous().float() for k in ("Bm", "Cm")] + [t["D"], t["z"][rows].contiguous(),
+                                                                    t["dy"][rows].contiguous()]
+    cpu_chunked.fwd_bwd(*args)                      # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while reps < 1 or (time.perf_counter() - t0 < budget_s and reps < 10000):
+        cpu_chunked.fwd_bwd(*args)
+        reps += 1
+    dt = time.perf_counter() - t0
+    tokens = args[0].shape[0] * args[0].shape[1] * reps
+    return {"value": tokens / dt / 1e6, "unit": "Mtok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"config-1 batch row 0 (1x512 tokens, D512 N16 fp32, z gate + D skip), fwd+bwd of the "
+                      f"torch-CPU restatement of the reference CPU path (SelectiveScanFn + scan_chunked), "
+                      f"{reps} reps in {dt:.1f} s"}
+
+
+def flush_buffer(dev):
+    return torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
+
+
+def bench_c1(args, dev):
+    import ssm_scan
+    from ssm_scan.synthetic import baseline_inputs
+    B, L, D, N = 16, 512, 512, 16
+    t = baseline_inputs(B, L, D, N, gate=True, with_dy=True)
+    names = ("u", "delta", "A", "Bm", "Cm", "D", "z")
+    leaves = [t[k].to(dev).requires_grad_() for k in names]
+    dy = t["dy"].to(dev)
+
+    def step():
+        out = ssm_scan.selective_scan_fn(leaves[0], leaves[1], leaves[2], leaves[3], leaves[4],
+                                         D=leaves[5], z=leaves[6])
+        return torch.autograd.grad(out, leaves, dy)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    with ssm_scan.KernelTimer() as timer:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    times = timer.times_ms()
+    ms_step = wall * 1e3 / args.steps
+    fwd_ms = statistics.mean(times["ssm_fwd"])
+    bwd_ms = statistics.mean(times["ssm_bwd"])
+    fb, bb = alg_bytes(B, L, D, N)
+
+    # cold caches: flush MALL + L2 with a 512 MB write before each step (flush not timed)
+    flush = flush_buffer(dev)
+    with ssm_scan.KernelTimer() as cold:
+        for _ in range(min(args.steps, 10)):
+            flush.fill_(1.0)
+            step()
+    ct = cold.times_ms()
+    del flush
+    cold_f, cold_b = statistics.mean(ct["ssm_fwd"]), statistics.mean(ct["ssm_bwd"])
+
+    achieved = bb / (bwd_ms * 1e-3) / 1e9
+    rec = {
+        "metric": METRIC,
+        "value": B * L / (ms_step * 1e-3) / 1e6,
+        "unit": "Mtok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "config 1: fused selective-scan fwd+bwd, B16 L512 D512 N16 fp32, "
+                               "zoh, z gate + D skip, channel-major (B,D,L) storage",
+                   "batch": B, "seqlen": L, "dim": D, "dstate": N, "method": "zoh"},
+        "hbm_frac_step": (fb + bb) / (ms_step * 1e-3) / (HBM_PEAK_GBS * 1e9),
+        "kernels_ms": {"ssm_fwd": fwd_ms, "ssm_bwd": bwd_ms, "ssm_fwd_cold": cold_f, "ssm_bwd_cold": cold_b},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic("ssm_bwd_c1"),
+                     "kernel": "ssm_bwd (k_bwd + k_bwd_finalize)", "alg_bytes_per_launch": bb,
+                     "fwd_achieved": fb / (fwd_ms * 1e-3) / 1e9},
+    }
+    if not args.no_cpu_baseline:
+        rec["cpu_baseline"] = cpu_baseline_c1(t)
+    return rec
+
+
+def bench_fwd(args, dev, B, L, dtype, workload):
+    import ssm_scan
+    from ssm_scan.synthetic import baseline_inputs
+    D, N = 512, 16
+    t = baseline_inputs(B, L, D, N, dtype=dtype)
+    ins = [t[k].to(dev) for k in ("u", "delta", "A", "Bm", "Cm")]
+    for _ in range(args.warmup):
+        with torch.no_grad():
+            ssm_scan.selective_scan_hip(*ins)
+    torch.cuda.synchronize()
+    with ssm_scan.KernelTimer() as timer:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            with torch.no_grad():
+                ssm_scan.selective_scan_hip(*ins)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    fwd_ms = statistics.mean(timer.times_ms()["ssm_fwd"])
+    s = torch.tensor([], dtype=dtype).element_size()
+    fb, _ = alg_bytes(B, L, D, N, s=s, gate=False, skip=False)
+    ms = wall * 1e3 / args.steps
+    achieved = fb / (fwd_ms * 1e-3) / 1e9
+    return {"metric": f"selective-scan fwd Mtok/s, {workload}", "value": B * L / (ms * 1e-3) / 1e6,
+            "unit": "Mtok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": {torch.float32: "f32", torch.bfloat16: "bf16"}[dtype], "data": "synthetic",
+            "config": {"workload": workload, "batch": B, "seqlen": L, "dim": D, "dstate": N},
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "ssm_fwd"}}
+
+
+def bench_copy(args, dev):
+    """A plain device copy of 256 MiB (reads 256 MiB, writes 256 MiB): PMC calibration."""
+    src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup + args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"metric": "device copy 256 MiB (PMC calibration)", "value": 256.0, "unit": "MiB",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "copy"])
+    ap.add_argument("--seqlen", type=int, default=131072)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): the hot path here is the "
+              "single-GPU scan kernel; multi-GPU sharding is described in DESIGN.md, not run.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    if args.workload == "c1":
+        rec = bench_c1(args, dev)
+    elif args.workload == "c0":
+        rec = bench_fwd(args, dev, 1, 512, torch.float32, "config 0: fwd B1 L512 D512 N16 fp32")
+    elif args.workload in ("c2", "c2bf16"):
+        dt = torch.bfloat16 if args.workload == "c2bf16" else torch.float32
+        rec = bench_fwd(args, dev, 1, args.seqlen, dt, f"config 2: fwd B1 L{args.seqlen} D512 N16")
+    else:
+        rec = bench_copy(args, dev)
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,238 @@
+/* ssm_scan.h -- C ABI of the MI355X (gfx950) selective-scan engine.
+ *
+ * One shared library, libssmscan.so, built from mamba-ssm-benchmark_amd/csrc/.  Every
+ * entry point takes plain pointers, element strides and sizes; no C++ or framework types
+ * cross the boundary.  The library never allocates device memory and never synchronizes:
+ * callers pass outputs and workspaces (sizes from the *_bytes queries) and a HIP stream
+ * (hipStream_t passed as void*; NULL = the null stream).  Kernels are enqueued on that
+ * stream only.  Calls are re-entrant; the last error message is thread-local.
+ *
+ * Logical layouts follow the reference (models/scan.py:279): x, delta, z, out (B,L,D);
+ * A (D,N); Bm, Cm (B,L,N); h0, last (B,D,N); D skip (D,).  Strides are in elements and
+ * may be anything (including 0 for broadcast, e.g. the scalar-decay A of
+ * models/mamba.py:82-83); the fast path is any tensor whose L or D axis has stride 1.
+ *
+ * Error model (mirrors the reference's Python exceptions):
+ *   SSM_EINVAL  bad argument           -> ValueError  (models/scan.py:55; kernels/triton_scan.py:324-328)
+ *   SSM_EKEY    unknown scan name       -> KeyError    (models/scan.py:261)
+ *   SSM_ESPACE  workspace too small     -> ValueError
+ *   SSM_EHIP    HIP launch/runtime error -> RuntimeError
+ */
+#ifndef SSM_SCAN_H
+#define SSM_SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SSM_ABI_VERSION 1
+
+enum { SSM_OK = 0, SSM_EINVAL = 1, SSM_EKEY = 2, SSM_ESPACE = 3, SSM_EHIP = 4 };
+
+/* Discretizations; the values are the reference's METHODS (kernels/triton_scan.py:23-24). */
+enum { SSM_ZOH = 0, SSM_EULER = 1, SSM_BILINEAR = 2 };
+
+/* Element types.  The state/compute type is float64 when dtype is SSM_F64 and float32
+ * otherwise (the reference computes in promote(dtype, float32), models/scan.py:289). */
+enum { SSM_F32 = 0, SSM_BF16 = 1, SSM_F16 = 2, SSM_F64 = 3 };
+
+/* Scan algorithm ids: the reference's `scan=` names (models/scan.py:281-283, 168-173). */
+enum {
+  SSM_SCAN_REFERENCE = 0,
+  SSM_SCAN_SEQUENTIAL = 1,
+  SSM_SCAN_HILLIS_STEELE = 2,
+  SSM_SCAN_BLELLOCH = 3,
+  SSM_SCAN_CHUNKED = 4,
+  SSM_SCAN_FUSED = 5, /* the reference's 'triton' fused kernels; here the fused HIP engine */
+  SSM_SCAN_AUTO = 6
+};
+
+/* A strided tensor view.  data == NULL means "absent" for optional tensors. */
+typedef struct ssm_tensor {
+  void *data;
+  int64_t stride[3];
+} ssm_tensor;
+
+/* ------------------------------------------------------------------ fused forward
+ * Replaces TritonSelectiveScanFn.forward / _launch_fwd / _fwd_kernel
+ * (kernels/triton_scan.py:27-74, 253-286) and the forward of SelectiveScanFn
+ * (models/scan.py:202-217), with the D skip and SiLU gate of models/mamba.py:124 fused:
+ *   delta' = softplus(delta + delta_bias) (each part optional), h_t = a_t h_{t-1} + b_t,
+ *   y_t = sum_n C_t[n] h_t[n],   out = (y + Dskip * x) * silu(z)   (each part optional). */
+typedef struct ssm_fwd_args {
+  int64_t batch, seqlen, dim, dstate;
+  int32_t method;          /* SSM_ZOH / SSM_EULER / SSM_BILINEAR */
+  int32_t dtype;           /* type of x, delta, Bm, Cm, z, out */
+  ssm_tensor x, delta;     /* (B,L,D) */
+  ssm_tensor A;            /* (D,N), state type */
+  ssm_tensor Bm, Cm;       /* (B,L,N) */
+  ssm_tensor Dskip;        /* (D,) state type, optional */
+  ssm_tensor z;            /* (B,L,D), optional gate */
+  ssm_tensor delta_bias;   /* (D,) state type, optional */
+  int32_t delta_softplus;  /* nonzero: delta' = softplus(delta + bias) */
+  int32_t reserved0;
+  ssm_tensor h0;           /* (B,D,N) state type, optional initial state */
+  ssm_tensor out;          /* (B,L,D) dtype, required */
+  ssm_tensor last;         /* (B,D,N) state type, optional final state */
+  void *saved;             /* optional: ssm_fwd_saved_bytes() of device memory; when given,
+                              the forward stores what ssm_bwd needs (chunk-boundary
+                              states and, with a gate, the pre-gate output) */
+  void *workspace;         /* scratch of ssm_fwd_workspace_bytes() (long-sequence path) */
+  int64_t workspace_bytes;
+} ssm_fwd_args;
+
+/* ------------------------------------------------------------------ fused backward
+ * Replaces TritonSelectiveScanFn.backward / _bwd_kernel (kernels/triton_scan.py:143-226,
+ * 288-319) and SelectiveScanFn.backward (models/scan.py:219-255).  Recomputes states
+ * inside each chunk from the saved chunk-boundary states; every reduction (dA, dB, dC,
+ * dD, ddelta_bias) is done in a fixed order, so results are bitwise reproducible. */
+typedef struct ssm_bwd_args {
+  int64_t batch, seqlen, dim, dstate;
+  int32_t method, dtype;
+  ssm_tensor x, delta, A, Bm, Cm, Dskip, z, delta_bias; /* as in ssm_fwd_args */
+  int32_t delta_softplus;
+  int32_t reserved0;
+  ssm_tensor h0;
+  const void *saved;       /* the `saved` buffer of the matching ssm_fwd call, or NULL
+                              (then the states are recomputed into the workspace) */
+  ssm_tensor dout;         /* (B,L,D) dtype: gradient of out */
+  ssm_tensor dlast;        /* (B,D,N) state type, optional: gradient of last */
+  ssm_tensor dx, ddelta;   /* (B,L,D) dtype; ddelta is w.r.t. the raw delta input */
+  ssm_tensor dA;           /* (D,N) state type */
+  ssm_tensor dBm, dCm;     /* (B,L,N) dtype */
+  ssm_tensor dD;           /* (D,) state type, required iff Dskip */
+  ssm_tensor dz;           /* (B,L,D) dtype, required iff z */
+  ssm_tensor ddelta_bias;  /* (D,) state type, required iff delta_bias */
+  ssm_tensor dh0;          /* (B,D,N) state type, optional (gradient of h0) */
+  void *workspace;         /* ssm_bwd_workspace_bytes() */
+  int64_t workspace_bytes;
+} ssm_bwd_args;
+
+/* ------------------------------------------------------------------ decode step
+ * Replaces the inline recurrent step of Mamba.forward (models/mamba.py:113-118,122-124):
+ *   h <- a h + b (in place),  out = (sum_n C[n] h[n] + Dskip x) * silu(z). */
+typedef struct ssm_step_args {
+  int64_t batch, dim, dstate;
+  int32_t method, dtype;
+  ssm_tensor x, delta;     /* (B,D) */
+  ssm_tensor A;            /* (D,N) state type */
+  ssm_tensor Bm, Cm;       /* (B,N) */
+  ssm_tensor Dskip;        /* (D,) optional */
+  ssm_tensor z;            /* (B,D) optional */
+  ssm_tensor delta_bias;   /* (D,) optional */
+  int32_t delta_softplus;
+  int32_t reserved0;
+  ssm_tensor h;            /* (B,D,N) state type, read and updated in place */
+  ssm_tensor out;          /* (B,D) dtype */
+} ssm_step_args;
+
+/* ------------------------------------------------------------------ linear scans
+ * Replaces the scan algorithms of models/scan.py:70-165 (scan_sequential,
+ * scan_hillis_steele, scan_blelloch, scan_chunked) on (a, b) of shape (B, L, M):
+ *   h_t = a_t h_{t-1} + b_t,  h_{-1} = h0 (or 0).   With reverse != 0 the recurrence
+ * runs from t = L-1 down to 0 (used by the composed backward, models/scan.py:240). */
+typedef struct ssm_lscan_args {
+  int64_t batch, seqlen, width;
+  int32_t algo;            /* SSM_SCAN_SEQUENTIAL .. SSM_SCAN_CHUNKED */
+  int32_t dtype;           /* SSM_F32 or SSM_F64 (a, b, h0, h all this type) */
+  int32_t reverse;
+  int32_t reserved0;
+  int64_t chunk;           /* SSM_SCAN_CHUNKED: chunk size; 0 = ssm_default_chunk(L) */
+  ssm_tensor a, b;         /* (B,L,M) */
+  ssm_tensor h0;           /* (B,M) optional */
+  ssm_tensor h;            /* (B,L,M) output */
+  void *workspace;         /* ssm_lscan_workspace_bytes() */
+  int64_t workspace_bytes;
+} ssm_lscan_args;
+
+/* ------------------------------------------------------------------ discretization
+ * models/scan.py:39-55, materialized: a, b (B,L,D,N), contiguous.  The backward maps
+ * (da, db) to (ddelta, dA, dBm, dx) exactly as autograd does through discretize
+ * (models/scan.py:249). */
+typedef struct ssm_disc_args {
+  int64_t batch, seqlen, dim, dstate;
+  int32_t method, dtype;   /* dtype: SSM_F32 or SSM_F64 for every tensor */
+  ssm_tensor delta, x;     /* (B,L,D) */
+  ssm_tensor A;            /* (D,N) */
+  ssm_tensor Bm;           /* (B,L,N) */
+  void *a, *b;             /* forward outputs (B,L,D,N) contiguous */
+  const void *da, *db;     /* backward inputs (B,L,D,N) contiguous */
+  ssm_tensor ddelta, dx;   /* backward outputs (B,L,D) */
+  ssm_tensor dA;           /* backward output (D,N) */
+  ssm_tensor dBm;          /* backward output (B,L,N) */
+  void *workspace;         /* ssm_disc_workspace_bytes() */
+  int64_t workspace_bytes;
+} ssm_disc_args;
+
+/* ------------------------------------------------------------------ causal depthwise conv
+ * models/mamba.py:101-107: y = silu(conv1d(pad_left(x), w, bias, groups=D)), with the
+ * chronological shift state of :104-106 (the previous width-1 inputs). */
+typedef struct ssm_conv_args {
+  int64_t batch, seqlen, dim, width;
+  int32_t dtype;           /* x, out, dx, dout; weight/bias in float32 (float64 for F64) */
+  int32_t silu;
+  ssm_tensor x;            /* (B,L,D) */
+  ssm_tensor weight;       /* (D,W) */
+  ssm_tensor bias;         /* (D,) optional */
+  ssm_tensor state_in;     /* (B,D,W-1) optional previous inputs (zeros when absent) */
+  ssm_tensor out;          /* (B,L,D) forward output */
+  ssm_tensor state_out;    /* (B,D,W-1) optional: the last W-1 inputs after this call */
+  ssm_tensor dout;         /* backward: (B,L,D) */
+  ssm_tensor dx;           /* backward: (B,L,D) */
+  ssm_tensor dweight;      /* backward: (D,W) float32/64 */
+  ssm_tensor dbias;        /* backward: (D,) optional */
+  void *workspace;         /* ssm_conv_workspace_bytes() */
+  int64_t workspace_bytes;
+} ssm_conv_args;
+
+/* ------------------------------------------------------------------ entry points */
+int ssm_abi_version(void);
+const char *ssm_last_error(void);
+
+/* Host-only argument validation (no device needed).  Returns SSM_OK or an error code. */
+int ssm_fwd_check(const ssm_fwd_args *args);
+int ssm_bwd_check(const ssm_bwd_args *args);
+int ssm_step_check(const ssm_step_args *args);
+int ssm_lscan_check(const ssm_lscan_args *args);
+int ssm_disc_check(const ssm_disc_args *args);
+int ssm_conv_check(const ssm_conv_args *args);
+
+/* Buffer sizes in bytes (host-only). */
+int64_t ssm_fwd_saved_bytes(const ssm_fwd_args *args);
+int64_t ssm_fwd_workspace_bytes(const ssm_fwd_args *args);
+int64_t ssm_bwd_workspace_bytes(const ssm_bwd_args *args);
+int64_t ssm_lscan_workspace_bytes(const ssm_lscan_args *args);
+int64_t ssm_disc_workspace_bytes(const ssm_disc_args *args);
+int64_t ssm_conv_workspace_bytes(const ssm_conv_args *args);
+
+/* Launches (asynchronous on `stream`). */
+int ssm_fwd(const ssm_fwd_args *args, void *stream);
+int ssm_bwd(const ssm_bwd_args *args, void *stream);
+int ssm_step(const ssm_step_args *args, void *stream);
+int ssm_lscan(const ssm_lscan_args *args, void *stream);
+int ssm_disc_fwd(const ssm_disc_args *args, void *stream);
+int ssm_disc_bwd(const ssm_disc_args *args, void *stream);
+int ssm_conv_fwd(const ssm_conv_args *args, void *stream);
+int ssm_conv_bwd(const ssm_conv_args *args, void *stream);
+
+/* ------------------------------------------------------------------ plans (host-only, exact integers)
+ * The reference's integer planning functions, returned bit-exactly. */
+int64_t ssm_default_chunk(int64_t seqlen);                        /* models/scan.py:138-139 */
+int64_t ssm_scan_blocks(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
+                        int64_t d_block, int64_t *bounds, int64_t capacity);
+                                                                  /* models/scan.py:185-190; writes
+                                                                     (start, end) pairs, returns count */
+int64_t ssm_block_d(int64_t batch, int64_t dim);                  /* kernels/triton_scan.py:245-250 */
+int64_t ssm_bwd_tile(int64_t batch, int64_t seqlen, int64_t dstate, int64_t block_d);
+                                                                  /* kernels/triton_scan.py:305 */
+int32_t ssm_resolve_scan(int32_t scan_id, int32_t on_gpu, int32_t method, int64_t dstate,
+                         int32_t engine_available);               /* models/scan.py:286-287, 305-314;
+                                                                     -1 for an unknown id */
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SSM_SCAN_H */

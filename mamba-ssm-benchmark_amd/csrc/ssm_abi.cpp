@@ -1,0 +1,364 @@
+// extern "C" entry points of libssmscan.so (declared in include/ssm_scan.h).
+//
+// Host-only work lives here: argument validation (callable without a device, so the error
+// paths are testable on a CPU host), workspace sizing, the integer planning functions of the
+// reference, and dispatch to the kernel launchers.  No device memory is allocated and no
+// stream is synchronized.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/ssm_scan.h"
+#include "ssm_internal.hpp"
+
+using namespace ssm;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = 0;
+  return SSM_OK;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(SSM_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+int state_size(int dtype) { return dtype == SSM_F64 ? 8 : 4; }
+
+KView kv(const ssm_tensor &t) { return KView{t.data, t.stride[0], t.stride[1], t.stride[2]}; }
+bool has(const ssm_tensor &t) { return t.data != nullptr; }
+
+const char *method_name(int m) { return m == 0 ? "zoh" : m == 1 ? "euler" : m == 2 ? "bilinear" : "?"; }
+
+int check_common(int64_t B, int64_t L, int64_t D, int64_t N, int method, int dtype) {
+  if (method < 0 || method > 2)
+    return fail(SSM_EINVAL, "unknown discretization %d (expected zoh=0, euler=1, bilinear=2)", method);
+  if (dtype < 0 || dtype > 3) return fail(SSM_EINVAL, "unsupported dtype code %d", dtype);
+  if (B < 1 || L < 1 || D < 1 || N < 1)
+    return fail(SSM_EINVAL, "empty problem: batch=%lld seqlen=%lld dim=%lld dstate=%lld", (long long)B,
+                (long long)L, (long long)D, (long long)N);
+  if (N > 64) return fail(SSM_EINVAL, "dstate=%lld > 64 is not supported", (long long)N);
+  if (B > 65535) return fail(SSM_EINVAL, "batch=%lld > 65535 is not supported", (long long)B);
+  if (L > (1LL << 30) || D > (1LL << 30))
+    return fail(SSM_EINVAL, "seqlen/dim must be < 2^30");
+  return SSM_OK;
+}
+
+#define REQUIRE(t, name)                                                        \
+  do {                                                                          \
+    if (!has(t)) return fail(SSM_EINVAL, "required tensor '%s' is missing", name); \
+  } while (0)
+
+// True when every present (B,L,D) view has x's strides, Cm has Bm's, and every element offset
+// inside one batch row fits in a signed 32-bit integer (the kernels' fast addressing).
+bool same3(const ssm_tensor &a, const ssm_tensor &b) {
+  return !has(a) || (a.stride[0] == b.stride[0] && a.stride[1] == b.stride[1] && a.stride[2] == b.stride[2]);
+}
+bool row_fits(const ssm_tensor &t, int64_t L, int64_t C) {
+  const int64_t lim = (int64_t)1 << 30;
+  const int64_t s1 = t.stride[1] < 0 ? -t.stride[1] : t.stride[1];
+  const int64_t s2 = t.stride[2] < 0 ? -t.stride[2] : t.stride[2];
+  return s1 < lim && s2 < lim && (L - 1) * s1 + (C - 1) * s2 + C < lim;
+}
+bool uniform_layout(const ssm_tensor *bld[], int nbld, const ssm_tensor &Bm, const ssm_tensor &Cm, int64_t L,
+                    int64_t D, int64_t N) {
+  for (int i = 0; i < nbld; ++i)
+    if (!same3(*bld[i], *bld[0])) return false;
+  return same3(Cm, Bm) && row_fits(*bld[0], L, D) && row_fits(Bm, L, N);
+}
+
+struct FwdLayout {
+  int np, ck, nchunks;
+  int64_t ckpt_bytes, ypre_bytes;
+};
+
+FwdLayout fwd_layout(int64_t B, int64_t L, int64_t D, int64_t N, int dtype, bool gate) {
+  FwdLayout f;
+  f.np = padded_n(N);
+  f.ck = chunk_steps(dtype);
+  f.nchunks = (int)cdiv(L, f.ck);
+  f.ckpt_bytes = align256(B * f.nchunks * D * f.np * state_size(dtype));
+  f.ypre_bytes = gate ? align256(B * L * D * state_size(dtype)) : 0;
+  return f;
+}
+
+struct BwdLayout {
+  FwdLayout f;
+  int ntiles;
+  int64_t saved, dB, dC, dA, dD, db, total;  // byte offsets
+};
+
+BwdLayout bwd_layout(const ssm_bwd_args *a) {
+  BwdLayout w;
+  w.f = fwd_layout(a->batch, a->seqlen, a->dim, a->dstate, a->dtype, has(a->z));
+  const int ss = state_size(a->dtype);
+  w.ntiles = (int)cdiv(a->dim, bwd_channels_per_block(a->dtype, w.f.np));
+  int64_t off = 0;
+  w.saved = off;
+  if (!a->saved) off += w.f.ckpt_bytes + w.f.ypre_bytes;
+  const int64_t part = align256(a->batch * w.ntiles * a->seqlen * w.f.np * ss);
+  w.dB = off; off += part;
+  w.dC = off; off += part;
+  w.dA = off; off += align256(a->batch * a->dim * w.f.np * ss);
+  w.dD = off; off += align256(a->batch * a->dim * ss);
+  w.db = off; off += align256(a->batch * a->dim * ss);
+  w.total = off;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ssm_abi_version(void) { return SSM_ABI_VERSION; }
+const char *ssm_last_error(void) { return g_err; }
+
+// ------------------------------------------------------------------ fused forward
+int ssm_fwd_check(const ssm_fwd_args *a) {
+  if (!a) return fail(SSM_EINVAL, "null args");
+  int rc = check_common(a->batch, a->seqlen, a->dim, a->dstate, a->method, a->dtype);
+  if (rc) return rc;
+  REQUIRE(a->x, "x");
+  REQUIRE(a->delta, "delta");
+  REQUIRE(a->A, "A");
+  REQUIRE(a->Bm, "Bm");
+  REQUIRE(a->Cm, "Cm");
+  REQUIRE(a->out, "out");
+  return ok();
+}
+
+int64_t ssm_fwd_saved_bytes(const ssm_fwd_args *a) {
+  if (ssm_fwd_check(a)) return -1;
+  FwdLayout f = fwd_layout(a->batch, a->seqlen, a->dim, a->dstate, a->dtype, has(a->z));
+  return f.ckpt_bytes + f.ypre_bytes;
+}
+
+int64_t ssm_fwd_workspace_bytes(const ssm_fwd_args *a) {
+  if (ssm_fwd_check(a)) return -1;
+  return 0;
+}
+
+static void fill_fwd(FwdParams &p, const ssm_fwd_args *a, const FwdLayout &f) {
+  memset(&p, 0, sizeof(p));
+  p.B = a->batch; p.L = a->seqlen; p.D = a->dim; p.N = a->dstate;
+  p.nchunks = f.nchunks;
+  p.softplus = a->delta_softplus != 0;
+  p.has_D = has(a->Dskip); p.has_z = has(a->z); p.has_bias = has(a->delta_bias);
+  p.has_h0 = has(a->h0); p.has_last = has(a->last); p.write_out = 1;
+  p.x = kv(a->x); p.dt = kv(a->delta); p.A = kv(a->A); p.Bm = kv(a->Bm); p.Cm = kv(a->Cm);
+  p.Dsk = kv(a->Dskip); p.z = kv(a->z); p.bias = kv(a->delta_bias); p.h0 = kv(a->h0);
+  p.out = kv(a->out); p.last = kv(a->last);
+  const ssm_tensor *bld[] = {&a->x, &a->delta, &a->z, &a->out};
+  p.uniform = uniform_layout(bld, 4, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate);
+}
+
+int ssm_fwd(const ssm_fwd_args *a, void *stream) {
+  int rc = ssm_fwd_check(a);
+  if (rc) return rc;
+  FwdLayout f = fwd_layout(a->batch, a->seqlen, a->dim, a->dstate, a->dtype, has(a->z));
+  FwdParams p;
+  fill_fwd(p, a, f);
+  if (a->saved) {
+    p.ckpt = a->saved;
+    p.ypre = has(a->z) ? (char *)a->saved + f.ckpt_bytes : nullptr;
+  }
+  hipError_t e = launch_fwd(p, a->dtype, a->method, f.np, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "ssm_fwd launch");
+  return ok();
+}
+
+// ------------------------------------------------------------------ fused backward
+int ssm_bwd_check(const ssm_bwd_args *a) {
+  if (!a) return fail(SSM_EINVAL, "null args");
+  int rc = check_common(a->batch, a->seqlen, a->dim, a->dstate, a->method, a->dtype);
+  if (rc) return rc;
+  REQUIRE(a->x, "x");
+  REQUIRE(a->delta, "delta");
+  REQUIRE(a->A, "A");
+  REQUIRE(a->Bm, "Bm");
+  REQUIRE(a->Cm, "Cm");
+  REQUIRE(a->dout, "dout");
+  REQUIRE(a->dx, "dx");
+  REQUIRE(a->ddelta, "ddelta");
+  REQUIRE(a->dA, "dA");
+  REQUIRE(a->dBm, "dBm");
+  REQUIRE(a->dCm, "dCm");
+  if (has(a->Dskip)) REQUIRE(a->dD, "dD");
+  if (has(a->z)) REQUIRE(a->dz, "dz");
+  if (has(a->delta_bias)) REQUIRE(a->ddelta_bias, "ddelta_bias");
+  if (has(a->dh0) && !has(a->h0)) return fail(SSM_EINVAL, "dh0 given without h0");
+  return ok();
+}
+
+int64_t ssm_bwd_workspace_bytes(const ssm_bwd_args *a) {
+  if (ssm_bwd_check(a)) return -1;
+  return bwd_layout(a).total;
+}
+
+int ssm_bwd(const ssm_bwd_args *a, void *stream) {
+  int rc = ssm_bwd_check(a);
+  if (rc) return rc;
+  BwdLayout w = bwd_layout(a);
+  if (!a->workspace || a->workspace_bytes < w.total)
+    return fail(SSM_ESPACE, "workspace of %lld bytes is smaller than the %lld required",
+                (long long)a->workspace_bytes, (long long)w.total);
+  hipStream_t s = (hipStream_t)stream;
+  char *ws = (char *)a->workspace;
+  const void *ckpt = a->saved;
+  const void *ypre = a->saved && has(a->z) ? (const char *)a->saved + w.f.ckpt_bytes : nullptr;
+  if (!a->saved) {  // recompute the chunk-boundary states (and the pre-gate output)
+    ssm_fwd_args fa;
+    memset(&fa, 0, sizeof(fa));
+    fa.batch = a->batch; fa.seqlen = a->seqlen; fa.dim = a->dim; fa.dstate = a->dstate;
+    fa.method = a->method; fa.dtype = a->dtype;
+    fa.x = a->x; fa.delta = a->delta; fa.A = a->A; fa.Bm = a->Bm; fa.Cm = a->Cm;
+    fa.Dskip = a->Dskip; fa.z = a->z; fa.delta_bias = a->delta_bias;
+    fa.delta_softplus = a->delta_softplus; fa.h0 = a->h0;
+    fa.out = a->x;  // placeholder with x's layout, never written (write_out = 0)
+    FwdParams fp;
+    fill_fwd(fp, &fa, w.f);
+    fp.write_out = 0;
+    fp.has_last = 0;
+    fp.ckpt = ws + w.saved;
+    fp.ypre = has(a->z) ? ws + w.saved + w.f.ckpt_bytes : nullptr;
+    hipError_t e = launch_fwd(fp, a->dtype, a->method, w.f.np, s);
+    if (e != hipSuccess) return hip_fail(e, "ssm_bwd state recompute launch");
+    ckpt = fp.ckpt;
+    ypre = fp.ypre;
+  }
+  BwdParams p;
+  memset(&p, 0, sizeof(p));
+  p.B = a->batch; p.L = a->seqlen; p.D = a->dim; p.N = a->dstate;
+  p.nchunks = w.f.nchunks; p.ntiles = w.ntiles;
+  p.softplus = a->delta_softplus != 0;
+  p.has_D = has(a->Dskip); p.has_z = has(a->z); p.has_bias = has(a->delta_bias);
+  p.has_h0 = has(a->h0); p.has_dlast = has(a->dlast); p.has_dh0 = has(a->dh0);
+  p.x = kv(a->x); p.dt = kv(a->delta); p.A = kv(a->A); p.Bm = kv(a->Bm); p.Cm = kv(a->Cm);
+  p.Dsk = kv(a->Dskip); p.z = kv(a->z); p.bias = kv(a->delta_bias); p.h0 = kv(a->h0);
+  p.dout = kv(a->dout); p.dlast = kv(a->dlast); p.dx = kv(a->dx); p.ddt = kv(a->ddelta);
+  p.dz = kv(a->dz); p.dh0 = kv(a->dh0);
+  p.ckpt = ckpt; p.ypre = ypre;
+  const ssm_tensor *bld[] = {&a->x, &a->delta, &a->z, &a->dout, &a->dx, &a->ddelta, &a->dz};
+  p.uniform = uniform_layout(bld, 7, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate);
+  p.ws_dB = ws + w.dB; p.ws_dC = ws + w.dC; p.ws_dA = ws + w.dA; p.ws_dD = ws + w.dD; p.ws_db = ws + w.db;
+  hipError_t e = launch_bwd(p, a->dtype, a->method, w.f.np, s);
+  if (e != hipSuccess) return hip_fail(e, "ssm_bwd launch");
+  FinParams fin;
+  memset(&fin, 0, sizeof(fin));
+  fin.B = a->batch; fin.L = a->seqlen; fin.D = a->dim; fin.N = a->dstate;
+  fin.ntiles = w.ntiles; fin.np = w.f.np;
+  fin.has_D = has(a->Dskip); fin.has_bias = has(a->delta_bias);
+  fin.ws_dB = p.ws_dB; fin.ws_dC = p.ws_dC; fin.ws_dA = p.ws_dA; fin.ws_dD = p.ws_dD; fin.ws_db = p.ws_db;
+  fin.dB = kv(a->dBm); fin.dC = kv(a->dCm); fin.dA = kv(a->dA); fin.dD = kv(a->dD); fin.dbias = kv(a->ddelta_bias);
+  e = launch_bwd_finalize(fin, a->dtype, s);
+  if (e != hipSuccess) return hip_fail(e, "ssm_bwd finalize launch");
+  return ok();
+}
+
+// ------------------------------------------------------------------ decode step
+int ssm_step_check(const ssm_step_args *a) {
+  if (!a) return fail(SSM_EINVAL, "null args");
+  int rc = check_common(a->batch, 1, a->dim, a->dstate, a->method, a->dtype);
+  if (rc) return rc;
+  REQUIRE(a->x, "x");
+  REQUIRE(a->delta, "delta");
+  REQUIRE(a->A, "A");
+  REQUIRE(a->Bm, "Bm");
+  REQUIRE(a->Cm, "Cm");
+  REQUIRE(a->h, "h");
+  REQUIRE(a->out, "out");
+  return ok();
+}
+
+int ssm_step(const ssm_step_args *a, void *stream) {
+  int rc = ssm_step_check(a);
+  if (rc) return rc;
+  StepParams p;
+  memset(&p, 0, sizeof(p));
+  p.B = a->batch; p.D = a->dim; p.N = a->dstate;
+  p.softplus = a->delta_softplus != 0;
+  p.has_D = has(a->Dskip); p.has_z = has(a->z); p.has_bias = has(a->delta_bias);
+  p.x = kv(a->x); p.dt = kv(a->delta); p.A = kv(a->A); p.Bm = kv(a->Bm); p.Cm = kv(a->Cm);
+  p.Dsk = kv(a->Dskip); p.z = kv(a->z); p.bias = kv(a->delta_bias); p.h = kv(a->h); p.out = kv(a->out);
+  hipError_t e = launch_step(p, a->dtype, a->method, padded_n(a->dstate), (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "ssm_step launch");
+  return ok();
+}
+
+// ------------------------------------------------------------------ plans
+int64_t ssm_default_chunk(int64_t L) {
+  // max(4, 2^ceil(log2(sqrt(L)))) == max(4, smallest 2^k with 4^k >= L), in exact integers
+  if (L < 0) return -1;
+  int k = 0;
+  while (k < 31 && (int64_t)1 << (2 * k) < L) ++k;
+  int64_t c = (int64_t)1 << k;
+  return c < 4 ? 4 : c;
+}
+
+int64_t ssm_scan_blocks(int64_t B, int64_t L, int64_t D, int64_t N, int64_t d_block, int64_t *bounds,
+                        int64_t capacity) {
+  if (B < 1 || L < 1 || D < 1 || N < 1) return -1;
+  if (d_block <= 0) {
+    d_block = ((int64_t)1 << 24) / (B * L * N);
+    if (d_block < 1) d_block = 1;
+  }
+  if (d_block > D) d_block = D;
+  int64_t count = cdiv(D, d_block);
+  if (bounds) {
+    for (int64_t i = 0, j = 0; i < D && j < capacity; i += d_block, ++j) {
+      bounds[2 * j] = i;
+      bounds[2 * j + 1] = i + d_block < D ? i + d_block : D;
+    }
+  }
+  return count;
+}
+
+int64_t ssm_block_d(int64_t B, int64_t D) {
+  int64_t bd = 16;
+  while (bd > 4 && B * cdiv(D, bd) < 128) bd /= 2;
+  return bd;
+}
+
+int64_t ssm_bwd_tile(int64_t B, int64_t L, int64_t N, int64_t bd) {
+  if (B < 1 || L < 1 || N < 1 || bd < 1) return -1;
+  int64_t t = (((int64_t)1 << 27) / (B * L * N)) / bd * bd;
+  return t > bd ? t : bd;
+}
+
+int32_t ssm_resolve_scan(int32_t scan_id, int32_t on_gpu, int32_t method, int64_t N, int32_t engine) {
+  if (scan_id == SSM_SCAN_AUTO) {
+    bool ok_ = engine && on_gpu && method >= 0 && method <= 2 && (N & (N - 1)) == 0;
+    return ok_ ? SSM_SCAN_FUSED : SSM_SCAN_CHUNKED;
+  }
+  if (scan_id < 0 || scan_id > SSM_SCAN_FUSED) return -1;
+  return scan_id;
+}
+
+// ------------------------------------------------------------------ not yet available
+int ssm_lscan_check(const ssm_lscan_args *a) { (void)a; return fail(SSM_EINVAL, "ssm_lscan: not built in this library version"); }
+int64_t ssm_lscan_workspace_bytes(const ssm_lscan_args *a) { (void)a; return -1; }
+int ssm_lscan(const ssm_lscan_args *a, void *s) { (void)s; return ssm_lscan_check(a); }
+int ssm_disc_check(const ssm_disc_args *a) { (void)a; return fail(SSM_EINVAL, "ssm_disc: not built in this library version"); }
+int64_t ssm_disc_workspace_bytes(const ssm_disc_args *a) { (void)a; return -1; }
+int ssm_disc_fwd(const ssm_disc_args *a, void *s) { (void)s; return ssm_disc_check(a); }
+int ssm_disc_bwd(const ssm_disc_args *a, void *s) { (void)s; return ssm_disc_check(a); }
+int ssm_conv_check(const ssm_conv_args *a) { (void)a; return fail(SSM_EINVAL, "ssm_conv: not built in this library version"); }
+int64_t ssm_conv_workspace_bytes(const ssm_conv_args *a) { (void)a; return -1; }
+int ssm_conv_fwd(const ssm_conv_args *a, void *s) { (void)s; return ssm_conv_check(a); }
+int ssm_conv_bwd(const ssm_conv_args *a, void *s) { (void)s; return ssm_conv_check(a); }
+
+}  // extern "C"

@@ -1,0 +1,401 @@
+// Fused selective-scan backward for gfx950.
+//
+// Replaces kernels/triton_scan.py:143-226 (_bwd_kernel) + :288-319 (host orchestration) and
+// the backward of models/scan.py:219-255.  Same wavefront-private mapping as the forward (one
+// lane per (channel, state), CW = 64/NP channels per wavefront), walking chunks of CK steps
+// from the last to the first:
+//   stage     x, delta (bias/softplus applied), dy = dout * silu(z), B, C into the wavefront's
+//             LDS region; dz is produced here from the saved pre-gate output (per (t, d)).
+//   recompute the chunk's states from the saved chunk-start state, keeping h_t, a_t and the
+//             b-coefficient of all CK steps in VGPRs (no (B, L, D, N) buffer anywhere).
+//   reverse   the adjoint recurrence dh_t = dy_t C_t + a_{t+1} dh_{t+1} (float64); per step each
+//             lane forms its contributions to dx, ddelta (summed over the states inside the
+//             wavefront) and dB, dC (summed over the wavefront's channels, then over the
+//             workgroup's wavefronts with one workgroup barrier per chunk).  dA is accumulated
+//             per lane in a VGPR over the whole sequence.
+//   store     dx (+ D skip), ddelta (x sigmoid for softplus) with coalesced writes; per-tile
+//             dB / dC partials to the workspace.
+// The finalize kernel sums the dB / dC partials over channel tiles and dA / dD / d_bias over
+// the batch, in a fixed order (bitwise reproducible; no float atomics).
+#include "ssm_device.hpp"
+#include "ssm_internal.hpp"
+#include "ssm_tiles.hpp"
+#include "ssm_wave.hpp"
+
+namespace ssm {
+
+template <typename CT, int NP>
+struct BwdWaveLds {
+  static constexpr int CW = kWave / NP, CK = kCK, CKP = ck_pad((int)sizeof(CT)), RH = bwd_half();
+  CT x[CW][CKP];
+  CT dt[CW][CKP];
+  CT dy[CW][CKP];
+  CT sg[CW][CKP];
+  CT gx[CW][CKP];
+  CT gd[CW][CKP];
+  CT B[NP][CKP];
+  CT C[NP][CKP];
+  CT pn[RH][CW][NP][2];  // (dx, ddelta) per-lane contributions
+  CT pd[RH][CW][NP][2];  // (dB, dC) per-lane contributions
+};
+
+template <typename CT, int NP, int WPB>
+struct BwdShared {
+  CT dbc[2][WPB][kCK][NP][2];  // per-wavefront (dB, dC) sums, double-buffered by chunk parity
+};
+template <typename CT, int NP>
+struct BwdShared<CT, NP, 1> {};
+
+template <typename IT, int NP, int METHOD, bool UL>
+__global__ void __launch_bounds__(kWave * bwd_waves(sizeof(typename Conv<IT>::CT), NP))
+k_bwd(const BwdParams p) {
+  typedef typename Conv<IT>::CT CT;
+  typedef BwdWaveLds<CT, NP> WL;
+  constexpr int CW = WL::CW, CK = WL::CK, RH = WL::RH;
+  constexpr int WPB = bwd_waves(sizeof(CT), NP);
+  constexpr int RB = 32 / (int)sizeof(CT) > RH ? RH : 32 / (int)sizeof(CT);  // register batch
+  constexpr int NT = WPB * kWave;
+  static_assert(sizeof(WL) == bwd_wave_bytes(sizeof(CT), NP), "LDS layout");
+  static_assert(RH % RB == 0 && CK % RH == 0, "batches");
+  __shared__ __align__(16) WL lds_all[WPB];
+  __shared__ __align__(16) BwdShared<CT, NP, WPB> sh;
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave, wv = tid / kWave;
+  WL &S = lds_all[wv];
+  const int c = lane / NP, n = lane % NP;
+  const int64_t b = blockIdx.y;
+  const int tile = blockIdx.x;
+  const int dw = (tile * WPB + wv) * CW;
+  const int d = dw + c;
+  const bool dval = d < p.D, nval = n < p.N;
+  const int L = (int)p.L, D = (int)p.D, N = (int)p.N;
+
+  CT Av = (CT)-1;
+  if (dval && nval) Av = vload<CT>(p.A, d * p.A.s0 + n * p.A.s1);
+  const AConst<CT> ac = make_aconst(Av);
+  // The adjoint state is carried in float64: dh_t = a_{t+1} dh_{t+1} + dy_t C_t is a long,
+  // slowly decaying accumulation (a -> 1 for small delta) and its float32 rounding dominates the
+  // error of ddelta, which sums the state terms with cancellation.  One v_fma_f64 per step keeps
+  // it at a single float64 rounding; dlast enters as "a_L dh_L" with a_L = 1.
+  double dh64 = 0.0;
+  if (p.has_dlast && dval && nval)
+    dh64 = (double)vload<CT>(p.dlast, b * p.dlast.s0 + d * p.dlast.s1 + n * p.dlast.s2);
+  CT a_next = 1;
+  CT h0v = 0;
+  if (p.has_h0 && dval && nval) h0v = vload<CT>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
+  CT dA_acc = 0;
+  CT dD_acc = 0, db_acc = 0;  // lanes < CW: channel dw + lane
+
+  const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = with_layout<UL>(p.z, p.x);
+  const KView vg = with_layout<UL>(p.dout, p.x), vdz = with_layout<UL>(p.dz, p.x);
+  const KView vdx = with_layout<UL>(p.dx, p.x), vddt = with_layout<UL>(p.ddt, p.x);
+  const KView vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
+  const bool xt = vx.s1 == 1, dtt = vdt.s1 == 1, bt = vB.s1 == 1, ctt = vC.s1 == 1;
+  const bool gt = vg.s1 == 1, dxt = vdx.s1 == 1, ddtt = vddt.s1 == 1;
+  const CT *ypre = (const CT *)p.ypre;
+
+  for (int k = p.nchunks - 1; k >= 0; --k) {
+    const int t0 = k * CK;
+    const int buf = k & 1;
+    // ---------------------------------------------------------------- stage
+    {
+      WaveTile<IT, CT, CK, CW, UL> tx, tdt;
+      WaveTile<IT, CT, CK, NP, UL> tB, tC;
+      tx.load(vx, b, t0, L, dw, D, xt, lane);
+      tdt.load(vdt, b, t0, L, dw, D, dtt, lane);
+      tB.load(vB, b, t0, L, 0, N, bt, lane);
+      tC.load(vC, b, t0, L, 0, N, ctt, lane);
+      tx.store(S.x, xt, lane);
+      store_delta_w<IT, CT, CK, CW, WL::CKP, UL>(tdt, S.dt, S.sg, dtt, lane, p.has_bias, p.softplus, p.bias, dw, D,
+                                              t0, L);
+      tB.store(S.B, bt, lane);
+      tC.store(S.C, ctt, lane);
+      // dy = dout * silu(z); dz = dout * (y + D x) * silu'(z), from the saved pre-gate output
+#pragma unroll
+      for (int i = 0; i < (CK * CW + kWave - 1) / kWave; ++i) {
+        const int e = lane + i * kWave;
+        if (e >= CK * CW) break;
+        int t, cc;
+        tc_of<CK, CW>(e, gt, t, cc);
+        const int tg = t0 + t, dd = dw + cc;
+        CT g = 0;
+        if (tg < L && dd < D) {
+          g = Conv<IT>::load(vp<IT>(vg) + b * vg.s0 + row_off<UL>(tg, dd, vg.s1, vg.s2));
+          if (p.has_z) {
+            const CT zv = Conv<IT>::load(vp<IT>(vz) + b * vz.s0 + row_off<UL>(tg, dd, vz.s1, vz.s2));
+            const CT sgz = sigmoid_ct<CT>(zv);
+            const CT yp = ypre[ypre_index(!xt, b, tg, dd, p.L, p.D)];
+            Conv<IT>::store(vpw<IT>(vdz) + b * vdz.s0 + row_off<UL>(tg, dd, vdz.s1, vdz.s2),
+                            g * yp * sgz * ((CT)1 + zv * ((CT)1 - sgz)));
+            g = g * zv * sgz;
+          }
+        }
+        S.dy[cc][t] = g;
+      }
+    }
+    wave_lds_sync();
+
+    // ---------------------------------------------------------------- recompute states
+    CT hh[CK + 1], aa[CK], cc_[CK];
+    if (k == 0) hh[0] = h0v;
+    else hh[0] = dval ? ((const CT *)p.ckpt)[((b * p.nchunks + (k - 1)) * p.D + d) * NP + n] : (CT)0;
+    {
+      CT rdt[RB], rx[RB], rB[RB];
+      lds_row(&S.dt[c][0], rdt);
+      lds_row(&S.x[c][0], rx);
+      lds_row(&S.B[n][0], rB);
+#pragma unroll
+      for (int q = 0; q < CK / RB; ++q) {
+        CT bx[RB];
+#pragma unroll
+        for (int tt = 0; tt < RB; ++tt) {
+          const int t = q * RB + tt;
+          disc<METHOD>(rdt[tt], ac, aa[t], cc_[t]);
+          bx[tt] = bcoef<METHOD>(rdt[tt], cc_[t]) * (rB[tt] * rx[tt]);
+        }
+        if (q + 1 < CK / RB) {
+          lds_row(&S.dt[c][(q + 1) * RB], rdt);
+          lds_row(&S.x[c][(q + 1) * RB], rx);
+          lds_row(&S.B[n][(q + 1) * RB], rB);
+        }
+#pragma unroll
+        for (int tt = 0; tt < RB; ++tt) hh[q * RB + tt + 1] = fma(aa[q * RB + tt], hh[q * RB + tt], bx[tt]);
+      }
+    }
+
+    // ---------------------------------------------------------------- reverse walk
+#pragma unroll
+    for (int half = CK / RH - 1; half >= 0; --half) {
+      CT rdt[RB], rx[RB], rdy[RB], rB[RB], rC[RB];
+#pragma unroll
+      for (int q = RH / RB - 1; q >= 0; --q) {
+        const int tb = half * RH + q * RB;  // first step of the batch
+        lds_row(&S.dt[c][tb], rdt);
+        lds_row(&S.x[c][tb], rx);
+        lds_row(&S.dy[c][tb], rdy);
+        lds_row(&S.B[n][tb], rB);
+        lds_row(&S.C[n][tb], rC);
+#pragma unroll
+        for (int tt = RB - 1; tt >= 0; --tt) {
+          const int t = tb + tt;
+          const int slot = t - half * RH;
+          const CT dtv = rdt[tt], xv = rx[tt], dyv = rdy[tt], Bv = rB[tt], Cv = rC[tt];
+          dh64 = fma(dh64, (double)a_next, (double)(dyv * Cv));
+          const CT dh = (CT)dh64;
+          a_next = aa[t];
+          const CT pC = dyv * hh[t + 1];
+          const CT da = dh * hh[t];
+          const CT dhc = dh * bcoef<METHOD>(dtv, cc_[t]);
+          const CT px = dhc * Bv;
+          const CT pB = dhc * xv;
+          const CT dhBx = dh * (Bv * xv);
+          CT dadz, dbdd, d2f;
+          dfactors<METHOD>(dtv, ac, aa[t], cc_[t], dadz, dbdd, d2f);
+          const CT g1 = da * dadz;
+          const CT pD = fma(g1, ac.A, dhBx * dbdd);
+          dA_acc = fma(dtv, g1, fma(dhBx, d2f, dA_acc));
+          S.pn[slot][c][n][0] = px;
+          S.pn[slot][c][n][1] = pD;
+          S.pd[slot][c][n][0] = pB;
+          S.pd[slot][c][n][1] = pC;
+        }
+      }
+      wave_lds_sync();
+      // (dx, ddelta): sum over the NP states of a channel
+#pragma unroll
+      for (int i = 0; i < (RH * CW + kWave - 1) / kWave; ++i) {
+        const int e = lane + i * kWave;
+        if (e >= RH * CW) break;
+        const int tt = e / CW, cn = e % CW;
+        CT part[2 * NP];
+        lds_row(&S.pn[tt][cn][0][0], part);
+        CT sx = 0, sd = 0;
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+          sx += part[2 * j];
+          sd += part[2 * j + 1];
+        }
+        S.gx[cn][half * RH + tt] = sx;
+        S.gd[cn][half * RH + tt] = sd;
+      }
+      // (dB, dC): sum over the wavefront's CW channels
+#pragma unroll
+      for (int i = 0; i < (RH * NP + kWave - 1) / kWave; ++i) {
+        const int e = lane + i * kWave;
+        if (e >= RH * NP) break;
+        const int tt = e / NP, nn = e % NP;
+        CT sb = 0, sc = 0;
+#pragma unroll
+        for (int j = 0; j < CW; ++j) {
+          sb += S.pd[tt][j][nn][0];
+          sc += S.pd[tt][j][nn][1];
+        }
+        const int t = half * RH + tt;
+        if constexpr (WPB > 1) {
+          sh.dbc[buf][wv][t][nn][0] = sb;
+          sh.dbc[buf][wv][t][nn][1] = sc;
+        } else {
+          if (t0 + t < L) {
+            const int64_t off = ((b * p.ntiles + tile) * p.L + t0 + t) * NP + nn;
+            ((CT *)p.ws_dB)[off] = sb;
+            ((CT *)p.ws_dC)[off] = sc;
+          }
+        }
+      }
+      wave_lds_sync();
+    }
+
+    // ---------------------------------------------------------------- store
+#pragma unroll
+    for (int i = 0; i < (CK * CW + kWave - 1) / kWave; ++i) {
+      const int e = lane + i * kWave;
+      if (e >= CK * CW) break;
+      int t, cc;
+      tc_of<CK, CW>(e, dxt, t, cc);
+      const int tg = t0 + t, dd = dw + cc;
+      if (tg >= L || dd >= D) continue;
+      CT gx = S.gx[cc][t];
+      if (p.has_D) gx += S.dy[cc][t] * vload<CT>(p.Dsk, dd * p.Dsk.s0);
+      Conv<IT>::store(vpw<IT>(vdx) + b * vdx.s0 + row_off<UL>(tg, dd, vdx.s1, vdx.s2), gx);
+    }
+#pragma unroll
+    for (int i = 0; i < (CK * CW + kWave - 1) / kWave; ++i) {
+      const int e = lane + i * kWave;
+      if (e >= CK * CW) break;
+      int t, cc;
+      tc_of<CK, CW>(e, ddtt, t, cc);
+      const int tg = t0 + t, dd = dw + cc;
+      if (tg >= L || dd >= D) continue;
+      Conv<IT>::store(vpw<IT>(vddt) + b * vddt.s0 + row_off<UL>(tg, dd, vddt.s1, vddt.s2),
+                      S.gd[cc][t] * S.sg[cc][t]);
+    }
+    if (lane < CW) {
+#pragma unroll
+      for (int t = 0; t < CK; ++t) {
+        if (t0 + t < L) {
+          dD_acc = fma(S.dy[lane][t], S.x[lane][t], dD_acc);
+          db_acc = fma(S.gd[lane][t], S.sg[lane][t], db_acc);
+        }
+      }
+    }
+    if constexpr (WPB > 1) {
+      __syncthreads();  // every wavefront's (dB, dC) sums of this chunk are in sh.dbc[buf]
+      for (int e = tid; e < CK * NP * 2; e += NT) {
+        const int q = e % 2, nn = (e / 2) % NP, t = e / (2 * NP);
+        if (t0 + t >= L) continue;
+        CT v = 0;
+#pragma unroll
+        for (int w = 0; w < WPB; ++w) v += sh.dbc[buf][w][t][nn][q];
+        const int64_t off = ((b * p.ntiles + tile) * p.L + t0 + t) * NP + nn;
+        ((CT *)(q == 0 ? p.ws_dB : p.ws_dC))[off] = v;
+      }
+    }
+    wave_lds_sync();
+  }
+
+  if (dval) ((CT *)p.ws_dA)[(b * p.D + d) * NP + n] = dA_acc;
+  if (p.has_dh0 && dval && nval)
+    vstore<CT>(p.dh0, b * p.dh0.s0 + d * p.dh0.s1 + n * p.dh0.s2, (CT)(dh64 * (double)a_next));
+  if (lane < CW && dw + lane < D) {
+    ((CT *)p.ws_dD)[b * p.D + dw + lane] = dD_acc;
+    ((CT *)p.ws_db)[b * p.D + dw + lane] = db_acc;
+  }
+}
+
+// Fixed-order final reductions: dB/dC over channel tiles, dA/dD/d_bias over the batch.
+template <typename OT, typename CT>
+__global__ void __launch_bounds__(256) k_bwd_finalize(const FinParams p) {
+  const int64_t nBLN = p.B * p.L * p.N;
+  const int64_t nDN = p.D * p.N;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < nBLN) {
+    const int64_t nn = i % p.N, t = (i / p.N) % p.L, b = i / (p.N * p.L);
+    const CT *wB = (const CT *)p.ws_dB, *wC = (const CT *)p.ws_dC;
+    CT sb = 0, sc = 0;
+    for (int tile = 0; tile < p.ntiles; ++tile) {
+      const int64_t off = ((b * p.ntiles + tile) * p.L + t) * p.np + nn;
+      sb += wB[off];
+      sc += wC[off];
+    }
+    Conv<OT>::store(vpw<OT>(p.dB) + b * p.dB.s0 + t * p.dB.s1 + nn * p.dB.s2, sb);
+    Conv<OT>::store(vpw<OT>(p.dC) + b * p.dC.s0 + t * p.dC.s1 + nn * p.dC.s2, sc);
+    return;
+  }
+  const int64_t j = i - nBLN;
+  if (j < nDN) {
+    const int64_t d = j / p.N, nn = j % p.N;
+    const CT *wA = (const CT *)p.ws_dA;
+    CT s = 0;
+    for (int64_t b = 0; b < p.B; ++b) s += wA[(b * p.D + d) * p.np + nn];
+    vstore<CT>(p.dA, d * p.dA.s0 + nn * p.dA.s1, s);
+    return;
+  }
+  const int64_t k = j - nDN;
+  if (k < p.D) {
+    if (p.has_D) {
+      CT s = 0;
+      for (int64_t b = 0; b < p.B; ++b) s += ((const CT *)p.ws_dD)[b * p.D + k];
+      vstore<CT>(p.dD, k * p.dD.s0, s);
+    }
+    if (p.has_bias) {
+      CT s = 0;
+      for (int64_t b = 0; b < p.B; ++b) s += ((const CT *)p.ws_db)[b * p.D + k];
+      vstore<CT>(p.dbias, k * p.dbias.s0, s);
+    }
+  }
+}
+
+template <typename IT, int NP, int M>
+static hipError_t launch_bwd_t(const BwdParams &p, hipStream_t s) {
+  typedef typename Conv<IT>::CT CT;
+  constexpr int WPB = bwd_waves(sizeof(CT), NP);
+  constexpr int DT = WPB * (kWave / NP);
+  if (p.ntiles != (int)((p.D + DT - 1) / DT)) return hipErrorInvalidValue;
+  dim3 grid((unsigned)p.ntiles, (unsigned)p.B);
+  if (p.uniform) hipLaunchKernelGGL((k_bwd<IT, NP, M, true>), grid, dim3(WPB * kWave), 0, s, p);
+  else hipLaunchKernelGGL((k_bwd<IT, NP, M, false>), grid, dim3(WPB * kWave), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename IT, int NP>
+static hipError_t launch_bwd_m(const BwdParams &p, int method, hipStream_t s) {
+  switch (method) {
+    case 0: return launch_bwd_t<IT, NP, 0>(p, s);
+    case 1: return launch_bwd_t<IT, NP, 1>(p, s);
+    default: return launch_bwd_t<IT, NP, 2>(p, s);
+  }
+}
+
+template <typename IT>
+static hipError_t launch_bwd_n(const BwdParams &p, int method, int np, hipStream_t s) {
+  switch (np) {
+    case 8: return launch_bwd_m<IT, 8>(p, method, s);
+    case 16: return launch_bwd_m<IT, 16>(p, method, s);
+    case 32: return launch_bwd_m<IT, 32>(p, method, s);
+    default: return launch_bwd_m<IT, 64>(p, method, s);
+  }
+}
+
+hipError_t launch_bwd(const BwdParams &p, int dtype, int method, int np, hipStream_t s) {
+  switch (dtype) {
+    case 0: return launch_bwd_n<float>(p, method, np, s);
+    case 1: return launch_bwd_n<bf16_t>(p, method, np, s);
+    case 2: return launch_bwd_n<f16_t>(p, method, np, s);
+    default: return launch_bwd_n<double>(p, method, np, s);
+  }
+}
+
+hipError_t launch_bwd_finalize(const FinParams &p, int dtype, hipStream_t s) {
+  const int64_t total = p.B * p.L * p.N + p.D * p.N + p.D;
+  dim3 grid((unsigned)((total + 255) / 256));
+  switch (dtype) {
+    case 0: hipLaunchKernelGGL((k_bwd_finalize<float, float>), grid, dim3(256), 0, s, p); break;
+    case 1: hipLaunchKernelGGL((k_bwd_finalize<bf16_t, float>), grid, dim3(256), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((k_bwd_finalize<f16_t, float>), grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL((k_bwd_finalize<double, double>), grid, dim3(256), 0, s, p); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace ssm

@@ -1,0 +1,200 @@
+// Fused selective-scan forward for gfx950.
+//
+// Replaces kernels/triton_scan.py:27-74 (_fwd_kernel) and :83-140 (_fwd_chunked_kernel) and
+// the forward of models/scan.py:202-217; the D skip and SiLU gate of models/mamba.py:124 (and
+// an optional delta bias + softplus, models/mamba.py:76) are fused.
+//
+// Mapping: one lane per (channel, state).  Each 64-lane wavefront owns CW = 64/NP channels
+// of one batch row and walks time in chunks of CK steps, entirely on its own (no workgroup
+// barrier: at B16 D512 N16 only 2 wavefronts share a SIMD, and barriers would idle it).
+// Per chunk a wavefront
+//   1. stores into its private LDS region the chunk's x, delta (bias/softplus applied) for
+//      its channels and B, C for all states -- loaded into registers one chunk ahead with
+//      coalesced reads along whichever of L / D has unit stride;
+//   2. runs the CK recurrence steps per lane in register batches of RB steps: a batch's
+//      inputs come from 16-byte LDS reads (the next batch is read before the current one is
+//      computed), its a_t and b_t are formed independently, then the RB dependent h-updates
+//      run back to back; each C_t h_t partial goes to LDS;
+//   3. sums the partials over the NP states with (t, channel)-mapped lanes, applies the skip
+//      and gate and stores the outputs (coalesced); saves the chunk-end state, and the
+//      pre-gate output when there is a gate, if the backward needs them.
+#include "ssm_device.hpp"
+#include "ssm_internal.hpp"
+#include "ssm_tiles.hpp"
+#include "ssm_wave.hpp"
+
+namespace ssm {
+
+template <typename CT, int NP>
+struct FwdWaveLds {
+  static constexpr int CW = kWave / NP, CK = kCK, CKP = ck_pad((int)sizeof(CT));
+  CT x[CW][CKP];
+  CT dt[CW][CKP];
+  CT B[NP][CKP];
+  CT C[NP][CKP];
+  CT y[CK][CW][NP];
+};
+
+template <typename IT, int NP, int METHOD, bool UL>
+__global__ void __launch_bounds__(kWave * fwd_waves(sizeof(typename Conv<IT>::CT), NP))
+k_fwd(const FwdParams p) {
+  typedef typename Conv<IT>::CT CT;
+  typedef FwdWaveLds<CT, NP> WL;
+  constexpr int CW = WL::CW, CK = WL::CK;
+  constexpr int WPB = fwd_waves(sizeof(CT), NP);
+  constexpr int RB = 32 / (int)sizeof(CT) > CK ? CK : 32 / (int)sizeof(CT);  // register batch
+  static_assert(sizeof(WL) == fwd_wave_bytes(sizeof(CT), NP), "LDS layout");
+  __shared__ __align__(16) WL lds_all[WPB];
+
+  const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  WL &S = lds_all[wv];
+  const int c = lane / NP, n = lane % NP;
+  const int64_t b = blockIdx.y;
+  const int dw = (blockIdx.x * WPB + wv) * CW;  // first channel of this wavefront
+  const int d = dw + c;
+  const bool dval = d < p.D, nval = n < p.N;
+  const int L = (int)p.L, D = (int)p.D, N = (int)p.N;
+
+  CT Av = (CT)-1;
+  if (dval && nval) Av = vload<CT>(p.A, d * p.A.s0 + n * p.A.s1);
+  const AConst<CT> ac = make_aconst(Av);
+  CT h = 0;
+  if (p.has_h0 && dval && nval) h = vload<CT>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
+
+  const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = with_layout<UL>(p.z, p.x);
+  const KView vout = with_layout<UL>(p.out, p.x), vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
+  const bool xt = vx.s1 == 1, dtt = vdt.s1 == 1, bt = vB.s1 == 1, ctt = vC.s1 == 1;
+  const bool ot = vout.s1 == 1;
+  WaveTile<IT, CT, CK, CW, UL> tx, tdt;
+  WaveTile<IT, CT, CK, NP, UL> tB, tC;
+  tx.load(vx, b, 0, L, dw, D, xt, lane);
+  tdt.load(vdt, b, 0, L, dw, D, dtt, lane);
+  tB.load(vB, b, 0, L, 0, N, bt, lane);
+  tC.load(vC, b, 0, L, 0, N, ctt, lane);
+
+  for (int k = 0; k < p.nchunks; ++k) {
+    const int t0 = k * CK;
+    tx.store(S.x, xt, lane);
+    store_delta_w<IT, CT, CK, CW, WL::CKP, UL>(tdt, S.dt, nullptr, dtt, lane, p.has_bias, p.softplus, p.bias, dw, D,
+                                            t0, L);
+    tB.store(S.B, bt, lane);
+    tC.store(S.C, ctt, lane);
+    wave_lds_sync();
+    if (k + 1 < p.nchunks) {  // next chunk's global reads overlap this chunk's compute
+      tx.load(vx, b, t0 + CK, L, dw, D, xt, lane);
+      tdt.load(vdt, b, t0 + CK, L, dw, D, dtt, lane);
+      tB.load(vB, b, t0 + CK, L, 0, N, bt, lane);
+      tC.load(vC, b, t0 + CK, L, 0, N, ctt, lane);
+    }
+
+    CT rdt[RB], rx[RB], rB[RB], rC[RB];
+    lds_row(&S.dt[c][0], rdt);
+    lds_row(&S.x[c][0], rx);
+    lds_row(&S.B[n][0], rB);
+    lds_row(&S.C[n][0], rC);
+#pragma unroll
+    for (int q = 0; q < CK / RB; ++q) {
+      CT ndt[RB], nx[RB], nB[RB], nC[RB];
+      if (q + 1 < CK / RB) {
+        lds_row(&S.dt[c][(q + 1) * RB], ndt);
+        lds_row(&S.x[c][(q + 1) * RB], nx);
+        lds_row(&S.B[n][(q + 1) * RB], nB);
+        lds_row(&S.C[n][(q + 1) * RB], nC);
+      }
+      CT a[RB], bx[RB];
+#pragma unroll
+      for (int tt = 0; tt < RB; ++tt) {
+        CT coef;
+        disc<METHOD>(rdt[tt], ac, a[tt], coef);
+        bx[tt] = bcoef<METHOD>(rdt[tt], coef) * (rB[tt] * rx[tt]);
+      }
+#pragma unroll
+      for (int tt = 0; tt < RB; ++tt) {
+        h = fma(a[tt], h, bx[tt]);
+        S.y[q * RB + tt][c][n] = rC[tt] * h;
+      }
+      if (q + 1 < CK / RB) {
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+          rdt[j] = ndt[j];
+          rx[j] = nx[j];
+          rB[j] = nB[j];
+          rC[j] = nC[j];
+        }
+      }
+    }
+    if (p.ckpt && dval)
+      ((CT *)p.ckpt)[((b * p.nchunks + k) * p.D + d) * NP + n] = h;
+    wave_lds_sync();
+
+    // outputs: sum over states, (y + D x) * silu(z), coalesced along the output's unit axis
+#pragma unroll
+    for (int i = 0; i < (CK * CW + kWave - 1) / kWave; ++i) {
+      const int e = lane + i * kWave;
+      if (e >= CK * CW) break;
+      int t, cc;
+      tc_of<CK, CW>(e, ot, t, cc);
+      const int tg = t0 + t, dd = dw + cc;
+      CT part[NP];
+      lds_row(&S.y[t][cc][0], part);
+      CT y = 0;
+#pragma unroll
+      for (int j = 0; j < NP; ++j) y += part[j];
+      if (tg >= L || dd >= D) continue;
+      const CT skip = p.has_D ? vload<CT>(p.Dsk, dd * p.Dsk.s0) * S.x[cc][t] : (CT)0;
+      if (p.ypre) ((CT *)p.ypre)[ypre_index(!xt, b, tg, dd, p.L, p.D)] = y + skip;
+      if (!p.write_out) continue;
+      CT o = y + skip;
+      if (p.has_z) {
+        const CT zv = Conv<IT>::load(vp<IT>(vz) + b * vz.s0 + row_off<UL>(tg, dd, vz.s1, vz.s2));
+        o *= zv * sigmoid_ct<CT>(zv);
+      }
+      Conv<IT>::store(vpw<IT>(vout) + b * vout.s0 + row_off<UL>(tg, dd, vout.s1, vout.s2), o);
+    }
+    wave_lds_sync();
+  }
+
+  if (p.has_last && dval && nval)
+    vstore<CT>(p.last, b * p.last.s0 + d * p.last.s1 + n * p.last.s2, h);
+}
+
+template <typename IT, int NP, int M>
+static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
+  typedef typename Conv<IT>::CT CT;
+  constexpr int WPB = fwd_waves(sizeof(CT), NP);
+  constexpr int DT = WPB * (kWave / NP);
+  dim3 grid((unsigned)((p.D + DT - 1) / DT), (unsigned)p.B);
+  if (p.uniform) hipLaunchKernelGGL((k_fwd<IT, NP, M, true>), grid, dim3(WPB * kWave), 0, s, p);
+  else hipLaunchKernelGGL((k_fwd<IT, NP, M, false>), grid, dim3(WPB * kWave), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename IT, int NP>
+static hipError_t launch_fwd_m(const FwdParams &p, int method, hipStream_t s) {
+  switch (method) {
+    case 0: return launch_fwd_t<IT, NP, 0>(p, s);
+    case 1: return launch_fwd_t<IT, NP, 1>(p, s);
+    default: return launch_fwd_t<IT, NP, 2>(p, s);
+  }
+}
+
+template <typename IT>
+static hipError_t launch_fwd_n(const FwdParams &p, int method, int np, hipStream_t s) {
+  switch (np) {
+    case 8: return launch_fwd_m<IT, 8>(p, method, s);
+    case 16: return launch_fwd_m<IT, 16>(p, method, s);
+    case 32: return launch_fwd_m<IT, 32>(p, method, s);
+    default: return launch_fwd_m<IT, 64>(p, method, s);
+  }
+}
+
+hipError_t launch_fwd(const FwdParams &p, int dtype, int method, int np, hipStream_t s) {
+  switch (dtype) {
+    case 0: return launch_fwd_n<float>(p, method, np, s);
+    case 1: return launch_fwd_n<bf16_t>(p, method, np, s);
+    case 2: return launch_fwd_n<f16_t>(p, method, np, s);
+    default: return launch_fwd_n<double>(p, method, np, s);
+  }
+}
+
+}  // namespace ssm

@@ -1,0 +1,98 @@
+// Parameter blocks and launcher declarations shared by the C ABI (ssm_abi.cpp) and the
+// kernel translation units.  Plain structs: they are passed to kernels by value.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ssm {
+
+struct KView {
+  const void *p;
+  int64_t s0, s1, s2;
+};
+
+// Geometry of the fused kernels.  A wavefront owns 64/NP channels x NP states; CK time steps
+// are staged per chunk, and the state at the end of every chunk is what the forward saves for
+// the backward.  Waves per workgroup are chosen so the per-wave LDS regions fit in 64 KiB.
+constexpr int kCK = 16;
+constexpr int kThreads = 256;  // threads per workgroup of the simple (non-scan) kernels
+inline int chunk_steps(int) { return kCK; }
+inline int padded_n(int64_t n) { return n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32 : 64; }
+__host__ __device__ constexpr int ck_pad(int s) { return kCK + 16 / s; }
+__host__ __device__ constexpr int fwd_wave_bytes(int s, int np) {
+  return ((2 * (64 / np) + 2 * np) * ck_pad(s) + kCK * 64) * s;
+}
+__host__ __device__ constexpr int bwd_half() { return 8; }  // reverse steps per LDS reduction round
+__host__ __device__ constexpr int bwd_wave_bytes(int s, int np) {
+  return ((6 * (64 / np) + 2 * np) * ck_pad(s) + 2 * bwd_half() * 64 * 2) * s;
+}
+__host__ __device__ constexpr int bwd_shared_bytes(int s, int np, int wpb) {
+  return wpb > 1 ? 2 * wpb * kCK * np * 2 * s : 0;
+}
+__host__ __device__ constexpr int fwd_waves(int s, int np) {
+  return 4 * fwd_wave_bytes(s, np) <= 65536 ? 4 : 2 * fwd_wave_bytes(s, np) <= 65536 ? 2 : 1;
+}
+__host__ __device__ constexpr int bwd_waves(int s, int np) {
+  return 4 * bwd_wave_bytes(s, np) + bwd_shared_bytes(s, np, 4) <= 65536 ? 4
+       : 2 * bwd_wave_bytes(s, np) + bwd_shared_bytes(s, np, 2) <= 65536 ? 2 : 1;
+}
+// Channels per backward workgroup (= the channel tile of the dB / dC partial sums).
+inline int bwd_channels_per_block(int dtype, int np) {
+  const int s = dtype == 3 ? 8 : 4;
+  return bwd_waves(s, np) * (64 / np);
+}
+
+struct FwdParams {
+  int64_t B, L, D, N;
+  int nchunks;
+  int softplus;
+  int has_D, has_z, has_bias, has_h0, has_last, write_out;
+  int uniform;  // all (B,L,D) views share x's strides, C shares B's, row offsets fit in int32
+  KView x, dt, A, Bm, Cm, Dsk, z, bias, h0, out, last;
+  void *ckpt;  // (B, nchunks, D, NP) state type: state at the end of each chunk
+  void *ypre;  // y + D x before the gate (iff gate and saving), state type; laid out
+               // (B, L, D) when x is D-contiguous, else (B, D, L) -- see ypre_index()
+};
+
+// Index of (b, t, d) in the saved pre-gate output: it follows x's unit-stride axis so that
+// the forward's writes and the backward's reads are coalesced.
+__host__ __device__ inline int64_t ypre_index(bool dfast, int64_t b, int64_t t, int64_t d, int64_t L, int64_t D) {
+  return dfast ? (b * L + t) * D + d : (b * D + d) * L + t;
+}
+
+struct BwdParams {
+  int64_t B, L, D, N;
+  int nchunks, ntiles;
+  int softplus;
+  int has_D, has_z, has_bias, has_h0, has_dlast, has_dh0;
+  int uniform;  // as in FwdParams
+  KView x, dt, A, Bm, Cm, Dsk, z, bias, h0, dout, dlast, dx, ddt, dz, dh0;
+  const void *ckpt;
+  const void *ypre;
+  void *ws_dB, *ws_dC;  // (B, ntiles, L, NP) partial sums over the tile's channels
+  void *ws_dA;          // (B, D, NP) partial over time
+  void *ws_dD, *ws_db;  // (B, D)
+};
+
+struct FinParams {
+  int64_t B, L, D, N;
+  int ntiles, np;
+  int has_D, has_bias;
+  const void *ws_dB, *ws_dC, *ws_dA, *ws_dD, *ws_db;
+  KView dB, dC, dA, dD, dbias;
+};
+
+struct StepParams {
+  int64_t B, D, N;
+  int softplus;
+  int has_D, has_z, has_bias;
+  KView x, dt, A, Bm, Cm, Dsk, z, bias, h, out;
+};
+
+hipError_t launch_fwd(const FwdParams &p, int dtype, int method, int np, hipStream_t s);
+hipError_t launch_bwd(const BwdParams &p, int dtype, int method, int np, hipStream_t s);
+hipError_t launch_bwd_finalize(const FinParams &p, int dtype, hipStream_t s);
+hipError_t launch_step(const StepParams &p, int dtype, int method, int np, hipStream_t s);
+
+}  // namespace ssm

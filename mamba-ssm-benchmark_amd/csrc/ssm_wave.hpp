@@ -1,0 +1,131 @@
+// Wavefront-level geometry and staging for the fused scan kernels.
+//
+// Every 64-lane wavefront works on its own CW = 64/NP channels: lane (c, n) = (lane / NP,
+// lane % NP) owns the state h[c, n].  A wavefront stages what its lanes need into a private
+// LDS region and reads it back without any workgroup barrier (a wavefront's LDS operations
+// complete in issue order, so only compiler reordering has to be fenced).  Two tile shapes
+// are staged per chunk of CK steps:
+//   (t, c) tiles -- CK x CW per-channel values (x, delta, z, dy, ...): element e of a tile is
+//                   handled by lane e % 64; the element -> (t, c) map walks the tensor's unit
+//                   stride axis across consecutive lanes, so global accesses are coalesced for
+//                   time-major (B,L,D) and channel-major (B,D,L) storage alike;
+//   (t, n) tiles -- CK x NP per-state values (B, C) shared by all channels.
+// Rows are stored time-contiguous ([c][t], [n][t]) and padded to 16-byte multiples so a lane
+// reads a run of steps with 16-byte LDS loads.
+#pragma once
+
+#include "ssm_device.hpp"
+#include "ssm_internal.hpp"
+#include "ssm_tiles.hpp"
+
+namespace ssm {
+
+constexpr int kWave = 64;
+
+// Compiler fence for wavefront-private LDS traffic (no hardware barrier is needed).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <typename CT> struct WaveCfg {
+  static constexpr int CK = 16;                          // steps per chunk (checkpoint interval)
+  static constexpr int CKP = CK + 16 / (int)sizeof(CT);  // padded row length
+};
+
+// Element e of a ROWS (time) x COLS tile -> (t, c); tfast = the time axis has unit stride.
+template <int ROWS, int COLS>
+__device__ __forceinline__ void tc_of(int e, bool tfast, int &t, int &c) {
+  if (tfast) {
+    t = e % ROWS;
+    c = e / ROWS;
+  } else {
+    t = e / COLS;
+    c = e % COLS;
+  }
+}
+
+// Element offset of (t, c) inside one batch row.  With a uniform layout (UL) every offset of
+// the row is known to fit in 32 bits (checked on the host), which keeps the address arithmetic
+// in 32-bit VALU ops.
+template <bool UL>
+__device__ __forceinline__ int64_t row_off(int t, int c, int64_t s1, int64_t s2) {
+  if (UL) return (int64_t)(t * (int)s1 + c * (int)s2);
+  return (int64_t)t * s1 + (int64_t)c * s2;
+}
+
+// With a uniform layout all (B, L, D) tensors share x's strides and C shares B's: kernels read
+// the strides from one view so the compiler computes each address once.
+template <bool UL>
+__device__ __forceinline__ KView with_layout(const KView &v, const KView &ref) {
+  return UL ? KView{v.p, ref.s0, ref.s1, ref.s2} : v;
+}
+
+// Register staging of a CK x COLS tile of a (B, L, C) view for one wavefront.
+template <typename IT, typename CT, int ROWS, int COLS, bool UL = false>
+struct WaveTile {
+  static constexpr int E = (ROWS * COLS + kWave - 1) / kWave;
+  CT v[E];
+
+  __device__ __forceinline__ void load(const KView &V, int64_t b, int t0, int L, int c0, int C, bool tfast,
+                                       int lane) {
+    const IT *base = (const IT *)V.p + b * V.s0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const int e = lane + i * kWave;
+      int t, c;
+      tc_of<ROWS, COLS>(e, tfast, t, c);
+      CT val = 0;
+      if (e < ROWS * COLS && t0 + t < L && c0 + c < C)
+        val = Conv<IT>::load(base + row_off<UL>(t0 + t, c0 + c, V.s1, V.s2));
+      v[i] = val;
+    }
+  }
+
+  template <int RP>
+  __device__ __forceinline__ void store(CT (*S)[RP], bool tfast, int lane) const {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const int e = lane + i * kWave;
+      if (e >= ROWS * COLS) break;
+      int t, c;
+      tc_of<ROWS, COLS>(e, tfast, t, c);
+      S[c][t] = v[i];
+    }
+  }
+};
+
+// delta' = softplus(delta + bias) (optional parts) for in-range elements, padding stays 0;
+// `sg` (optional) receives the softplus derivative sigmoid(delta + bias) (1 without softplus).
+template <typename IT, typename CT, int ROWS, int COLS, int RP, bool UL>
+__device__ __forceinline__ void store_delta_w(const WaveTile<IT, CT, ROWS, COLS, UL> &tl, CT (*S)[RP], CT (*sg)[RP],
+                                              bool tfast, int lane, int has_bias, int softplus,
+                                              const KView &bias, int c0, int C, int t0, int L) {
+#pragma unroll
+  for (int i = 0; i < WaveTile<IT, CT, ROWS, COLS, UL>::E; ++i) {
+    const int e = lane + i * kWave;
+    if (e >= ROWS * COLS) break;
+    int t, c;
+    tc_of<ROWS, COLS>(e, tfast, t, c);
+    CT v = tl.v[i], g = 1;
+    if (t0 + t < L && c0 + c < C) {
+      if (has_bias) v += vload<CT>(bias, (int64_t)(c0 + c) * bias.s0);
+      if (softplus) {
+        g = sigmoid_ct<CT>(v);
+        v = softplus_ct<CT>(v);
+      }
+    }
+    S[c][t] = v;
+    if (sg) sg[c][t] = g;
+  }
+}
+
+// Waves per workgroup so that WPB copies of a per-wave LDS struct fit in 64 KiB.
+template <int BYTES_PER_WAVE, int EXTRA = 0>
+struct WavesPerBlock {
+  static constexpr int fit = (64 * 1024 - EXTRA) / BYTES_PER_WAVE;
+  static constexpr int value = fit >= 4 ? 4 : fit >= 2 ? 2 : 1;
+};
+
+}  // namespace ssm

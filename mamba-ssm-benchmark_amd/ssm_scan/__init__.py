@@ -1,0 +1,23 @@
+"""MI355X (gfx950) selective-scan engine.
+
+Drop-in counterpart of the reference's scan path:
+  ssm_scan.scan      <-> models/scan.py        (selective_scan, discretize, SCANS, ...)
+  ssm_scan.hip_scan  <-> kernels/triton_scan.py (fused forward/backward)
+  ssm_scan.step      <-> the recurrent decode step of models/mamba.py:113-118
+All compute runs in libssmscan.so (hand-written HIP kernels behind a C ABI, see
+include/ssm_scan.h); the package only prepares views, allocates outputs with torch and
+launches on torch's current stream.  There is no CPU fallback.
+"""
+
+from . import _abi, plan
+from .hip_scan import (METHODS, FusedSelectiveScanFn, selective_scan_fn, selective_scan_hip,
+                       selective_scan_triton)
+from .profiling import KernelTimer
+from .step import ssm_step
+
+__all__ = ["METHODS", "FusedSelectiveScanFn", "selective_scan_fn", "selective_scan_hip",
+           "selective_scan_triton", "ssm_step", "KernelTimer", "plan"]
+
+
+def library_path():
+    return _abi.LIB_PATH

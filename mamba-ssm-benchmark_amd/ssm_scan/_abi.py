@@ -1,0 +1,167 @@
+"""ctypes mirror of include/ssm_scan.h and the loader of libssmscan.so.
+
+The library is loaded after ``import torch`` so that it binds to the HIP runtime torch
+already loaded (both use the soname libamdhip64.so.7); the kernels then run on torch's
+streams and device memory.  A missing library is an error: there is no fallback path.
+"""
+
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssmscan.so")
+ABI_VERSION = 1
+
+OK, EINVAL, EKEY, ESPACE, EHIP = 0, 1, 2, 3, 4
+ZOH, EULER, BILINEAR = 0, 1, 2
+F32, BF16, F16, F64 = 0, 1, 2, 3
+SCAN_IDS = {"reference": 0, "sequential": 1, "hillis_steele": 2, "blelloch": 3, "chunked": 4,
+            "triton": 5, "auto": 6}
+SCAN_NAMES = {v: k for k, v in SCAN_IDS.items()}
+DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.float64: F64}
+
+c_i64, c_i32, c_vp = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [("data", c_vp), ("stride", c_i64 * 3)]
+
+
+class FwdArgs(ctypes.Structure):
+    _fields_ = [("batch", c_i64), ("seqlen", c_i64), ("dim", c_i64), ("dstate", c_i64),
+                ("method", c_i32), ("dtype", c_i32),
+                ("x", Tensor), ("delta", Tensor), ("A", Tensor), ("Bm", Tensor), ("Cm", Tensor),
+                ("Dskip", Tensor), ("z", Tensor), ("delta_bias", Tensor),
+                ("delta_softplus", c_i32), ("reserved0", c_i32),
+                ("h0", Tensor), ("out", Tensor), ("last", Tensor),
+                ("saved", c_vp), ("workspace", c_vp), ("workspace_bytes", c_i64)]
+
+
+class BwdArgs(ctypes.Structure):
+    _fields_ = [("batch", c_i64), ("seqlen", c_i64), ("dim", c_i64), ("dstate", c_i64),
+                ("method", c_i32), ("dtype", c_i32),
+                ("x", Tensor), ("delta", Tensor), ("A", Tensor), ("Bm", Tensor), ("Cm", Tensor),
+                ("Dskip", Tensor), ("z", Tensor), ("delta_bias", Tensor),
+                ("delta_softplus", c_i32), ("reserved0", c_i32),
+                ("h0", Tensor), ("saved", c_vp), ("dout", Tensor), ("dlast", Tensor),
+                ("dx", Tensor), ("ddelta", Tensor), ("dA", Tensor), ("dBm", Tensor), ("dCm", Tensor),
+                ("dD", Tensor), ("dz", Tensor), ("ddelta_bias", Tensor), ("dh0", Tensor),
+                ("workspace", c_vp), ("workspace_bytes", c_i64)]
+
+
+class StepArgs(ctypes.Structure):
+    _fields_ = [("batch", c_i64), ("dim", c_i64), ("dstate", c_i64),
+                ("method", c_i32), ("dtype", c_i32),
+                ("x", Tensor), ("delta", Tensor), ("A", Tensor), ("Bm", Tensor), ("Cm", Tensor),
+                ("Dskip", Tensor), ("z", Tensor), ("delta_bias", Tensor),
+                ("delta_softplus", c_i32), ("reserved0", c_i32),
+                ("h", Tensor), ("out", Tensor)]
+
+
+class LscanArgs(ctypes.Structure):
+    _fields_ = [("batch", c_i64), ("seqlen", c_i64), ("width", c_i64),
+                ("algo", c_i32), ("dtype", c_i32), ("reverse", c_i32), ("reserved0", c_i32),
+                ("chunk", c_i64),
+                ("a", Tensor), ("b", Tensor), ("h0", Tensor), ("h", Tensor),
+                ("workspace", c_vp), ("workspace_bytes", c_i64)]
+
+
+class DiscArgs(ctypes.Structure):
+    _fields_ = [("batch", c_i64), ("seqlen", c_i64), ("dim", c_i64), ("dstate", c_i64),
+                ("method", c_i32), ("dtype", c_i32),
+                ("delta", Tensor), ("x", Tensor), ("A", Tensor), ("Bm", Tensor),
+                ("a", c_vp), ("b", c_vp), ("da", c_vp), ("db", c_vp),
+                ("ddelta", Tensor), ("dx", Tensor), ("dA", Tensor), ("dBm", Tensor),
+                ("workspace", c_vp), ("workspace_bytes", c_i64)]
+
+
+class ConvArgs(ctypes.Structure):
+    _fields_ = [("batch", c_i64), ("seqlen", c_i64), ("dim", c_i64), ("width", c_i64),
+                ("dtype", c_i32), ("silu", c_i32),
+                ("x", Tensor), ("weight", Tensor), ("bias", Tensor), ("state_in", Tensor),
+                ("out", Tensor), ("state_out", Tensor), ("dout", Tensor), ("dx", Tensor),
+                ("dweight", Tensor), ("dbias", Tensor),
+                ("workspace", c_vp), ("workspace_bytes", c_i64)]
+
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "ssm_abi_version": (c_i32, []),
+    "ssm_last_error": (ctypes.c_char_p, []),
+    "ssm_fwd_check": (c_i32, [ctypes.POINTER(FwdArgs)]),
+    "ssm_bwd_check": (c_i32, [ctypes.POINTER(BwdArgs)]),
+    "ssm_step_check": (c_i32, [ctypes.POINTER(StepArgs)]),
+    "ssm_lscan_check": (c_i32, [ctypes.POINTER(LscanArgs)]),
+    "ssm_disc_check": (c_i32, [ctypes.POINTER(DiscArgs)]),
+    "ssm_conv_check": (c_i32, [ctypes.POINTER(ConvArgs)]),
+    "ssm_fwd_saved_bytes": (c_i64, [ctypes.POINTER(FwdArgs)]),
+    "ssm_fwd_workspace_bytes": (c_i64, [ctypes.POINTER(FwdArgs)]),
+    "ssm_bwd_workspace_bytes": (c_i64, [ctypes.POINTER(BwdArgs)]),
+    "ssm_lscan_workspace_bytes": (c_i64, [ctypes.POINTER(LscanArgs)]),
+    "ssm_disc_workspace_bytes": (c_i64, [ctypes.POINTER(DiscArgs)]),
+    "ssm_conv_workspace_bytes": (c_i64, [ctypes.POINTER(ConvArgs)]),
+    "ssm_fwd": (c_i32, [ctypes.POINTER(FwdArgs), c_vp]),
+    "ssm_bwd": (c_i32, [ctypes.POINTER(BwdArgs), c_vp]),
+    "ssm_step": (c_i32, [ctypes.POINTER(StepArgs), c_vp]),
+    "ssm_lscan": (c_i32, [ctypes.POINTER(LscanArgs), c_vp]),
+    "ssm_disc_fwd": (c_i32, [ctypes.POINTER(DiscArgs), c_vp]),
+    "ssm_disc_bwd": (c_i32, [ctypes.POINTER(DiscArgs), c_vp]),
+    "ssm_conv_fwd": (c_i32, [ctypes.POINTER(ConvArgs), c_vp]),
+    "ssm_conv_bwd": (c_i32, [ctypes.POINTER(ConvArgs), c_vp]),
+    "ssm_default_chunk": (c_i64, [c_i64]),
+    "ssm_scan_blocks": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.POINTER(c_i64), c_i64]),
+    "ssm_block_d": (c_i64, [c_i64, c_i64]),
+    "ssm_bwd_tile": (c_i64, [c_i64, c_i64, c_i64, c_i64]),
+    "ssm_resolve_scan": (c_i32, [c_i32, c_i32, c_i32, c_i64, c_i32]),
+}
+EXPORTED = tuple(_SIGS)
+
+_lib = None
+
+
+def lib():
+    """The loaded engine library; raises if it is not built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                               "(make -C mamba-ssm-benchmark_amd/csrc)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = handle.ssm_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"libssmscan ABI version {ver} != expected {ABI_VERSION}")
+        _lib = handle
+    return _lib
+
+
+_ERRORS = {EINVAL: ValueError, EKEY: KeyError, ESPACE: ValueError, EHIP: RuntimeError}
+
+
+def check(rc, what):
+    if rc != OK:
+        msg = (lib().ssm_last_error() or b"").decode(errors="replace")
+        raise _ERRORS.get(rc, RuntimeError)(f"{what}: {msg}")
+
+
+def view(t):
+    """ssm_tensor for a torch tensor (None -> absent); strides in elements, padded to 3."""
+    v = Tensor()
+    if t is None:
+        v.data = None
+        return v
+    if t.dim() > 3:
+        raise ValueError(f"expected a tensor of at most 3 dims, got shape {tuple(t.shape)}")
+    v.data = t.data_ptr()
+    st = list(t.stride()) + [0, 0, 0]
+    for i in range(3):
+        v.stride[i] = st[i]
+    return v
+
+
+def stream_handle(device):
+    return torch.cuda.current_stream(device).cuda_stream

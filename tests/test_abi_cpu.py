@@ -1,0 +1,177 @@
+"""CPU-tier checks of the C ABI and the host logic (no device calls).
+
+* libssmscan.so loads and exports every function include/ssm_scan.h declares;
+* the ctypes structs have the C layout (compiled with gcc against the header);
+* the integer plans equal the oracle's restatement of the reference over exhaustive ranges
+  and the committed golden table (bit-exact);
+* argument validation returns the reference's error classes.
+"""
+
+import ctypes
+import json
+import os
+import random
+import re
+import subprocess
+
+import pytest
+import torch
+
+from oracle import scan_ref as R
+from ssm_scan import _abi, hip_scan, plan
+import ssm_scan
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ssm_scan.h")
+GOLDEN = os.path.join(ROOT, "tests", "golden", "plans.json")
+
+
+def header_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z0-9_]+\s*\*?\s*(ssm_[a-z0-9_]+)\s*\(", src, flags=re.M)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _abi.lib()
+    names = header_functions()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_abi.EXPORTED)
+    assert lib.ssm_abi_version() == _abi.ABI_VERSION
+
+
+def test_ctypes_layout_matches_c_header(tmp_path):
+    structs = {"ssm_tensor": _abi.Tensor, "ssm_fwd_args": _abi.FwdArgs, "ssm_bwd_args": _abi.BwdArgs,
+               "ssm_step_args": _abi.StepArgs, "ssm_lscan_args": _abi.LscanArgs,
+               "ssm_disc_args": _abi.DiscArgs, "ssm_conv_args": _abi.ConvArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    (tmp_path / "l.c").write_text("\n".join(lines))
+    subprocess.run(["gcc", str(tmp_path / "l.c"), "-o", str(tmp_path / "l")], check=True)
+    out = subprocess.run([str(tmp_path / "l")], check=True, capture_output=True, text=True).stdout
+    for line in out.splitlines():
+        cname, field, val = line.split()
+        py = structs[cname]
+        got = ctypes.sizeof(py) if field == "size" else getattr(py, field).offset
+        assert got == int(val), line
+
+
+def test_default_chunk_exact():
+    for L in list(range(0, 70000)) + [2 ** k + d for k in range(17, 45) for d in (-1, 0, 1)]:
+        assert plan.default_chunk(L) == R.default_chunk(L), L
+
+
+def test_blocks_block_d_bwd_tile_exact():
+    rng = random.Random(0)
+    for _ in range(3000):
+        B, L, D, N = rng.randint(1, 64), rng.randint(1, 1 << 17), rng.randint(1, 2048), rng.choice([1, 3, 8, 16, 64])
+        db = rng.choice([None, 0, 1, 2, 7, 24, 128, 4096])
+        assert plan.blocks((B, L, D), N, db) == R.blocks((B, L, D), N, db)
+        assert plan.block_d(B, D) == R.block_d(B, D)
+        bd = R.block_d(B, D)
+        assert plan.bwd_tile(B, L, N, bd) == R.bwd_tile(B, L, N, bd)
+
+
+def test_resolve_scan_exact():
+    for scan in R.SCAN_NAMES:
+        for on_gpu in (False, True):
+            for method in ("zoh", "euler", "bilinear", "rk4"):
+                for N in range(0, 70):
+                    for eng in (False, True):
+                        assert plan.resolve_scan(scan, on_gpu, method, N, eng) == \
+                            R.resolve_scan(scan, on_gpu, method, N, eng)
+    with pytest.raises(KeyError):
+        plan.resolve_scan("parallel", True, "zoh", 16)
+
+
+def test_plans_match_committed_golden_table():
+    table = json.load(open(GOLDEN))
+    for row in table["default_chunk"]:
+        assert plan.default_chunk(row[0]) == row[1]
+    for row in table["blocks"]:
+        assert [list(b) for b in plan.blocks(row[0], row[1], row[2])] == row[3]
+    for row in table["block_d"]:
+        assert plan.block_d(*row[0]) == row[1]
+    for row in table["bwd_tile"]:
+        assert plan.bwd_tile(*row[0]) == row[1]
+    for row in table["resolve_scan"]:
+        assert plan.resolve_scan(*row[0]) == row[1]
+
+
+def _fwd_args(B=2, L=8, D=4, N=16, method=0, dtype=0, drop=()):
+    x = torch.zeros(B, L, D)
+    A = torch.zeros(D, N)
+    Bm = torch.zeros(B, L, N)
+    a = _abi.FwdArgs()
+    a.batch, a.seqlen, a.dim, a.dstate, a.method, a.dtype = B, L, D, N, method, dtype
+    for name, t in (("x", x), ("delta", x), ("A", A), ("Bm", Bm), ("Cm", Bm), ("out", x)):
+        if name not in drop:
+            setattr(a, name, _abi.view(t))
+    a._keep = (x, A, Bm)
+    return a
+
+
+@pytest.mark.parametrize("kw,exc", [
+    (dict(method=3), ValueError), (dict(dtype=7), ValueError), (dict(L=0), ValueError),
+    (dict(B=0), ValueError), (dict(N=65), ValueError), (dict(drop=("Cm",)), ValueError),
+    (dict(drop=("out",)), ValueError)])
+def test_forward_validation_errors(kw, exc):
+    a = _fwd_args(**kw)
+    rc = _abi.lib().ssm_fwd_check(ctypes.byref(a))
+    with pytest.raises(exc):
+        _abi.check(rc, "ssm_fwd")
+
+
+def test_forward_validation_accepts_and_sizes():
+    a = _fwd_args(B=16, L=512, D=512, N=16)
+    lib = _abi.lib()
+    assert lib.ssm_fwd_check(ctypes.byref(a)) == 0
+    # chunk-boundary states: B * ceil(L/16) * D * 16 float32
+    assert lib.ssm_fwd_saved_bytes(ctypes.byref(a)) == 16 * 32 * 512 * 16 * 4
+
+
+def test_backward_requires_gradient_buffers():
+    b = _abi.BwdArgs()
+    x = torch.zeros(2, 8, 4)
+    A = torch.zeros(4, 16)
+    Bm = torch.zeros(2, 8, 16)
+    b.batch, b.seqlen, b.dim, b.dstate = 2, 8, 4, 16
+    for name, t in (("x", x), ("delta", x), ("A", A), ("Bm", Bm), ("Cm", Bm), ("dout", x), ("dx", x),
+                    ("ddelta", x), ("dA", A), ("dBm", Bm), ("dCm", Bm)):
+        setattr(b, name, _abi.view(t))
+    lib = _abi.lib()
+    assert lib.ssm_bwd_check(ctypes.byref(b)) == 0
+    b.Dskip = _abi.view(torch.zeros(4))
+    with pytest.raises(ValueError, match="dD"):
+        _abi.check(lib.ssm_bwd_check(ctypes.byref(b)), "ssm_bwd")
+    b.dD = _abi.view(torch.zeros(4))
+    assert lib.ssm_bwd_check(ctypes.byref(b)) == 0
+    assert lib.ssm_bwd_workspace_bytes(ctypes.byref(b)) > 0
+
+
+def test_python_api_rejects_cpu_tensors_and_bad_arguments():
+    x = torch.zeros(1, 4, 8)
+    A = -torch.ones(8, 16)
+    Bm = torch.zeros(1, 4, 16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ssm_scan.selective_scan_hip(x, x, A, Bm, Bm)
+    with pytest.raises(ValueError):
+        ssm_scan.selective_scan_hip(x, x, A, Bm, Bm, method="rk4")
+    with pytest.raises(ValueError, match="power of two"):
+        ssm_scan.selective_scan_hip(x, x, -torch.ones(8, 3), Bm[..., :3], Bm[..., :3])
+
+
+def test_dense_layout_helper():
+    t = torch.zeros(2, 5, 7)
+    assert hip_scan.is_dense(t) and hip_scan.is_dense(t.transpose(1, 2))
+    assert not hip_scan.is_dense(torch.zeros(2, 5, 14)[..., :7])
+    assert not hip_scan.is_dense(torch.zeros(7, 1).expand(7, 4))
+    out = hip_scan.empty_like_layout(torch.zeros(2, 7, 5).transpose(1, 2), torch.bfloat16)
+    assert out.stride() == (35, 1, 5) and out.dtype == torch.bfloat16
+    assert hip_scan.empty_like_layout(torch.zeros(2, 5, 14)[..., :7], torch.float32).is_contiguous()

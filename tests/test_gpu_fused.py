@@ -1,0 +1,209 @@
+"""Parity of the fused HIP engine (libssmscan.so, ssm_fwd / ssm_bwd) with the float64 oracle.
+
+Tolerances: float32 inputs rtol 1e-4 / atol 1e-5 on outputs and
+every gradient; bf16 inputs with a float32 state rtol 2e-2.  Shapes: the reference's own GPU
+test shapes (tests/test_triton.py:31), the BASELINE configs 0 and 1, and edge cases (L = 1,
+ragged L and D, dstate not a power of two, non-contiguous views, expanded A).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import ssm_scan
+from oracle import c_oracle
+from oracle import scan_ref as R
+from ssm_inputs import baseline_inputs, np64, triton_test_inputs
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-4, 1e-5            # float32 parity bar
+RTOL_BF16, ATOL_BF16 = 2e-2, 2e-2  # bf16 inputs, float32 state
+
+
+def close(got, ref, rtol=RTOL, atol=ATOL, name=""):
+    got = np64(got) if isinstance(got, torch.Tensor) else got
+    np.testing.assert_allclose(got, ref, rtol=rtol, atol=atol, err_msg=name)
+
+
+def run_fused(ins, dev, method, D=None, z=None, bias=None, softplus=False, dout=None, dlast=None):
+    """GPU forward + backward through autograd; returns (out, last, grads dict)."""
+    x, delta, A, Bm, Cm, h0 = ins
+    names = ["dx", "ddelta", "dA", "dB", "dC", "dD", "dz", "ddelta_bias", "dh0"]
+    leaves = [x, delta, A, Bm, Cm, D, z, bias, h0]
+    gl = [None if t is None else t.to(dev).requires_grad_() for t in leaves]
+    out, last = ssm_scan.selective_scan_fn(gl[0], gl[1], gl[2], gl[3], gl[4], D=gl[5], z=gl[6],
+                                           delta_bias=gl[7], delta_softplus=softplus, h0=gl[8],
+                                           method=method, return_last_state=True)
+    loss = (out * dout.to(dev)).sum()
+    if dlast is not None:
+        loss = loss + (last * dlast.to(dev)).sum()
+    loss.backward()
+    grads = {n: t.grad for n, t in zip(names, gl) if t is not None}
+    return out.detach(), last.detach(), grads
+
+
+def oracle(ins, method, D=None, z=None, bias=None, softplus=False, dout=None, dlast=None, use_c=False):
+    x, delta, A, Bm, Cm, h0 = (np64(t) for t in ins)
+    raw = delta
+    if bias is not None:
+        raw = raw + np64(bias)
+    d_eff = np.log1p(np.exp(raw)) if softplus else raw
+    fwd = c_oracle.fwd if use_c else R.selective_scan_fwd
+    out, _, last = fwd(x, d_eff, A, Bm, Cm, h0, method, np64(D), np64(z))
+    bwd = c_oracle.bwd if use_c else R.selective_scan_bwd
+    g = bwd(x, d_eff, A, Bm, Cm, np64(dout), h0, method, np64(D), np64(z), np64(dlast))
+    if softplus or bias is not None:
+        dd_raw = g["ddelta"] * (1.0 / (1.0 + np.exp(-raw)) if softplus else 1.0)
+        g["ddelta"] = dd_raw
+        if bias is not None:
+            g["ddelta_bias"] = dd_raw.sum(axis=(0, 1))
+    return out, last, g
+
+
+GRAD_MAP = {"dx": "dx", "ddelta": "ddelta", "dA": "dA", "dB": "dB", "dC": "dC", "dD": "dD",
+            "dz": "dz", "ddelta_bias": "ddelta_bias", "dh0": "dh0"}
+
+
+def check_all(got, ref, rtol=RTOL, atol=ATOL):
+    out, last, grads = got
+    rout, rlast, rg = ref
+    close(out, rout, rtol, atol, "out")
+    close(last, rlast, rtol, atol, "last")
+    for k, v in grads.items():
+        close(v, rg[GRAD_MAP[k]], rtol, atol, k)
+
+
+@pytest.mark.parametrize("method", ["zoh", "euler", "bilinear"])
+@pytest.mark.parametrize("shape", [(2, 1, 32, 16), (2, 37, 50, 16), (3, 130, 96, 8)])
+@pytest.mark.parametrize("h0", [False, True])
+def test_reference_shapes_match_oracle(dev, method, shape, h0):
+    """tests/test_triton.py:28-44 shapes and input distributions; y, last and all 6 grads."""
+    ins = triton_test_inputs(*shape, h0)
+    g = torch.Generator().manual_seed(1)
+    dout = torch.randn(shape[0], shape[1], shape[2], generator=g)
+    dlast = torch.randn(shape[0], shape[2], shape[3], generator=g)
+    got = run_fused(ins, dev, method, dout=dout, dlast=dlast)
+    ref = oracle(ins, method, dout=dout, dlast=dlast)
+    check_all(got, ref)
+
+
+@pytest.mark.parametrize("method", ["zoh", "euler", "bilinear"])
+def test_gate_skip_bias_softplus_match_oracle(dev, method):
+    B, L, D, N = 2, 75, 40, 16
+    ins = triton_test_inputs(B, L, D, N, True, seed=3)
+    g = torch.Generator().manual_seed(4)
+    Dv = torch.randn(D, generator=g)
+    z = torch.randn(B, L, D, generator=g)
+    bias = torch.randn(D, generator=g) * 0.5 - 3.0
+    raw_delta = torch.randn(B, L, D, generator=g) * 0.5
+    ins = (ins[0], raw_delta, *ins[2:])
+    dout = torch.randn(B, L, D, generator=g)
+    got = run_fused(ins, dev, method, D=Dv, z=z, bias=bias, softplus=True, dout=dout)
+    ref = oracle(ins, method, D=Dv, z=z, bias=bias, softplus=True, dout=dout)
+    check_all(got, ref)
+
+
+@pytest.mark.parametrize("N", [1, 3, 8, 12, 32, 64])
+def test_dstate_padding(dev, N):
+    """dstate that is not a padded width (1, 3, 12) or the larger tiles (32, 64)."""
+    ins = triton_test_inputs(2, 45, 20, N, True, seed=N)
+    g = torch.Generator().manual_seed(N + 1)
+    dout = torch.randn(2, 45, 20, generator=g)
+    got = run_fused(ins, dev, "zoh", dout=dout)
+    ref = oracle(ins, "zoh", dout=dout)
+    check_all(got, ref)
+
+
+def test_config0_forward_matches_c_oracle(dev):
+    """B1 L512 D512 N16 fp32, no gate."""
+    t = baseline_inputs(1, 512, 512, 16)
+    with torch.no_grad():
+        y, last = ssm_scan.selective_scan_hip(t["u"].to(dev), t["delta"].to(dev), t["A"].to(dev),
+                                              t["Bm"].to(dev), t["Cm"].to(dev))
+    ry, _, rlast = c_oracle.fwd(np64(t["u"]), np64(t["delta"]), np64(t["A"]), np64(t["Bm"]), np64(t["Cm"]))
+    close(y, ry, name="y")
+    close(last, rlast, name="last")
+
+
+def test_config1_fwd_bwd_matches_c_oracle(dev):
+    """B16 L512 D512 N16 fp32 with z gate and D skip; all gradients."""
+    t = baseline_inputs(16, 512, 512, 16, gate=True, with_dy=True)
+    ins = (t["u"], t["delta"], t["A"], t["Bm"], t["Cm"], None)
+    got = run_fused(ins, dev, "zoh", D=t["D"], z=t["z"], dout=t["dy"])
+    ref = oracle(ins, "zoh", D=t["D"], z=t["z"], dout=t["dy"], use_c=True)
+    check_all(got, ref)
+
+
+def test_backward_is_bitwise_deterministic(dev):
+    """tests/test_gpu.py:28-46: two backward passes are torch.equal (always, not only in
+    torch's deterministic mode: every reduction here is fixed-order)."""
+    x, delta, A, Bm, Cm, _ = triton_test_inputs(3, 300, 96, 16, False)
+    ins = [t.to(dev).requires_grad_() for t in (x, delta, A, Bm, Cm)]
+
+    def grads():
+        y, _ = ssm_scan.selective_scan_hip(*ins)
+        return torch.autograd.grad(y.square().sum(), ins)
+
+    g1, g2 = grads(), grads()
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_layouts_and_strided_views_agree(dev):
+    """Time-major, channel-major and strided split views (models/mamba.py:75,101,107) give
+    bitwise identical results; A may be an expanded (stride-0) scalar-decay view."""
+    B, L, D, N = 2, 70, 48, 16
+    x, delta, A, Bm, Cm, h0 = (t.to(dev) for t in triton_test_inputs(B, L, D, N, True, seed=5))
+    A_scalar = A[:, :1].expand(D, N)
+    ref_y, ref_last = ssm_scan.selective_scan_hip(x, delta, A_scalar.contiguous(), Bm, Cm, h0)
+    xc = x.transpose(1, 2).contiguous().transpose(1, 2)          # channel-major storage
+    proj = torch.cat([torch.randn(B, L, 5, device=dev), Bm, Cm], -1)  # x_proj-style split
+    Bv, Cv = proj[..., 5:5 + N], proj[..., 5 + N:]
+    y2, last2 = ssm_scan.selective_scan_hip(xc, delta.transpose(1, 2).contiguous().transpose(1, 2),
+                                            A_scalar, Bv, Cv, h0)
+    assert torch.equal(ref_y, y2) and torch.equal(ref_last, last2)
+
+
+def test_bf16_inputs(dev):
+    """bf16 u, delta, B, C (state float32): rtol 2e-2 against the oracle on the rounded inputs."""
+    t = baseline_inputs(2, 256, 128, 16, dtype=torch.bfloat16)
+    ins = [t[k].to(dev) for k in ("u", "delta", "A", "Bm", "Cm")]
+    with torch.no_grad():
+        y, last = ssm_scan.selective_scan_hip(*ins)
+    assert y.dtype == torch.bfloat16 and last.dtype == torch.float32
+    ry, _, rlast = c_oracle.fwd(*(np64(v) for v in ins))
+    close(y, ry, RTOL_BF16, ATOL_BF16, "y")
+    close(last, rlast, RTOL_BF16, ATOL_BF16, "last")
+
+
+def test_float64_inputs(dev):
+    """float64 inputs compute in float64 (promote(dtype, float32)); tight agreement."""
+    ins = [t.double() if t is not None else None for t in triton_test_inputs(2, 50, 24, 16, True, seed=8)]
+    g = torch.Generator().manual_seed(9)
+    dout = torch.randn(2, 50, 24, generator=g, dtype=torch.float64)
+    got = run_fused(ins, dev, "zoh", dout=dout)
+    ref = oracle(ins, "zoh", dout=dout)
+    check_all(got, ref, rtol=1e-9, atol=1e-10)
+
+
+def test_decode_step_matches_forward(dev):
+    """The recurrent step applied L times equals the fused forward (tests/test_gpu.py:49-65)."""
+    B, L, D, N = 4, 24, 64, 16
+    x, delta, A, Bm, Cm, h0 = (t.to(dev) for t in triton_test_inputs(B, L, D, N, True, seed=11))
+    g = torch.Generator().manual_seed(12)
+    Dv = torch.randn(D, generator=g).to(dev)
+    z = torch.randn(B, L, D, generator=g).to(dev)
+    with torch.no_grad():
+        out, last = ssm_scan.selective_scan_fn(x, delta, A, Bm, Cm, D=Dv, z=z, h0=h0, return_last_state=True)
+        h = h0.clone()
+        steps = [ssm_scan.ssm_step(h, x[:, t], delta[:, t], A, Bm[:, t], Cm[:, t], D=Dv, z=z[:, t])
+                 for t in range(L)]
+    torch.testing.assert_close(torch.stack(steps, 1), out, rtol=RTOL, atol=ATOL)
+    torch.testing.assert_close(h, last, rtol=RTOL, atol=ATOL)
+
+
+def test_cpu_tensors_are_rejected():
+    x, delta, A, Bm, Cm, _ = triton_test_inputs(1, 4, 8, 16, False)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ssm_scan.selective_scan_hip(x, delta, A, Bm, Cm)
