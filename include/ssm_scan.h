@@ -148,6 +148,25 @@ typedef struct ssm_lscan_args {
   int64_t workspace_bytes;
 } ssm_lscan_args;
 
+/* Adjoint of ssm_lscan: given dh = dL/dh (B,L,M), returns da, db (B,L,M) and dh0 (B,M).
+ * It is the reverse scan lambda_t = dh_t + a_{t+1} lambda_{t+1} run with the same algorithm
+ * (models/scan.py:239-240 scans a_next with the forward's scan_fn), then da_t = lambda_t h_{t-1},
+ * db_t = lambda_t, dh0 = a_0 lambda_0 (models/scan.py:242-248).  `reverse` is the direction of
+ * the forward scan being differentiated. */
+typedef struct ssm_lscan_bwd_args {
+  int64_t batch, seqlen, width;
+  int32_t algo, dtype, reverse, reserved0;
+  int64_t chunk;
+  ssm_tensor a;            /* forward input (B,L,M) */
+  ssm_tensor h0;           /* forward input (B,M), optional */
+  ssm_tensor h;            /* forward output (B,L,M) */
+  ssm_tensor dh;           /* upstream gradient (B,L,M) */
+  ssm_tensor da, db;       /* outputs (B,L,M) */
+  ssm_tensor dh0;          /* output (B,M), optional */
+  void *workspace;         /* ssm_lscan_bwd_workspace_bytes() */
+  int64_t workspace_bytes;
+} ssm_lscan_bwd_args;
+
 /* ------------------------------------------------------------------ discretization
  * models/scan.py:39-55, materialized: a, b (B,L,D,N), contiguous.  The backward maps
  * (da, db) to (ddelta, dA, dBm, dx) exactly as autograd does through discretize
@@ -197,6 +216,7 @@ int ssm_fwd_check(const ssm_fwd_args *args);
 int ssm_bwd_check(const ssm_bwd_args *args);
 int ssm_step_check(const ssm_step_args *args);
 int ssm_lscan_check(const ssm_lscan_args *args);
+int ssm_lscan_bwd_check(const ssm_lscan_bwd_args *args);
 int ssm_disc_check(const ssm_disc_args *args);
 int ssm_conv_check(const ssm_conv_args *args);
 
@@ -205,6 +225,7 @@ int64_t ssm_fwd_saved_bytes(const ssm_fwd_args *args);
 int64_t ssm_fwd_workspace_bytes(const ssm_fwd_args *args);
 int64_t ssm_bwd_workspace_bytes(const ssm_bwd_args *args);
 int64_t ssm_lscan_workspace_bytes(const ssm_lscan_args *args);
+int64_t ssm_lscan_bwd_workspace_bytes(const ssm_lscan_bwd_args *args);
 int64_t ssm_disc_workspace_bytes(const ssm_disc_args *args);
 int64_t ssm_conv_workspace_bytes(const ssm_conv_args *args);
 
@@ -213,6 +234,7 @@ int ssm_fwd(const ssm_fwd_args *args, void *stream);
 int ssm_bwd(const ssm_bwd_args *args, void *stream);
 int ssm_step(const ssm_step_args *args, void *stream);
 int ssm_lscan(const ssm_lscan_args *args, void *stream);
+int ssm_lscan_bwd(const ssm_lscan_bwd_args *args, void *stream);
 int ssm_disc_fwd(const ssm_disc_args *args, void *stream);
 int ssm_disc_bwd(const ssm_disc_args *args, void *stream);
 int ssm_conv_fwd(const ssm_conv_args *args, void *stream);

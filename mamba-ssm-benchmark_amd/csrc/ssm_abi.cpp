@@ -348,14 +348,204 @@ int32_t ssm_resolve_scan(int32_t scan_id, int32_t on_gpu, int32_t method, int64_
   return scan_id;
 }
 
+// ------------------------------------------------------------------ linear scans
+static int lscan_common(int64_t B, int64_t L, int64_t M, int algo, int dtype, int64_t chunk) {
+  if (algo < SSM_SCAN_SEQUENTIAL || algo > SSM_SCAN_CHUNKED)
+    return fail(SSM_EINVAL, "unknown scan algorithm %d (sequential=1 .. chunked=4)", algo);
+  if (dtype != SSM_F32 && dtype != SSM_F64) return fail(SSM_EINVAL, "linear scans take float32 or float64");
+  if (B < 1 || L < 1 || M < 1)
+    return fail(SSM_EINVAL, "empty scan: batch=%lld seqlen=%lld width=%lld", (long long)B, (long long)L,
+                (long long)M);
+  if (B > 65535) return fail(SSM_EINVAL, "batch=%lld > 65535 is not supported", (long long)B);
+  if (L >= (1LL << 30) || M >= (1LL << 31) || B * L * M >= (1LL << 39))
+    return fail(SSM_EINVAL, "scan too large");
+  if (chunk < 0 || chunk >= (1LL << 30)) return fail(SSM_EINVAL, "chunk=%lld out of range", (long long)chunk);
+  return SSM_OK;
+}
+
+static int64_t lscan_chunk(int64_t L, int64_t chunk) { return chunk ? chunk : ssm_default_chunk(L); }
+
+static int64_t lscan_ws(int64_t B, int64_t L, int64_t M, int algo, int dtype, int64_t chunk) {
+  if (algo != SSM_SCAN_CHUNKED) return 0;
+  return align256(3 * B * cdiv(L, lscan_chunk(L, chunk)) * M * state_size(dtype));
+}
+
+static LscanParams lscan_params(int64_t B, int64_t L, int64_t M, int64_t chunk, int reverse, int shift) {
+  LscanParams p;
+  memset(&p, 0, sizeof(p));
+  p.B = B;
+  p.L = L;
+  p.M = M;
+  p.chunk = (int)lscan_chunk(L, chunk);
+  p.nc = cdiv(L, p.chunk);
+  p.reverse = reverse != 0;
+  p.shift = shift;
+  return p;
+}
+
+int ssm_lscan_check(const ssm_lscan_args *a) {
+  if (!a) return fail(SSM_EINVAL, "null args");
+  int rc = lscan_common(a->batch, a->seqlen, a->width, a->algo, a->dtype, a->chunk);
+  if (rc) return rc;
+  REQUIRE(a->a, "a");
+  REQUIRE(a->b, "b");
+  REQUIRE(a->h, "h");
+  return ok();
+}
+
+int64_t ssm_lscan_workspace_bytes(const ssm_lscan_args *a) {
+  if (ssm_lscan_check(a)) return -1;
+  return lscan_ws(a->batch, a->seqlen, a->width, a->algo, a->dtype, a->chunk);
+}
+
+int ssm_lscan(const ssm_lscan_args *a, void *stream) {
+  int rc = ssm_lscan_check(a);
+  if (rc) return rc;
+  const int64_t need = lscan_ws(a->batch, a->seqlen, a->width, a->algo, a->dtype, a->chunk);
+  if (need && (!a->workspace || a->workspace_bytes < need))
+    return fail(SSM_ESPACE, "workspace of %lld bytes required", (long long)need);
+  LscanParams p = lscan_params(a->batch, a->seqlen, a->width, a->chunk, a->reverse, 0);
+  p.a = kv(a->a);
+  p.b = kv(a->b);
+  p.h0 = kv(a->h0);
+  p.h = kv(a->h);
+  p.ws = a->workspace;
+  hipError_t e = launch_lscan(p, a->algo, a->dtype, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "ssm_lscan");
+}
+
+int ssm_lscan_bwd_check(const ssm_lscan_bwd_args *a) {
+  if (!a) return fail(SSM_EINVAL, "null args");
+  int rc = lscan_common(a->batch, a->seqlen, a->width, a->algo, a->dtype, a->chunk);
+  if (rc) return rc;
+  REQUIRE(a->a, "a");
+  REQUIRE(a->h, "h");
+  REQUIRE(a->dh, "dh");
+  REQUIRE(a->da, "da");
+  REQUIRE(a->db, "db");
+  if (has(a->dh0) && !has(a->h0)) return fail(SSM_EINVAL, "dh0 requested without h0");
+  return ok();
+}
+
+int64_t ssm_lscan_bwd_workspace_bytes(const ssm_lscan_bwd_args *a) {
+  if (ssm_lscan_bwd_check(a)) return -1;
+  return lscan_ws(a->batch, a->seqlen, a->width, a->algo, a->dtype, a->chunk);
+}
+
+int ssm_lscan_bwd(const ssm_lscan_bwd_args *a, void *stream) {
+  int rc = ssm_lscan_bwd_check(a);
+  if (rc) return rc;
+  const int64_t need = lscan_ws(a->batch, a->seqlen, a->width, a->algo, a->dtype, a->chunk);
+  if (need && (!a->workspace || a->workspace_bytes < need))
+    return fail(SSM_ESPACE, "workspace of %lld bytes required", (long long)need);
+  // lambda = reverse-direction scan of dh with the shifted multipliers, written into db
+  LscanParams p = lscan_params(a->batch, a->seqlen, a->width, a->chunk, !a->reverse, 1);
+  p.a = kv(a->a);
+  p.b = kv(a->dh);
+  p.h = kv(a->db);
+  p.ws = a->workspace;
+  hipError_t e = launch_lscan(p, a->algo, a->dtype, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "ssm_lscan_bwd");
+  LscanGradParams g;
+  memset(&g, 0, sizeof(g));
+  g.B = a->batch;
+  g.L = a->seqlen;
+  g.M = a->width;
+  g.reverse = a->reverse != 0;
+  g.a = kv(a->a);
+  g.h0 = kv(a->h0);
+  g.h = kv(a->h);
+  g.db = kv(a->db);
+  g.da = kv(a->da);
+  g.dh0 = kv(a->dh0);
+  e = launch_lscan_grad(g, a->dtype, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "ssm_lscan_bwd");
+}
+
+// ------------------------------------------------------------------ materialized discretization
+static DiscParams disc_params(const ssm_disc_args *a) {
+  DiscParams p;
+  memset(&p, 0, sizeof(p));
+  p.B = a->batch;
+  p.L = a->seqlen;
+  p.D = a->dim;
+  p.N = a->dstate;
+  const int64_t R = p.B * p.L;
+  p.dtiles = cdiv(p.D, disc_channels(padded_n(p.N)));
+  int64_t groups = cdiv(4096, p.dtiles);
+  if (groups > R) groups = R;
+  p.rows_per_group = cdiv(R, groups);
+  p.ngroups = cdiv(R, p.rows_per_group);
+  return p;
+}
+
+int ssm_disc_check(const ssm_disc_args *a) {
+  if (!a) return fail(SSM_EINVAL, "null args");
+  int rc = check_common(a->batch, a->seqlen, a->dim, a->dstate, a->method, a->dtype);
+  if (rc) return rc;
+  if (a->dtype != SSM_F32 && a->dtype != SSM_F64)
+    return fail(SSM_EINVAL, "materialized discretization takes float32 or float64");
+  if (a->batch * a->seqlen * a->dim * a->dstate >= (1LL << 39)) return fail(SSM_EINVAL, "problem too large");
+  REQUIRE(a->delta, "delta");
+  REQUIRE(a->x, "x");
+  REQUIRE(a->A, "A");
+  REQUIRE(a->Bm, "Bm");
+  return ok();
+}
+
+int64_t ssm_disc_workspace_bytes(const ssm_disc_args *a) {
+  if (ssm_disc_check(a)) return -1;
+  DiscParams p = disc_params(a);
+  const int ss = state_size(a->dtype);
+  return align256(p.B * p.L * p.dtiles * p.N * ss) + align256(p.ngroups * p.D * p.N * ss);
+}
+
+int ssm_disc_fwd(const ssm_disc_args *a, void *stream) {
+  int rc = ssm_disc_check(a);
+  if (rc) return rc;
+  if (!a->a || !a->b) return fail(SSM_EINVAL, "required outputs 'a' and 'b' are missing");
+  DiscParams p = disc_params(a);
+  p.delta = kv(a->delta);
+  p.x = kv(a->x);
+  p.A = kv(a->A);
+  p.Bm = kv(a->Bm);
+  p.a = a->a;
+  p.b = a->b;
+  hipError_t e = launch_disc_fwd(p, a->dtype, a->method, padded_n(a->dstate), (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "ssm_disc_fwd");
+}
+
+int ssm_disc_bwd(const ssm_disc_args *a, void *stream) {
+  int rc = ssm_disc_check(a);
+  if (rc) return rc;
+  if (!a->da || !a->db) return fail(SSM_EINVAL, "required inputs 'da' and 'db' are missing");
+  REQUIRE(a->ddelta, "ddelta");
+  REQUIRE(a->dx, "dx");
+  REQUIRE(a->dA, "dA");
+  REQUIRE(a->dBm, "dBm");
+  DiscParams p = disc_params(a);
+  const int ss = state_size(a->dtype);
+  const int64_t wsB = align256(p.B * p.L * p.dtiles * p.N * ss);
+  const int64_t need = wsB + align256(p.ngroups * p.D * p.N * ss);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(SSM_ESPACE, "workspace of %lld bytes required", (long long)need);
+  p.delta = kv(a->delta);
+  p.x = kv(a->x);
+  p.A = kv(a->A);
+  p.Bm = kv(a->Bm);
+  p.da = a->da;
+  p.db = a->db;
+  p.ddelta = kv(a->ddelta);
+  p.dx = kv(a->dx);
+  p.dA = kv(a->dA);
+  p.dBm = kv(a->dBm);
+  p.ws_dB = a->workspace;
+  p.ws_dA = (char *)a->workspace + wsB;
+  hipError_t e = launch_disc_bwd(p, a->dtype, a->method, padded_n(a->dstate), (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "ssm_disc_bwd");
+}
+
 // ------------------------------------------------------------------ not yet available
-int ssm_lscan_check(const ssm_lscan_args *a) { (void)a; return fail(SSM_EINVAL, "ssm_lscan: not built in this library version"); }
-int64_t ssm_lscan_workspace_bytes(const ssm_lscan_args *a) { (void)a; return -1; }
-int ssm_lscan(const ssm_lscan_args *a, void *s) { (void)s; return ssm_lscan_check(a); }
-int ssm_disc_check(const ssm_disc_args *a) { (void)a; return fail(SSM_EINVAL, "ssm_disc: not built in this library version"); }
-int64_t ssm_disc_workspace_bytes(const ssm_disc_args *a) { (void)a; return -1; }
-int ssm_disc_fwd(const ssm_disc_args *a, void *s) { (void)s; return ssm_disc_check(a); }
-int ssm_disc_bwd(const ssm_disc_args *a, void *s) { (void)s; return ssm_disc_check(a); }
 int ssm_conv_check(const ssm_conv_args *a) { (void)a; return fail(SSM_EINVAL, "ssm_conv: not built in this library version"); }
 int64_t ssm_conv_workspace_bytes(const ssm_conv_args *a) { (void)a; return -1; }
 int ssm_conv_fwd(const ssm_conv_args *a, void *s) { (void)s; return ssm_conv_check(a); }

@@ -78,10 +78,13 @@ k_bwd(const BwdParams p) {
   // slowly decaying accumulation (a -> 1 for small delta) and its float32 rounding dominates the
   // error of ddelta, which sums the state terms with cancellation.  One v_fma_f64 per step keeps
   // it at a single float64 rounding; dlast enters as "a_L dh_L" with a_L = 1.
+  // For ZOH the recompute keeps am1 = a - 1 (accurate expm1) in aa[], and the step
+  // a_{t+1} dh_{t+1} is formed as dh + am1 * dh in float64.
+  constexpr bool M1 = METHOD == 0;
   double dh64 = 0.0;
   if (p.has_dlast && dval && nval)
     dh64 = (double)vload<CT>(p.dlast, b * p.dlast.s0 + d * p.dlast.s1 + n * p.dlast.s2);
-  CT a_next = 1;
+  CT a_next = M1 ? (CT)0 : (CT)1;  // a (or a - 1 for ZOH) of the step after the current one
   CT h0v = 0;
   if (p.has_h0 && dval && nval) h0v = vload<CT>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
   CT dA_acc = 0;
@@ -151,7 +154,8 @@ k_bwd(const BwdParams p) {
 #pragma unroll
         for (int tt = 0; tt < RB; ++tt) {
           const int t = q * RB + tt;
-          disc<METHOD>(rdt[tt], ac, aa[t], cc_[t]);
+          if constexpr (M1) disc_zoh_m1(rdt[tt], ac, aa[t], cc_[t]);
+          else disc<METHOD>(rdt[tt], ac, aa[t], cc_[t]);
           bx[tt] = bcoef<METHOD>(rdt[tt], cc_[t]) * (rB[tt] * rx[tt]);
         }
         if (q + 1 < CK / RB) {
@@ -160,7 +164,11 @@ k_bwd(const BwdParams p) {
           lds_row(&S.B[n][(q + 1) * RB], rB);
         }
 #pragma unroll
-        for (int tt = 0; tt < RB; ++tt) hh[q * RB + tt + 1] = fma(aa[q * RB + tt], hh[q * RB + tt], bx[tt]);
+        for (int tt = 0; tt < RB; ++tt) {
+          const int t = q * RB + tt;
+          if constexpr (M1) hh[t + 1] = fma(aa[t], hh[t], hh[t] + bx[tt]);
+          else hh[t + 1] = fma(aa[t], hh[t], bx[tt]);
+        }
       }
     }
 
@@ -181,9 +189,11 @@ k_bwd(const BwdParams p) {
           const int t = tb + tt;
           const int slot = t - half * RH;
           const CT dtv = rdt[tt], xv = rx[tt], dyv = rdy[tt], Bv = rB[tt], Cv = rC[tt];
-          dh64 = fma(dh64, (double)a_next, (double)(dyv * Cv));
+          if constexpr (M1) dh64 = fma(dh64, (double)a_next, dh64 + (double)(dyv * Cv));
+          else dh64 = fma(dh64, (double)a_next, (double)(dyv * Cv));
           const CT dh = (CT)dh64;
           a_next = aa[t];
+          const CT at = M1 ? (CT)1 + aa[t] : aa[t];
           const CT pC = dyv * hh[t + 1];
           const CT da = dh * hh[t];
           const CT dhc = dh * bcoef<METHOD>(dtv, cc_[t]);
@@ -191,7 +201,7 @@ k_bwd(const BwdParams p) {
           const CT pB = dhc * xv;
           const CT dhBx = dh * (Bv * xv);
           CT dadz, dbdd, d2f;
-          dfactors<METHOD>(dtv, ac, aa[t], cc_[t], dadz, dbdd, d2f);
+          dfactors<METHOD>(dtv, ac, at, cc_[t], dadz, dbdd, d2f);
           const CT g1 = da * dadz;
           const CT pD = fma(g1, ac.A, dhBx * dbdd);
           dA_acc = fma(dtv, g1, fma(dhBx, d2f, dA_acc));
@@ -296,7 +306,8 @@ k_bwd(const BwdParams p) {
 
   if (dval) ((CT *)p.ws_dA)[(b * p.D + d) * NP + n] = dA_acc;
   if (p.has_dh0 && dval && nval)
-    vstore<CT>(p.dh0, b * p.dh0.s0 + d * p.dh0.s1 + n * p.dh0.s2, (CT)(dh64 * (double)a_next));
+    vstore<CT>(p.dh0, b * p.dh0.s0 + d * p.dh0.s1 + n * p.dh0.s2,
+               (CT)(M1 ? fma(dh64, (double)a_next, dh64) : dh64 * (double)a_next));
   if (lane < CW && dw + lane < D) {
     ((CT *)p.ws_dD)[b * p.D + dw + lane] = dD_acc;
     ((CT *)p.ws_db)[b * p.D + dw + lane] = db_acc;

@@ -137,6 +137,19 @@ __device__ __forceinline__ void disc(double dt, const AConst<double> &c, double 
   }
 }
 
+// ZOH with a - 1 instead of a: am1 = expm1(dt A) (the accurate polynomial / a - 1 value above)
+// and coef = am1 / A.  Carrying am1 lets a product a * v be formed as v + am1 * v, which keeps
+// the relative accuracy of expm1 when a is close to 1.
+__device__ __forceinline__ void disc_zoh_m1(float dt, const AConst<float> &c, float &am1, float &coef) {
+  const float z2 = dt * c.A2;
+  am1 = em1_from(z2, fast_exp2(z2));
+  coef = am1 * c.invA;
+}
+__device__ __forceinline__ void disc_zoh_m1(double dt, const AConst<double> &c, double &am1, double &coef) {
+  am1 = expm1(dt * c.A);
+  coef = am1 * c.invA;
+}
+
 // b coefficient multiplying B*x (bilinear stores u in coef).
 template <int METHOD, typename CT>
 __device__ __forceinline__ CT bcoef(CT dt, CT coef) {

@@ -1,0 +1,155 @@
+// Materialized discretization (models/scan.py:39-55) and its backward, for the composed
+// scan path (models/scan.py:202-255), which discretizes a channel tile into (B, L, d, N)
+// tensors, scans them with a chosen algorithm, and maps the scan's gradients (da, db) back to
+// (ddelta, dA, dBm, dx) through autograd (:249).
+//
+// Forward: one lane per output element; the (B, L, D, N) outputs are written contiguously.
+// Backward: a workgroup owns 256/NP channels x NP states and walks a group of (b, l) rows.
+//   ddelta, dx  (B, L, D)  sums over n: cross-lane butterfly inside each NP-lane group;
+//   dBm (B, L, N)          sum over d: per-row LDS reduction over the tile's channels into a
+//                          (row, tile, n) partial, then a fixed-order sum over tiles;
+//   dA (D, N)              sum over (b, l): register accumulation over the group's rows into a
+//                          (group, d, n) partial, then a fixed-order sum over groups.
+// All sums run in a fixed order, so results are bitwise reproducible.
+#include "ssm_device.hpp"
+#include "ssm_internal.hpp"
+#include "ssm_tiles.hpp"
+
+namespace ssm {
+
+template <typename CT, int METHOD>
+__global__ void __launch_bounds__(kThreads) k_disc_fwd(const DiscParams p) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t total = p.B * p.L * p.D * p.N;
+  if (i >= total) return;
+  const int64_t n = i % p.N, d = (i / p.N) % p.D, row = i / (p.N * p.D);
+  const int64_t b = row / p.L, t = row % p.L;
+  const CT dt = vload<CT>(p.delta, b * p.delta.s0 + t * p.delta.s1 + d * p.delta.s2);
+  const CT xv = vload<CT>(p.x, b * p.x.s0 + t * p.x.s1 + d * p.x.s2);
+  const CT Bv = vload<CT>(p.Bm, b * p.Bm.s0 + t * p.Bm.s1 + n * p.Bm.s2);
+  const AConst<CT> ac = make_aconst(vload<CT>(p.A, d * p.A.s0 + n * p.A.s1));
+  CT a, coef;
+  disc<METHOD>(dt, ac, a, coef);
+  ((CT *)p.a)[i] = a;
+  ((CT *)p.b)[i] = bcoef<METHOD>(dt, coef) * (Bv * xv);
+}
+
+template <typename CT, int NP, int METHOD>
+__global__ void __launch_bounds__(kThreads) k_disc_bwd(const DiscParams p) {
+  constexpr int DT = kThreads / NP;
+  __shared__ CT red[DT][NP];
+  const int tid = threadIdx.x, c = tid / NP, n = tid % NP;
+  const int64_t tile = blockIdx.x, g = blockIdx.y;
+  const int64_t d = tile * DT + c;
+  const bool valid = d < p.D && n < p.N;
+  const int64_t R = p.B * p.L;
+  const int64_t r0 = g * p.rows_per_group, r1 = r0 + p.rows_per_group < R ? r0 + p.rows_per_group : R;
+  AConst<CT> ac = make_aconst<CT>(-1);
+  if (valid) ac = make_aconst(vload<CT>(p.A, d * p.A.s0 + n * p.A.s1));
+  CT gA = 0;
+  for (int64_t r = r0; r < r1; ++r) {
+    const int64_t b = r / p.L, t = r % p.L;
+    CT gd = 0, gx = 0, gB = 0;
+    if (valid) {
+      const CT dt = vload<CT>(p.delta, b * p.delta.s0 + t * p.delta.s1 + d * p.delta.s2);
+      const CT xv = vload<CT>(p.x, b * p.x.s0 + t * p.x.s1 + d * p.x.s2);
+      const CT Bv = vload<CT>(p.Bm, b * p.Bm.s0 + t * p.Bm.s1 + n * p.Bm.s2);
+      const int64_t e = (r * p.D + d) * p.N + n;
+      const CT ga = ((const CT *)p.da)[e], gb = ((const CT *)p.db)[e];
+      CT a, coef, dadz, dbdd, d2f;
+      disc<METHOD>(dt, ac, a, coef);
+      dfactors<METHOD>(dt, ac, a, coef, dadz, dbdd, d2f);
+      const CT bx = Bv * xv, gz = ga * dadz, gbc = gb * bcoef<METHOD>(dt, coef);
+      gd = fma(ac.A, gz, gb * dbdd * bx);
+      gA += fma(dt, gz, gb * d2f * bx);
+      gx = gbc * Bv;
+      gB = gbc * xv;
+    }
+#pragma unroll
+    for (int off = NP / 2; off > 0; off >>= 1) {
+      gd += __shfl_xor(gd, off);
+      gx += __shfl_xor(gx, off);
+    }
+    if (n == 0 && d < p.D) {
+      const int64_t b = r / p.L, t = r % p.L;
+      vstore<CT>(p.ddelta, b * p.ddelta.s0 + t * p.ddelta.s1 + d * p.ddelta.s2, gd);
+      vstore<CT>(p.dx, b * p.dx.s0 + t * p.dx.s1 + d * p.dx.s2, gx);
+    }
+    red[c][n] = gB;
+    __syncthreads();
+    if (tid < NP) {
+      CT s = 0;
+#pragma unroll
+      for (int k = 0; k < DT; ++k) s += red[k][tid];
+      if (tid < p.N) ((CT *)p.ws_dB)[(r * p.dtiles + tile) * p.N + tid] = s;
+    }
+    __syncthreads();
+  }
+  if (valid) ((CT *)p.ws_dA)[(g * p.D + d) * p.N + n] = gA;
+}
+
+template <typename CT>
+__global__ void __launch_bounds__(kThreads) k_disc_fin(const DiscParams p) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t nB = p.B * p.L * p.N, nA = p.D * p.N;
+  if (i < nB) {
+    const int64_t n = i % p.N, r = i / p.N, b = r / p.L, t = r % p.L;
+    const CT *w = (const CT *)p.ws_dB + r * p.dtiles * p.N + n;
+    CT s = 0;
+    for (int64_t k = 0; k < p.dtiles; ++k) s += w[k * p.N];
+    vstore<CT>(p.dBm, b * p.dBm.s0 + t * p.dBm.s1 + n * p.dBm.s2, s);
+  } else if (i < nB + nA) {
+    const int64_t j = i - nB, n = j % p.N, d = j / p.N;
+    const CT *w = (const CT *)p.ws_dA + j;
+    CT s = 0;
+    for (int64_t k = 0; k < p.ngroups; ++k) s += w[k * nA];
+    vstore<CT>(p.dA, d * p.dA.s0 + n * p.dA.s1, s);
+  }
+}
+
+template <typename CT, int M>
+static hipError_t disc_fwd_t(const DiscParams &p, hipStream_t s) {
+  const int64_t total = p.B * p.L * p.D * p.N;
+  hipLaunchKernelGGL((k_disc_fwd<CT, M>), dim3((unsigned)((total + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                     s, p);
+  return hipGetLastError();
+}
+
+template <typename CT>
+static hipError_t disc_fwd_m(const DiscParams &p, int method, hipStream_t s) {
+  return method == 0 ? disc_fwd_t<CT, 0>(p, s) : method == 1 ? disc_fwd_t<CT, 1>(p, s) : disc_fwd_t<CT, 2>(p, s);
+}
+
+hipError_t launch_disc_fwd(const DiscParams &p, int dtype, int method, int, hipStream_t s) {
+  return dtype == 3 ? disc_fwd_m<double>(p, method, s) : disc_fwd_m<float>(p, method, s);
+}
+
+template <typename CT, int NP, int M>
+static hipError_t disc_bwd_t(const DiscParams &p, hipStream_t s) {
+  hipLaunchKernelGGL((k_disc_bwd<CT, NP, M>), dim3((unsigned)p.dtiles, (unsigned)p.ngroups), dim3(kThreads), 0, s, p);
+  const int64_t n = p.B * p.L * p.N + p.D * p.N;
+  hipLaunchKernelGGL((k_disc_fin<CT>), dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename CT, int NP>
+static hipError_t disc_bwd_m(const DiscParams &p, int method, hipStream_t s) {
+  return method == 0 ? disc_bwd_t<CT, NP, 0>(p, s) : method == 1 ? disc_bwd_t<CT, NP, 1>(p, s)
+                                                                : disc_bwd_t<CT, NP, 2>(p, s);
+}
+
+template <typename CT>
+static hipError_t disc_bwd_n(const DiscParams &p, int method, int np, hipStream_t s) {
+  switch (np) {
+    case 8: return disc_bwd_m<CT, 8>(p, method, s);
+    case 16: return disc_bwd_m<CT, 16>(p, method, s);
+    case 32: return disc_bwd_m<CT, 32>(p, method, s);
+    default: return disc_bwd_m<CT, 64>(p, method, s);
+  }
+}
+
+hipError_t launch_disc_bwd(const DiscParams &p, int dtype, int method, int np, hipStream_t s) {
+  return dtype == 3 ? disc_bwd_n<double>(p, method, np, s) : disc_bwd_n<float>(p, method, np, s);
+}
+
+}  // namespace ssm

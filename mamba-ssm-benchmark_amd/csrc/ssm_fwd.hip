@@ -101,16 +101,20 @@ k_fwd(const FwdParams p) {
         lds_row(&S.B[n][(q + 1) * RB], nB);
         lds_row(&S.C[n][(q + 1) * RB], nC);
       }
+      // ZOH keeps a - 1 (accurate expm1) and updates h <- h + (a - 1) h + b, which keeps the
+      // decay's relative accuracy for slowly decaying states (a close to 1).
       CT a[RB], bx[RB];
 #pragma unroll
       for (int tt = 0; tt < RB; ++tt) {
         CT coef;
-        disc<METHOD>(rdt[tt], ac, a[tt], coef);
+        if constexpr (METHOD == 0) disc_zoh_m1(rdt[tt], ac, a[tt], coef);
+        else disc<METHOD>(rdt[tt], ac, a[tt], coef);
         bx[tt] = bcoef<METHOD>(rdt[tt], coef) * (rB[tt] * rx[tt]);
       }
 #pragma unroll
       for (int tt = 0; tt < RB; ++tt) {
-        h = fma(a[tt], h, bx[tt]);
+        if constexpr (METHOD == 0) h = fma(a[tt], h, h + bx[tt]);
+        else h = fma(a[tt], h, bx[tt]);
         S.y[q * RB + tt][c][n] = rC[tt] * h;
       }
       if (q + 1 < CK / RB) {

@@ -90,9 +90,45 @@ struct StepParams {
   KView x, dt, A, Bm, Cm, Dsk, z, bias, h, out;
 };
 
+// Linear scan h_t = mult_t h_{t-1} + b_t over (B, L, M), processed in the order t = 0..L-1
+// (reverse: L-1..0).  shift: mult at a processing position is the a of the previous position
+// (1 at the first), which turns the scan into the adjoint recurrence.
+struct LscanParams {
+  int64_t B, L, M;
+  int64_t nc;   // chunks (chunked algorithm)
+  int chunk;    // steps per chunk
+  int reverse, shift;
+  KView a, b, h0, h;  // h0: (B, M) with strides s0, s1
+  void *ws;           // chunked: 3 x (B, nc, M) state type (P, E, h_in)
+};
+
+// da_t = lambda_t h_prev(t) and dh0 = a_first lambda_first; `reverse` is the forward's direction.
+struct LscanGradParams {
+  int64_t B, L, M;
+  int reverse;
+  KView a, h0, h, db, da, dh0;  // db holds lambda
+};
+
+// Materialized discretization on contiguous (B, L, D, N) tensors.
+struct DiscParams {
+  int64_t B, L, D, N;
+  int64_t rows_per_group, ngroups, dtiles;
+  KView delta, x, A, Bm, ddelta, dx, dA, dBm;
+  void *a, *b;
+  const void *da, *db;
+  void *ws_dB;  // (B*L, dtiles, N) partial sums over each channel tile
+  void *ws_dA;  // (ngroups, D, N) partial sums over each group of rows
+};
+
 hipError_t launch_fwd(const FwdParams &p, int dtype, int method, int np, hipStream_t s);
 hipError_t launch_bwd(const BwdParams &p, int dtype, int method, int np, hipStream_t s);
 hipError_t launch_bwd_finalize(const FinParams &p, int dtype, hipStream_t s);
 hipError_t launch_step(const StepParams &p, int dtype, int method, int np, hipStream_t s);
+hipError_t launch_lscan(const LscanParams &p, int algo, int dtype, hipStream_t s);
+hipError_t launch_lscan_grad(const LscanGradParams &p, int dtype, hipStream_t s);
+// Channels per workgroup of the discretize backward (its dB partial-sum tile).
+inline int disc_channels(int np) { return kThreads / np; }
+hipError_t launch_disc_fwd(const DiscParams &p, int dtype, int method, int np, hipStream_t s);
+hipError_t launch_disc_bwd(const DiscParams &p, int dtype, int method, int np, hipStream_t s);
 
 }  // namespace ssm

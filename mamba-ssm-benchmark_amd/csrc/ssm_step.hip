@@ -28,12 +28,14 @@ __global__ void __launch_bounds__(kThreads) k_step(const StepParams p) {
     if (nval) {
       const AConst<CT> ac = make_aconst(vload<CT>(p.A, d * p.A.s0 + n * p.A.s1));
       CT a, coef;
-      disc<METHOD>(dt, ac, a, coef);
+      if constexpr (METHOD == 0) disc_zoh_m1(dt, ac, a, coef);  // a holds a - 1
+      else disc<METHOD>(dt, ac, a, coef);
       const CT Bv = Conv<IT>::load(vp<IT>(p.Bm) + b * p.Bm.s0 + n * p.Bm.s1);
       const CT Cv = Conv<IT>::load(vp<IT>(p.Cm) + b * p.Cm.s0 + n * p.Cm.s1);
       const int64_t ho = b * p.h.s0 + d * p.h.s1 + n * p.h.s2;
       CT h = vload<CT>(p.h, ho);
-      h = fma(a, h, bcoef<METHOD>(dt, coef) * (Bv * xv));
+      const CT bx = bcoef<METHOD>(dt, coef) * (Bv * xv);
+      h = METHOD == 0 ? fma(a, h, h + bx) : fma(a, h, bx);
       vstore<CT>(p.h, ho, h);
       y = Cv * h;
     }

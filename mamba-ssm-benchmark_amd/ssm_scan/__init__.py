@@ -9,14 +9,19 @@ include/ssm_scan.h); the package only prepares views, allocates outputs with tor
 launches on torch's current stream.  There is no CPU fallback.
 """
 
-from . import _abi, plan
+from . import _abi, plan, scan
 from .hip_scan import (METHODS, FusedSelectiveScanFn, selective_scan_fn, selective_scan_hip,
                        selective_scan_triton)
 from .profiling import KernelTimer
+from .scan import (DISCRETIZATIONS, SCANS, SelectiveScanFn, default_chunk, discretize,
+                   scan_blelloch, scan_chunked, scan_hillis_steele, scan_sequential,
+                   selective_scan, selective_scan_reference)
 from .step import ssm_step
 
 __all__ = ["METHODS", "FusedSelectiveScanFn", "selective_scan_fn", "selective_scan_hip",
-           "selective_scan_triton", "ssm_step", "KernelTimer", "plan"]
+           "selective_scan_triton", "ssm_step", "KernelTimer", "plan", "scan", "DISCRETIZATIONS",
+           "SCANS", "SelectiveScanFn", "default_chunk", "discretize", "scan_blelloch", "scan_chunked",
+           "scan_hillis_steele", "scan_sequential", "selective_scan", "selective_scan_reference"]
 
 
 def library_path():

@@ -67,6 +67,15 @@ class LscanArgs(ctypes.Structure):
                 ("workspace", c_vp), ("workspace_bytes", c_i64)]
 
 
+class LscanBwdArgs(ctypes.Structure):
+    _fields_ = [("batch", c_i64), ("seqlen", c_i64), ("width", c_i64),
+                ("algo", c_i32), ("dtype", c_i32), ("reverse", c_i32), ("reserved0", c_i32),
+                ("chunk", c_i64),
+                ("a", Tensor), ("h0", Tensor), ("h", Tensor), ("dh", Tensor),
+                ("da", Tensor), ("db", Tensor), ("dh0", Tensor),
+                ("workspace", c_vp), ("workspace_bytes", c_i64)]
+
+
 class DiscArgs(ctypes.Structure):
     _fields_ = [("batch", c_i64), ("seqlen", c_i64), ("dim", c_i64), ("dstate", c_i64),
                 ("method", c_i32), ("dtype", c_i32),
@@ -93,18 +102,21 @@ _SIGS = {
     "ssm_bwd_check": (c_i32, [ctypes.POINTER(BwdArgs)]),
     "ssm_step_check": (c_i32, [ctypes.POINTER(StepArgs)]),
     "ssm_lscan_check": (c_i32, [ctypes.POINTER(LscanArgs)]),
+    "ssm_lscan_bwd_check": (c_i32, [ctypes.POINTER(LscanBwdArgs)]),
     "ssm_disc_check": (c_i32, [ctypes.POINTER(DiscArgs)]),
     "ssm_conv_check": (c_i32, [ctypes.POINTER(ConvArgs)]),
     "ssm_fwd_saved_bytes": (c_i64, [ctypes.POINTER(FwdArgs)]),
     "ssm_fwd_workspace_bytes": (c_i64, [ctypes.POINTER(FwdArgs)]),
     "ssm_bwd_workspace_bytes": (c_i64, [ctypes.POINTER(BwdArgs)]),
     "ssm_lscan_workspace_bytes": (c_i64, [ctypes.POINTER(LscanArgs)]),
+    "ssm_lscan_bwd_workspace_bytes": (c_i64, [ctypes.POINTER(LscanBwdArgs)]),
     "ssm_disc_workspace_bytes": (c_i64, [ctypes.POINTER(DiscArgs)]),
     "ssm_conv_workspace_bytes": (c_i64, [ctypes.POINTER(ConvArgs)]),
     "ssm_fwd": (c_i32, [ctypes.POINTER(FwdArgs), c_vp]),
     "ssm_bwd": (c_i32, [ctypes.POINTER(BwdArgs), c_vp]),
     "ssm_step": (c_i32, [ctypes.POINTER(StepArgs), c_vp]),
     "ssm_lscan": (c_i32, [ctypes.POINTER(LscanArgs), c_vp]),
+    "ssm_lscan_bwd": (c_i32, [ctypes.POINTER(LscanBwdArgs), c_vp]),
     "ssm_disc_fwd": (c_i32, [ctypes.POINTER(DiscArgs), c_vp]),
     "ssm_disc_bwd": (c_i32, [ctypes.POINTER(DiscArgs), c_vp]),
     "ssm_conv_fwd": (c_i32, [ctypes.POINTER(ConvArgs), c_vp]),

@@ -141,6 +141,52 @@ SCANS = {"sequential": scan_sequential, "hillis_steele": scan_hillis_steele,
          "blelloch": scan_blelloch, "chunked": scan_chunked}          # models/scan.py:168-173
 
 
+def scan_vjp(a, h0, h, dh):
+    """Adjoint of scan_sequential, as models/scan.py:233-248 computes it inside
+    SelectiveScanFn.backward: lambda_t = dh_t + a_{t+1} lambda_{t+1} (the reverse scan of
+    :239-240), da_t = lambda_t h_{t-1} (h_{-1} = h0 or 0), db_t = lambda_t, dh0 = a_0 lambda_0.
+    Returns (da, db, dh0)."""
+    L = a.shape[1]
+    lam = np.empty_like(dh)
+    acc = np.zeros_like(dh[:, 0])
+    for t in range(L - 1, -1, -1):
+        acc = dh[:, t] + (a[:, t + 1] * acc if t + 1 < L else 0.0)
+        lam[:, t] = acc
+    hz = np.zeros_like(h[:, 0]) if h0 is None else h0
+    h_prev = np.concatenate([hz[:, None], h[:, :-1]], 1)
+    return lam * h_prev, lam, (None if h0 is None else a[:, 0] * lam[:, 0])
+
+
+def discretize_vjp(delta, A, Bm, x, ga, gb, method="zoh"):
+    """Vector-Jacobian product of discretize (the autograd.grad of models/scan.py:249):
+    given ga = dL/da, gb = dL/db (B, L, D, N) returns (ddelta, dA, dBm, dx).  Closed-form
+    derivatives of the three discretizations (ZOH db/dA uses f(z) = (z e^z - expm1 z)/z^2,
+    a 4-term series below |z| < 1e-3 as kernels/triton_scan.py:199-200 does)."""
+    z = delta[..., None] * A
+    Bx = x[..., None] * Bm[:, :, None, :]
+    dt = delta[..., None]
+    if method == "zoh":
+        a = np.exp(z)
+        e = np.expm1(z)
+        small = np.abs(z) < 1e-3
+        zs = np.where(small, 1.0, z)
+        f = np.where(small, 0.5 + z / 3.0 + z * z / 8.0 + z ** 3 / 30.0, (zs * a - e) / (zs * zs))
+        dadz, dbdd, d2f, coef = a, a, dt * dt * f, e / A
+    elif method == "euler":
+        a = np.exp(z)
+        dadz, dbdd, d2f, coef = a, np.ones_like(z), np.zeros_like(z), dt * np.ones_like(z)
+    elif method == "bilinear":
+        u = 1.0 / (1.0 - 0.5 * z)
+        dadz, dbdd, d2f, coef = u * u, u * u, 0.5 * dt * dt * u * u, dt * u
+    else:
+        raise ValueError(f"unknown discretization {method!r}")
+    ddelta = np.sum(ga * dadz * A + gb * dbdd * Bx, axis=3)
+    dA = np.sum(ga * dadz * dt + gb * d2f * Bx, axis=(0, 1))
+    dBm = np.sum(gb * coef * x[..., None], axis=2)
+    dx = np.sum(gb * coef * Bm[:, :, None, :], axis=3)
+    return ddelta, dA, dBm, dx
+
+
 # ----------------------------------------------------------------------------- selective scan
 
 def silu(v):

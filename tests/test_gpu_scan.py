@@ -1,0 +1,238 @@
+"""Parity of the composed scan path (ssm_scan.scan <-> models/scan.py) with the float64 oracle.
+
+Covers the materialized discretization (ssm_disc_fwd / ssm_disc_bwd), the four linear-scan
+algorithms and their adjoint (ssm_lscan / ssm_lscan_bwd), SelectiveScanFn over channel tiles,
+and the selective_scan dispatcher.  The reference's own checks are mirrored: all algorithms
+equal the sequential loop incl. ragged chunks (tests/test_scan.py:34-54), extreme decays
+(:132-142), gradients against the textbook recurrence (:67-88).  Tolerances: float32 rtol
+1e-4 / atol 1e-5; float64 rtol 1e-10.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import ssm_scan
+from ssm_scan import scan as S
+from oracle import scan_ref as R
+from ssm_inputs import np64
+
+pytestmark = pytest.mark.gpu
+
+ALGOS = ("sequential", "hillis_steele", "blelloch", "chunked")
+TOL = {torch.float32: (1e-4, 1e-5), torch.float64: (1e-10, 1e-12)}
+
+
+def close(got, ref, dtype, name="", scale_ref=True):
+    rtol, atol = TOL[dtype]
+    ref = np.asarray(ref)
+    scale = max(1.0, float(np.sqrt(np.mean(np.square(ref))))) if scale_ref and ref.size else 1.0
+    np.testing.assert_allclose(np64(got), ref, rtol=rtol, atol=atol * scale, err_msg=name)
+
+
+def sel_inputs(B=2, L=33, D=20, N=8, seed=0, h0=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, L, D, generator=g, dtype=torch.float64)
+    delta = torch.rand(B, L, D, generator=g, dtype=torch.float64) * 0.5 + 0.01
+    A = -torch.rand(D, N, generator=g, dtype=torch.float64) * 2 - 0.1
+    Bm = torch.randn(B, L, N, generator=g, dtype=torch.float64)
+    Cm = torch.randn(B, L, N, generator=g, dtype=torch.float64)
+    hz = torch.randn(B, D, N, generator=g, dtype=torch.float64) if h0 else None
+    return x, delta, A, Bm, Cm, hz
+
+
+def ab_inputs(shape, seed=0, lo=0.05, hi=0.95):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.rand(shape, generator=g, dtype=torch.float64) * (hi - lo) + lo
+    b = torch.randn(shape, generator=g, dtype=torch.float64)
+    h0 = torch.randn((shape[0],) + tuple(shape[2:]), generator=g, dtype=torch.float64)
+    return a, b, h0
+
+
+# ------------------------------------------------------------------ discretization
+@pytest.mark.parametrize("method", R.DISCRETIZATIONS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_discretize_forward_and_vjp(dev, method, dtype):
+    x, delta, A, Bm, _, _ = sel_inputs(B=2, L=37, D=21, N=5, seed=1, h0=False)
+    g = torch.Generator().manual_seed(2)
+    ga = torch.randn(2, 37, 21, 5, generator=g, dtype=torch.float64)
+    gb = torch.randn(2, 37, 21, 5, generator=g, dtype=torch.float64)
+    leaves = [t.to(dev, dtype).requires_grad_() for t in (delta, A, Bm, x)]
+    a, b = S.discretize(*leaves, method=method)
+    assert a.shape == (2, 37, 21, 5) and a.dtype == dtype
+    ra, rb = R.discretize(*(np64(t) for t in (delta, A, Bm, x)), method)
+    close(a.detach(), ra, dtype, "a")
+    close(b.detach(), rb, dtype, "b")
+    torch.autograd.backward((a, b), (ga.to(dev, dtype), gb.to(dev, dtype)))
+    ref = R.discretize_vjp(*(np64(t) for t in (delta, A, Bm, x)), np64(ga), np64(gb), method)
+    for name, t, r in zip(("ddelta", "dA", "dBm", "dx"), leaves, ref):
+        close(t.grad, r, dtype, name)
+
+
+def test_discretize_strided_views_and_errors(dev):
+    x, delta, A, Bm, _, _ = sel_inputs(B=2, L=16, D=8, N=4, seed=3, h0=False)
+    xs = x.transpose(1, 2).contiguous().transpose(1, 2).to(dev, torch.float32)   # (B, D, L) storage
+    big = torch.randn(2, 16, 12, dtype=torch.float64)
+    big[..., 2:6] = Bm
+    Bv = big[..., 2:6].to(dev, torch.float32)                                  # strided split view
+    a, b = S.discretize(delta.to(dev, torch.float32), A.to(dev, torch.float32), Bv, xs, "zoh")
+    ra, rb = R.discretize(np64(delta), np64(A), np64(Bm), np64(x), "zoh")
+    close(a, ra, torch.float32)
+    close(b, rb, torch.float32)
+    with pytest.raises(ValueError):
+        S.discretize(delta.to(dev), A.to(dev), Bm.to(dev), x.to(dev), "rk4")
+
+
+def test_zoh_matrix_matches_diagonal_discretize(dev):
+    A = -torch.tensor([0.5, 1.5, 3.0], dtype=torch.float64, device=dev)
+    Ad, Bd = S.zoh_matrix(torch.diag(A), torch.ones(3, 1, dtype=torch.float64, device=dev), 0.3)
+    a, b = S.discretize(torch.full((1, 1, 1), 0.3, dtype=torch.float64, device=dev), A[None],
+                        torch.ones(1, 1, 3, dtype=torch.float64, device=dev),
+                        torch.ones(1, 1, 1, dtype=torch.float64, device=dev), "zoh")
+    close(torch.diagonal(Ad), np64(a[0, 0, 0]), torch.float64)
+    close(Bd[:, 0], np64(b[0, 0, 0]), torch.float64)
+
+
+# ------------------------------------------------------------------ linear scans
+@pytest.mark.parametrize("name", ALGOS)
+@pytest.mark.parametrize("L", [1, 2, 7, 255, 256, 257, 512, 600, 1031])
+@pytest.mark.parametrize("with_h0", [False, True])
+def test_scans_match_sequential_oracle(dev, name, L, with_h0):
+    a, b, h0 = ab_inputs((2, L, 3, 5), seed=L)
+    h0 = h0 if with_h0 else None
+    ref = R.scan_sequential(np64(a), np64(b), None if h0 is None else np64(h0))
+    for dtype in (torch.float64, torch.float32):
+        got = S.SCANS[name](a.to(dev, dtype), b.to(dev, dtype), None if h0 is None else h0.to(dev, dtype))
+        assert got.shape == a.shape and got.dtype == dtype
+        close(got, ref, dtype, f"{name} {dtype}")
+
+
+@pytest.mark.parametrize("chunk", [1, 3, 4, 5, 16, 64, 100, 700])
+def test_chunked_any_chunk_size(dev, chunk):
+    a, b, h0 = ab_inputs((3, 97, 4), seed=chunk)
+    ref = R.scan_sequential(np64(a), np64(b), np64(h0))
+    got = S.scan_chunked(a.to(dev), b.to(dev), h0.to(dev), chunk_size=chunk)
+    close(got, ref, torch.float64)
+
+
+@pytest.mark.parametrize("name", ALGOS)
+def test_scans_long_sequence_extreme_decays(dev, name):
+    """tests/test_scan.py:132-142: decays near 0 and near 1 over a long sequence."""
+    g = torch.Generator().manual_seed(4)
+    L = 4096
+    a = torch.where(torch.rand(2, L, 8, generator=g) < 0.5, torch.full((2, L, 8), 1e-6),
+                    torch.full((2, L, 8), 1 - 1e-6)).double()
+    b = torch.randn(2, L, 8, generator=g, dtype=torch.float64)
+    ref = R.scan_sequential(np64(a), np64(b))
+    close(S.SCANS[name](a.to(dev), b.to(dev)), ref, torch.float64)
+    a32, b32 = a.float(), b.float()     # the oracle consumes the same float32-rounded decays
+    ref32 = R.scan_sequential(np64(a32), np64(b32))
+    close(S.SCANS[name](a32.to(dev), b32.to(dev)), ref32, torch.float32)
+
+
+@pytest.mark.parametrize("name", ALGOS)
+@pytest.mark.parametrize("with_h0", [False, True])
+def test_scan_adjoint_matches_oracle(dev, name, with_h0):
+    a, b, h0 = ab_inputs((2, 301, 6), seed=11)
+    g = torch.Generator().manual_seed(12)
+    dh = torch.randn(2, 301, 6, generator=g, dtype=torch.float64)
+    for dtype in (torch.float64, torch.float32):
+        leaves = [a.to(dev, dtype).requires_grad_(), b.to(dev, dtype).requires_grad_()]
+        hz = h0.to(dev, dtype).requires_grad_() if with_h0 else None
+        h = S.SCANS[name](leaves[0], leaves[1], hz)
+        h.backward(dh.to(dev, dtype))
+        href = R.scan_sequential(np64(a), np64(b), np64(h0) if with_h0 else None)
+        da, db, dh0 = R.scan_vjp(np64(a), np64(h0) if with_h0 else None, href, np64(dh))
+        close(leaves[0].grad, da, dtype, "da")
+        close(leaves[1].grad, db, dtype, "db")
+        if with_h0:
+            close(hz.grad, dh0, dtype, "dh0")
+
+
+def test_reverse_scan_and_errors(dev):
+    a, b, h0 = ab_inputs((2, 50, 3), seed=13)
+    ref = np.flip(R.scan_sequential(np.flip(np64(a), 1), np.flip(np64(b), 1), np64(h0)), 1)
+    for algo in (1, 2, 3, 4):
+        got = S.LinearScanFn.apply(a.to(dev), b.to(dev), h0.to(dev), algo, None, True)
+        close(got, ref, torch.float64, f"reverse algo {algo}")
+    with pytest.raises(KeyError):
+        S.SCANS["parallel"]
+    with pytest.raises(ValueError):
+        S.scan_sequential(a.to(dev), b[:, :10].to(dev))
+
+
+# ------------------------------------------------------------------ composed selective scan
+def _oracle_sel(ins, method, dy, dlast):
+    x, delta, A, Bm, Cm, h0 = (np64(t) for t in ins)
+    _, y, last = R.selective_scan_fwd(x, delta, A, Bm, Cm, h0, method)
+    g = R.selective_scan_bwd(x, delta, A, Bm, Cm, np64(dy), h0, method, dlast=np64(dlast))
+    return y, last, g
+
+
+@pytest.mark.parametrize("scan", ALGOS)
+@pytest.mark.parametrize("method", R.DISCRETIZATIONS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_selective_scan_composed_matches_oracle(dev, scan, method, dtype):
+    ins = sel_inputs(B=2, L=45, D=20, N=8, seed=5, h0=True)
+    g = torch.Generator().manual_seed(6)
+    dy = torch.randn(2, 45, 20, generator=g, dtype=torch.float64)
+    dlast = torch.randn(2, 20, 8, generator=g, dtype=torch.float64)
+    leaves = [t.to(dev, dtype).requires_grad_() for t in ins]
+    y, last = S.selective_scan(*leaves, method=method, scan=scan, d_block=7,
+                               chunk_size=5 if scan == "chunked" else None)
+    assert y.dtype == dtype and last.dtype == dtype and last.shape == (2, 20, 8)
+    ((y * dy.to(dev, dtype)).sum() + (last * dlast.to(dev, dtype)).sum()).backward()
+    ry, rlast, rg = _oracle_sel(ins, method, dy, dlast)
+    close(y.detach(), ry, dtype, "y")
+    close(last.detach(), rlast, dtype, "last")
+    for name, t in zip(("dx", "ddelta", "dA", "dB", "dC", "dh0"), leaves):
+        close(t.grad, rg[name], dtype, name)
+
+
+@pytest.mark.parametrize("scan", ["reference", "triton", "auto", "chunked"])
+def test_selective_scan_dispatch_names(dev, scan):
+    ins = sel_inputs(B=2, L=40, D=16, N=16, seed=8, h0=True)
+    leaves = [t.to(dev, torch.float32).requires_grad_() for t in ins]
+    y, last = S.selective_scan(*leaves, method="zoh", scan=scan)
+    dy = torch.ones_like(y)
+    y.backward(dy)
+    ry, rlast, rg = _oracle_sel(ins, "zoh", dy.cpu().double(), None)
+    close(y.detach(), ry, torch.float32, "y")
+    close(last.detach(), rlast, torch.float32, "last")
+    for name, t in zip(("dx", "ddelta", "dA", "dB", "dC", "dh0"), leaves):
+        close(t.grad, rg[name], torch.float32, name)
+
+
+def test_selective_scan_auto_non_power_of_two_uses_chunked(dev):
+    ins = sel_inputs(B=1, L=20, D=8, N=6, seed=9, h0=False)
+    assert ssm_scan.plan.resolve_scan("auto", True, "zoh", 6) == "chunked"
+    y, last = S.selective_scan(*(None if t is None else t.to(dev, torch.float32) for t in ins), scan="auto")
+    ry, rlast, _ = _oracle_sel(ins, "zoh", torch.zeros(1, 20, 8, dtype=torch.float64), None)
+    close(y, ry, torch.float32)
+    close(last, rlast, torch.float32)
+
+
+def test_selective_scan_errors_and_dtypes(dev):
+    ins = [None if t is None else t.to(dev, torch.float32) for t in sel_inputs(B=1, L=8, D=4, N=4, h0=False)]
+    with pytest.raises(KeyError):
+        S.selective_scan(*ins, scan="parallel")
+    with pytest.raises(ValueError):
+        S.selective_scan(*ins, method="rk4", scan="chunked")
+    with pytest.raises(ValueError):
+        S.selective_scan(*ins, method="rk4", scan="triton")
+    bf = [t.to(torch.bfloat16) if t is not None else None for t in ins]
+    for scan in ("chunked", "triton", "reference"):
+        y, last = S.selective_scan(*bf, scan=scan)
+        assert y.dtype == torch.bfloat16 and last.dtype == torch.float32
+
+
+def test_composed_backward_is_deterministic(dev):
+    ins = sel_inputs(B=2, L=64, D=24, N=8, seed=10, h0=True)
+    runs = []
+    for _ in range(2):
+        leaves = [t.to(dev, torch.float32).requires_grad_() for t in ins]
+        y, last = S.selective_scan(*leaves, scan="blelloch", d_block=5)
+        (y.sum() + last.sum()).backward()
+        runs.append([t.grad.clone() for t in leaves])
+    for g1, g2 in zip(*runs):
+        assert torch.equal(g1, g2)

@@ -324,3 +324,54 @@ def test_c_oracle_matches_numpy_oracle(method, h0, gate):
     assert set(g1) == set(g2)
     for k in g1:
         np.testing.assert_allclose(g2[k], g1[k], rtol=1e-11, atol=1e-12, err_msg=k)
+
+
+# --------------------------------------------------------------------------- scan / discretize VJPs
+
+@pytest.mark.parametrize("with_h0", [False, True])
+def test_scan_vjp_matches_torch_autograd(with_h0):
+    a, b = rand_ab(B=2, L=13, D=2, N=3, seed=5)
+    g = np.random.default_rng(6)
+    h0 = g.standard_normal((2, 2, 3)) if with_h0 else None
+    dh = g.standard_normal(b.shape)
+    h = R.scan_sequential(a, b, h0)
+    da, db, dh0 = R.scan_vjp(a, h0, h, dh)
+    ta, tb = torch.tensor(a, requires_grad=True), torch.tensor(b, requires_grad=True)
+    th0 = torch.tensor(h0, requires_grad=True) if with_h0 else None
+    hh = torch.zeros_like(tb[:, 0]) if th0 is None else th0
+    outs = []
+    for t in range(a.shape[1]):
+        hh = ta[:, t] * hh + tb[:, t]
+        outs.append(hh)
+    (torch.stack(outs, 1) * torch.tensor(dh)).sum().backward()
+    np.testing.assert_allclose(da, ta.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(db, tb.grad.numpy(), rtol=1e-12, atol=1e-12)
+    if with_h0:
+        np.testing.assert_allclose(dh0, th0.grad.numpy(), rtol=1e-12, atol=1e-12)
+    else:
+        assert dh0 is None
+
+
+@pytest.mark.parametrize("method", R.DISCRETIZATIONS)
+@pytest.mark.parametrize("tiny", [False, True])
+def test_discretize_vjp_matches_torch_autograd(method, tiny):
+    g = np.random.default_rng(9)
+    B, L, D, N = 2, 5, 3, 4
+    delta = g.random((B, L, D)) * (1e-5 if tiny else 0.8) + (1e-6 if tiny else 0.01)
+    A = -g.random((D, N)) * 3 - 0.1
+    Bm, x = g.standard_normal((B, L, N)), g.standard_normal((B, L, D))
+    ga, gb = g.standard_normal((B, L, D, N)), g.standard_normal((B, L, D, N))
+    ours = R.discretize_vjp(delta, A, Bm, x, ga, gb, method)
+    tt = [torch.tensor(v, requires_grad=True) for v in (delta, A, Bm, x)]
+    dA_ = tt[0].unsqueeze(-1) * tt[1]
+    Bx = tt[3].unsqueeze(-1) * tt[2].unsqueeze(2)
+    if method == "zoh":
+        a, b = torch.exp(dA_), torch.expm1(dA_) / tt[1] * Bx
+    elif method == "euler":
+        a, b = torch.exp(dA_), tt[0].unsqueeze(-1) * Bx
+    else:
+        a = (1 + dA_ / 2) / (1 - dA_ / 2)
+        b = tt[0].unsqueeze(-1) / (1 - dA_ / 2) * Bx
+    ((a * torch.tensor(ga)).sum() + (b * torch.tensor(gb)).sum()).backward()
+    for got, t in zip(ours, tt):
+        np.testing.assert_allclose(got, t.grad.numpy(), rtol=1e-9, atol=1e-12)
