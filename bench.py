@@ -75,6 +75,34 @@ def cpu_baseline_c1(t, budget_s=12.0):
                       f"{reps} reps in {dt:.1f} s"}
 
 
+def cpu_baseline_c2(L, budget_s=20.0):
+    """Time the reference CPU path's forward (oracle/cpu_chunked.fwd: SelectiveScanFn over
+    channel tiles of d_block = 2^24 // (L N), scan_chunked inside) at B1 D512 N16 on a bounded
+    sample: whole channel tiles, as many as fit the budget; the full forward is that time x
+    (number of tiles) / (tiles run), since the tiles are independent and equal."""
+    from oracle import cpu_chunked
+    from ssm_scan.synthetic import baseline_inputs
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    D, N = 512, 16
+    t = baseline_inputs(1, L, D, N)
+    tiles = cpu_chunked._blocks(1, L, D, N)
+    i, j = tiles[0]
+    args = [t[k][..., i:j].contiguous() for k in ("u", "delta")] + [t["A"][i:j]] + \
+        [t[k].contiguous() for k in ("Bm", "Cm")]
+    cpu_chunked.fwd(*args)                          # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while reps < 1 or (time.perf_counter() - t0 < budget_s and reps < len(tiles)):
+        cpu_chunked.fwd(*args)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    full_s = dt * len(tiles)
+    return {"value": L / full_s / 1e6, "unit": "Mtok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "seconds_full_forward": full_s,
+            "sample": f"config-2 forward B1 L{L} D512 N16 fp32 on the torch-CPU restatement of the reference "
+                      f"CPU path (SelectiveScanFn + scan_chunked, d_block {j - i}): {reps} of its {len(tiles)} "
+                      f"independent channel tiles timed ({dt:.2f} s each), scaled to all tiles"}
+
+
 def flush_buffer(dev):
     return torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
 
@@ -148,15 +176,17 @@ def bench_fwd(args, dev, B, L, dtype, workload):
     D, N = 512, 16
     t = baseline_inputs(B, L, D, N, dtype=dtype)
     ins = [t[k].to(dev) for k in ("u", "delta", "A", "Bm", "Cm")]
-    for _ in range(args.warmup):
+    def step():
         with torch.no_grad():
-            ssm_scan.selective_scan_hip(*ins)
+            return ssm_scan.selective_scan_fn(*ins, return_last_state=True, segments=args.segments)
+
+    for _ in range(args.warmup):
+        step()
     torch.cuda.synchronize()
     with ssm_scan.KernelTimer() as timer:
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            with torch.no_grad():
-                ssm_scan.selective_scan_hip(*ins)
+            step()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     fwd_ms = statistics.mean(timer.times_ms()["ssm_fwd"])
@@ -164,13 +194,20 @@ def bench_fwd(args, dev, B, L, dtype, workload):
     fb, _ = alg_bytes(B, L, D, N, s=s, gate=False, skip=False)
     ms = wall * 1e3 / args.steps
     achieved = fb / (fwd_ms * 1e-3) / 1e9
-    return {"metric": f"selective-scan fwd Mtok/s, {workload}", "value": B * L / (ms * 1e-3) / 1e6,
+    rec = {"metric": f"selective-scan fwd Mtok/s, {workload}", "value": B * L / (ms * 1e-3) / 1e6,
             "unit": "Mtok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": {torch.float32: "f32", torch.bfloat16: "bf16"}[dtype], "data": "synthetic",
             "config": {"workload": workload, "batch": B, "seqlen": L, "dim": D, "dstate": N},
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "ssm_fwd"}}
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "ssm_fwd",
+                         "alg_bytes_per_launch": fb},
+           "segments": args.segments or "auto"}
+    if L >= 4096 and not args.no_cpu_baseline:
+        cb = cpu_baseline_c2(L)
+        rec["cpu_baseline"] = cb
+        rec["gpu_time_frac_of_cpu"] = fwd_ms * 1e-3 / cb["seconds_full_forward"]
+    return rec
 
 
 def bench_copy(args, dev):
@@ -191,6 +228,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "copy"])
     ap.add_argument("--seqlen", type=int, default=131072)
+    ap.add_argument("--segments", type=int, default=0, help="forward time segments (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -73,7 +73,11 @@ typedef struct ssm_fwd_args {
   ssm_tensor z;            /* (B,L,D), optional gate */
   ssm_tensor delta_bias;   /* (D,) state type, optional */
   int32_t delta_softplus;  /* nonzero: delta' = softplus(delta + bias) */
-  int32_t reserved0;
+  int32_t segments;        /* time segments scanned in parallel: 0 = chosen by the library
+                              (more than 1 only when B x D alone cannot fill the GPU, e.g.
+                              one long sequence); the segment-end states are combined
+                              exactly like scan_chunked's chunk summaries
+                              (models/scan.py:158-164) and need ssm_fwd_workspace_bytes() */
   ssm_tensor h0;           /* (B,D,N) state type, optional initial state */
   ssm_tensor out;          /* (B,L,D) dtype, required */
   ssm_tensor last;         /* (B,D,N) state type, optional final state */

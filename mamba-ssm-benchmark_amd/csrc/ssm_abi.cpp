@@ -4,6 +4,7 @@
 // paths are testable on a CPU host), workspace sizing, the integer planning functions of the
 // reference, and dispatch to the kernel launchers.  No device memory is allocated and no
 // stream is synchronized.
+#include <algorithm>
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -138,6 +139,7 @@ int ssm_fwd_check(const ssm_fwd_args *a) {
   REQUIRE(a->Bm, "Bm");
   REQUIRE(a->Cm, "Cm");
   REQUIRE(a->out, "out");
+  if (a->segments < 0) return fail(SSM_EINVAL, "segments=%d must be >= 0", a->segments);
   return ok();
 }
 
@@ -147,15 +149,42 @@ int64_t ssm_fwd_saved_bytes(const ssm_fwd_args *a) {
   return f.ckpt_bytes + f.ypre_bytes;
 }
 
+// Time segments of the forward.  One unless the B x ceil(D / channels-per-wavefront)
+// wavefronts leave the GPU short of work (fewer than kSegEnough); then enough segments for
+// about kSegTarget wavefronts, each segment at least kSegMinChunks chunks long.  A positive
+// `requested` overrides the choice (clamped to the valid range).
+constexpr int64_t kSegEnough = 2048, kSegTarget = 4096, kSegMinChunks = 16;
+
+struct SegPlan {
+  int nseg, seg_chunks;
+  int64_t buf_bytes;  // one (B, nseg, D, NP) state-type buffer
+};
+
+static SegPlan seg_plan(const ssm_fwd_args *a, const FwdLayout &f) {
+  SegPlan s;
+  const int64_t waves = a->batch * cdiv(a->dim, 64 / f.np);
+  int64_t n = 1;
+  if (a->segments > 0) n = a->segments;
+  else if (waves < kSegEnough) n = std::min(cdiv(kSegTarget, waves), (int64_t)f.nchunks / kSegMinChunks);
+  n = std::max((int64_t)1, std::min(n, std::min((int64_t)f.nchunks, 65535 / a->batch)));
+  s.seg_chunks = (int)cdiv(f.nchunks, n);
+  s.nseg = (int)cdiv(f.nchunks, s.seg_chunks);
+  s.buf_bytes = s.nseg > 1 ? align256(a->batch * s.nseg * a->dim * f.np * state_size(a->dtype)) : 0;
+  return s;
+}
+
 int64_t ssm_fwd_workspace_bytes(const ssm_fwd_args *a) {
   if (ssm_fwd_check(a)) return -1;
-  return 0;
+  FwdLayout f = fwd_layout(a->batch, a->seqlen, a->dim, a->dstate, a->dtype, has(a->z));
+  return 3 * seg_plan(a, f).buf_bytes;
 }
 
 static void fill_fwd(FwdParams &p, const ssm_fwd_args *a, const FwdLayout &f) {
   memset(&p, 0, sizeof(p));
   p.B = a->batch; p.L = a->seqlen; p.D = a->dim; p.N = a->dstate;
   p.nchunks = f.nchunks;
+  p.nseg = 1;
+  p.seg_chunks = f.nchunks;
   p.softplus = a->delta_softplus != 0;
   p.has_D = has(a->Dskip); p.has_z = has(a->z); p.has_bias = has(a->delta_bias);
   p.has_h0 = has(a->h0); p.has_last = has(a->last); p.write_out = 1;
@@ -175,6 +204,17 @@ int ssm_fwd(const ssm_fwd_args *a, void *stream) {
   if (a->saved) {
     p.ckpt = a->saved;
     p.ypre = has(a->z) ? (char *)a->saved + f.ckpt_bytes : nullptr;
+  }
+  const SegPlan sp = seg_plan(a, f);
+  if (sp.nseg > 1) {
+    if (!a->workspace || a->workspace_bytes < 3 * sp.buf_bytes)
+      return fail(SSM_ESPACE, "workspace of %lld bytes is smaller than the %lld required",
+                  (long long)a->workspace_bytes, (long long)(3 * sp.buf_bytes));
+    p.nseg = sp.nseg;
+    p.seg_chunks = sp.seg_chunks;
+    p.seg_P = a->workspace;
+    p.seg_E = (char *)a->workspace + sp.buf_bytes;
+    p.seg_hin = (char *)a->workspace + 2 * sp.buf_bytes;
   }
   hipError_t e = launch_fwd(p, a->dtype, a->method, f.np, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "ssm_fwd launch");

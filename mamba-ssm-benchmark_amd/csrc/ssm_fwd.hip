@@ -18,6 +18,13 @@
 //   3. sums the partials over the NP states with (t, channel)-mapped lanes, applies the skip
 //      and gate and stores the outputs (coalesced); saves the chunk-end state, and the
 //      pre-gate output when there is a gate, if the backward needs them.
+//
+// Long sequences (few batch rows x channels, e.g. B1 D512 at L = 131072) are split into time
+// segments so that enough wavefronts exist: the two-level structure of scan_chunked
+// (models/scan.py:142-165) with segments in place of chunks.  A summary pass (SUM = true)
+// walks each segment from a zero state, skipping C and the outputs, and keeps the product of
+// its decays; a carry kernel scans the (product, end state) pairs per (b, d, n); the main pass
+// then restarts every segment from the state that enters it.
 #include "ssm_device.hpp"
 #include "ssm_internal.hpp"
 #include "ssm_tiles.hpp"
@@ -35,7 +42,7 @@ struct FwdWaveLds {
   CT y[CK][CW][NP];
 };
 
-template <typename IT, int NP, int METHOD, bool UL>
+template <typename IT, int NP, int METHOD, bool UL, bool SUM>
 __global__ void __launch_bounds__(kWave * fwd_waves(sizeof(typename Conv<IT>::CT), NP))
 k_fwd(const FwdParams p) {
   typedef typename Conv<IT>::CT CT;
@@ -49,7 +56,10 @@ k_fwd(const FwdParams p) {
   const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
   WL &S = lds_all[wv];
   const int c = lane / NP, n = lane % NP;
-  const int64_t b = blockIdx.y;
+  const int64_t b = blockIdx.y / p.nseg;
+  const int seg = (int)(blockIdx.y % p.nseg);
+  const int k0 = seg * p.seg_chunks;
+  const int k1 = k0 + p.seg_chunks < p.nchunks ? k0 + p.seg_chunks : p.nchunks;
   const int dw = (blockIdx.x * WPB + wv) * CW;  // first channel of this wavefront
   const int d = dw + c;
   const bool dval = d < p.D, nval = n < p.N;
@@ -58,8 +68,12 @@ k_fwd(const FwdParams p) {
   CT Av = (CT)-1;
   if (dval && nval) Av = vload<CT>(p.A, d * p.A.s0 + n * p.A.s1);
   const AConst<CT> ac = make_aconst(Av);
-  CT h = 0;
-  if (p.has_h0 && dval && nval) h = vload<CT>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
+  CT h = 0, prod = 1;
+  const int64_t sidx = ((b * p.nseg + seg) * p.D + d) * NP + n;  // (B, nseg, D, NP) summaries
+  if (!SUM && dval && nval) {
+    if (p.nseg > 1) h = ((const CT *)p.seg_hin)[sidx];
+    else if (p.has_h0) h = vload<CT>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
+  }
 
   const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = with_layout<UL>(p.z, p.x);
   const KView vout = with_layout<UL>(p.out, p.x), vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
@@ -67,31 +81,31 @@ k_fwd(const FwdParams p) {
   const bool ot = vout.s1 == 1;
   WaveTile<IT, CT, CK, CW, UL> tx, tdt;
   WaveTile<IT, CT, CK, NP, UL> tB, tC;
-  tx.load(vx, b, 0, L, dw, D, xt, lane);
-  tdt.load(vdt, b, 0, L, dw, D, dtt, lane);
-  tB.load(vB, b, 0, L, 0, N, bt, lane);
-  tC.load(vC, b, 0, L, 0, N, ctt, lane);
+  tx.load(vx, b, k0 * CK, L, dw, D, xt, lane);
+  tdt.load(vdt, b, k0 * CK, L, dw, D, dtt, lane);
+  tB.load(vB, b, k0 * CK, L, 0, N, bt, lane);
+  if (!SUM) tC.load(vC, b, k0 * CK, L, 0, N, ctt, lane);
 
-  for (int k = 0; k < p.nchunks; ++k) {
+  for (int k = k0; k < k1; ++k) {
     const int t0 = k * CK;
     tx.store(S.x, xt, lane);
     store_delta_w<IT, CT, CK, CW, WL::CKP, UL>(tdt, S.dt, nullptr, dtt, lane, p.has_bias, p.softplus, p.bias, dw, D,
                                             t0, L);
     tB.store(S.B, bt, lane);
-    tC.store(S.C, ctt, lane);
+    if (!SUM) tC.store(S.C, ctt, lane);
     wave_lds_sync();
-    if (k + 1 < p.nchunks) {  // next chunk's global reads overlap this chunk's compute
+    if (k + 1 < k1) {  // next chunk's global reads overlap this chunk's compute
       tx.load(vx, b, t0 + CK, L, dw, D, xt, lane);
       tdt.load(vdt, b, t0 + CK, L, dw, D, dtt, lane);
       tB.load(vB, b, t0 + CK, L, 0, N, bt, lane);
-      tC.load(vC, b, t0 + CK, L, 0, N, ctt, lane);
+      if (!SUM) tC.load(vC, b, t0 + CK, L, 0, N, ctt, lane);
     }
 
     CT rdt[RB], rx[RB], rB[RB], rC[RB];
     lds_row(&S.dt[c][0], rdt);
     lds_row(&S.x[c][0], rx);
     lds_row(&S.B[n][0], rB);
-    lds_row(&S.C[n][0], rC);
+    if (!SUM) lds_row(&S.C[n][0], rC);
 #pragma unroll
     for (int q = 0; q < CK / RB; ++q) {
       CT ndt[RB], nx[RB], nB[RB], nC[RB];
@@ -99,7 +113,7 @@ k_fwd(const FwdParams p) {
         lds_row(&S.dt[c][(q + 1) * RB], ndt);
         lds_row(&S.x[c][(q + 1) * RB], nx);
         lds_row(&S.B[n][(q + 1) * RB], nB);
-        lds_row(&S.C[n][(q + 1) * RB], nC);
+        if (!SUM) lds_row(&S.C[n][(q + 1) * RB], nC);
       }
       // ZOH keeps a - 1 (accurate expm1) and updates h <- h + (a - 1) h + b, which keeps the
       // decay's relative accuracy for slowly decaying states (a close to 1).
@@ -115,7 +129,12 @@ k_fwd(const FwdParams p) {
       for (int tt = 0; tt < RB; ++tt) {
         if constexpr (METHOD == 0) h = fma(a[tt], h, h + bx[tt]);
         else h = fma(a[tt], h, bx[tt]);
-        S.y[q * RB + tt][c][n] = rC[tt] * h;
+        if constexpr (SUM) {  // padded steps (t >= L) have delta 0, i.e. a = 1, b = 0
+          if constexpr (METHOD == 0) prod = fma(a[tt], prod, prod);
+          else prod *= a[tt];
+        } else {
+          S.y[q * RB + tt][c][n] = rC[tt] * h;
+        }
       }
       if (q + 1 < CK / RB) {
 #pragma unroll
@@ -123,9 +142,13 @@ k_fwd(const FwdParams p) {
           rdt[j] = ndt[j];
           rx[j] = nx[j];
           rB[j] = nB[j];
-          rC[j] = nC[j];
+          if (!SUM) rC[j] = nC[j];
         }
       }
+    }
+    if constexpr (SUM) {
+      wave_lds_sync();
+      continue;
     }
     if (p.ckpt && dval)
       ((CT *)p.ckpt)[((b * p.nchunks + k) * p.D + d) * NP + n] = h;
@@ -158,8 +181,31 @@ k_fwd(const FwdParams p) {
     wave_lds_sync();
   }
 
-  if (p.has_last && dval && nval)
+  if constexpr (SUM) {
+    if (dval && nval) {
+      ((CT *)p.seg_P)[sidx] = prod;
+      ((CT *)p.seg_E)[sidx] = h;
+    }
+  } else if (p.has_last && dval && nval && seg == p.nseg - 1) {
     vstore<CT>(p.last, b * p.last.s0 + d * p.last.s1 + n * p.last.s2, h);
+  }
+}
+
+// State entering each time segment: h_in[0] = h0 (or 0), h_in[s+1] = P[s] h_in[s] + E[s],
+// one lane per (b, d, n), segments in order (models/scan.py:160-164 over segments).
+template <typename CT, int NP>
+__global__ void __launch_bounds__(kThreads) k_fwd_carry(const FwdParams p) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= p.B * p.D * NP) return;
+  const int n = (int)(i % NP);
+  const int64_t d = (i / NP) % p.D, b = i / (NP * p.D);
+  if (n >= p.N) return;
+  CT h = p.has_h0 ? vload<CT>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2) : (CT)0;
+  for (int s = 0; s < p.nseg; ++s) {
+    const int64_t k = ((b * p.nseg + s) * p.D + d) * NP + n;
+    ((CT *)p.seg_hin)[k] = h;
+    h = fma(((const CT *)p.seg_P)[k], h, ((const CT *)p.seg_E)[k]);
+  }
 }
 
 template <typename IT, int NP, int M>
@@ -167,9 +213,16 @@ static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
   typedef typename Conv<IT>::CT CT;
   constexpr int WPB = fwd_waves(sizeof(CT), NP);
   constexpr int DT = WPB * (kWave / NP);
-  dim3 grid((unsigned)((p.D + DT - 1) / DT), (unsigned)p.B);
-  if (p.uniform) hipLaunchKernelGGL((k_fwd<IT, NP, M, true>), grid, dim3(WPB * kWave), 0, s, p);
-  else hipLaunchKernelGGL((k_fwd<IT, NP, M, false>), grid, dim3(WPB * kWave), 0, s, p);
+  dim3 grid((unsigned)((p.D + DT - 1) / DT), (unsigned)(p.B * p.nseg));
+  if (p.nseg > 1) {
+    if (p.uniform) hipLaunchKernelGGL((k_fwd<IT, NP, M, true, true>), grid, dim3(WPB * kWave), 0, s, p);
+    else hipLaunchKernelGGL((k_fwd<IT, NP, M, false, true>), grid, dim3(WPB * kWave), 0, s, p);
+    const int64_t lanes = p.B * p.D * NP;
+    hipLaunchKernelGGL((k_fwd_carry<CT, NP>), dim3((unsigned)((lanes + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                       s, p);
+  }
+  if (p.uniform) hipLaunchKernelGGL((k_fwd<IT, NP, M, true, false>), grid, dim3(WPB * kWave), 0, s, p);
+  else hipLaunchKernelGGL((k_fwd<IT, NP, M, false, false>), grid, dim3(WPB * kWave), 0, s, p);
   return hipGetLastError();
 }
 

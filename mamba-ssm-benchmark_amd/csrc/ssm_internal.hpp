@@ -33,9 +33,15 @@ __host__ __device__ constexpr int bwd_shared_bytes(int s, int np, int wpb) {
 __host__ __device__ constexpr int fwd_waves(int s, int np) {
   return 4 * fwd_wave_bytes(s, np) <= 65536 ? 4 : 2 * fwd_wave_bytes(s, np) <= 65536 ? 2 : 1;
 }
+// gfx950 gives a workgroup up to 160 KiB of LDS.  The backward uses as many wavefronts per
+// workgroup as fit (up to 8): every extra wavefront widens the channel tile over which dB and
+// dC are summed in LDS, and so shrinks the partial sums written to HBM by that factor.
+constexpr int kLdsBytes = 160 * 1024;
+__host__ __device__ constexpr int bwd_fits(int s, int np, int w) {
+  return w * bwd_wave_bytes(s, np) + bwd_shared_bytes(s, np, w) <= kLdsBytes;
+}
 __host__ __device__ constexpr int bwd_waves(int s, int np) {
-  return 4 * bwd_wave_bytes(s, np) + bwd_shared_bytes(s, np, 4) <= 65536 ? 4
-       : 2 * bwd_wave_bytes(s, np) + bwd_shared_bytes(s, np, 2) <= 65536 ? 2 : 1;
+  return bwd_fits(s, np, 8) ? 8 : bwd_fits(s, np, 4) ? 4 : bwd_fits(s, np, 2) ? 2 : 1;
 }
 // Channels per backward workgroup (= the channel tile of the dB / dC partial sums).
 inline int bwd_channels_per_block(int dtype, int np) {
@@ -49,6 +55,12 @@ struct FwdParams {
   int softplus;
   int has_D, has_z, has_bias, has_h0, has_last, write_out;
   int uniform;  // all (B,L,D) views share x's strides, C shares B's, row offsets fit in int32
+  // Time segments: grid row blockIdx.y = b * nseg + segment; a segment spans seg_chunks chunks.
+  // With nseg > 1 a summary pass writes each segment's decay product and zero-start end state
+  // (seg_P, seg_E), a carry pass turns them into the state entering each segment (seg_hin),
+  // and the main pass starts every segment from seg_hin.  All three are (B, nseg, D, NP).
+  int nseg, seg_chunks;
+  void *seg_P, *seg_E, *seg_hin;
   KView x, dt, A, Bm, Cm, Dsk, z, bias, h0, out, last;
   void *ckpt;  // (B, nchunks, D, NP) state type: state at the end of each chunk
   void *ypre;  // y + D x before the gate (iff gate and saving), state type; laid out
@@ -120,6 +132,7 @@ struct DiscParams {
   void *ws_dA;  // (ngroups, D, N) partial sums over each group of rows
 };
 
+// Runs the summary and carry passes first when p.nseg > 1.
 hipError_t launch_fwd(const FwdParams &p, int dtype, int method, int np, hipStream_t s);
 hipError_t launch_bwd(const BwdParams &p, int dtype, int method, int np, hipStream_t s);
 hipError_t launch_bwd_finalize(const FinParams &p, int dtype, hipStream_t s);

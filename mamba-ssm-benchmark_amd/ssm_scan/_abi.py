@@ -33,7 +33,7 @@ class FwdArgs(ctypes.Structure):
                 ("method", c_i32), ("dtype", c_i32),
                 ("x", Tensor), ("delta", Tensor), ("A", Tensor), ("Bm", Tensor), ("Cm", Tensor),
                 ("Dskip", Tensor), ("z", Tensor), ("delta_bias", Tensor),
-                ("delta_softplus", c_i32), ("reserved0", c_i32),
+                ("delta_softplus", c_i32), ("segments", c_i32),
                 ("h0", Tensor), ("out", Tensor), ("last", Tensor),
                 ("saved", c_vp), ("workspace", c_vp), ("workspace_bytes", c_i64)]
 

@@ -97,7 +97,7 @@ class FusedSelectiveScanFn(torch.autograd.Function):
     """out, last = fused scan; gradients for x, delta, A, Bm, Cm, D, z, delta_bias, h0."""
 
     @staticmethod
-    def forward(ctx, x, delta, A, Bm, Cm, D, z, delta_bias, h0, method, delta_softplus):
+    def forward(ctx, x, delta, A, Bm, Cm, D, z, delta_bias, h0, method, delta_softplus, segments=0):
         io, ct = _dtypes(x, (delta, Bm, Cm, z))
         xs, ds, Bs, Cs, zs = (_cast_keep(t, io) for t in (x, delta, Bm, Cm, z))
         As, Dv, bv, h0v = (_cast_keep(t, ct) for t in (A, D, delta_bias, h0))
@@ -109,7 +109,14 @@ class FusedSelectiveScanFn(torch.autograd.Function):
         args = _abi.FwdArgs()
         _fill_common(args, xs, ds, As, Bs, Cs, Dv, zs, bv, delta_softplus, h0v, method, io)
         args.out, args.last = _abi.view(out), _abi.view(last)
+        args.segments = int(segments or 0)
         lib = _abi.lib()
+        wbytes = lib.ssm_fwd_workspace_bytes(ctypes.byref(args))
+        if wbytes < 0:
+            _abi.check(lib.ssm_fwd_check(ctypes.byref(args)), "ssm_fwd")
+        ws = torch.empty(wbytes, dtype=torch.uint8, device=dev) if wbytes else None
+        if ws is not None:
+            args.workspace, args.workspace_bytes = ws.data_ptr(), wbytes
         need_bwd = any(ctx.needs_input_grad[:9])
         saved = None
         if need_bwd:
@@ -171,21 +178,23 @@ class FusedSelectiveScanFn(torch.autograd.Function):
         out = []
         for g, dt in zip(grads, ctx.in_dtypes):
             out.append(None if g is None or dt is None else _cast_keep(g, dt))
-        return (*out, None, None)
+        return (*out, None, None, None)
 
 
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                      h0=None, method="zoh", return_last_state=False):
+                      h0=None, method="zoh", return_last_state=False, segments=None):
     """out = (scan(u, delta', A, B, C) + D u) * silu(z), delta' = softplus(delta + bias).
 
     Logical layouts as the reference: u, delta, z (B, L, D); A (D, N); B, C (B, L, N);
-    h0 (B, D, N).  Pass ``x.transpose(1, 2)`` for channel-major (B, D, L) storage."""
+    h0 (B, D, N).  Pass ``x.transpose(1, 2)`` for channel-major (B, D, L) storage.
+    ``segments`` forces the number of time segments the forward scans in parallel (default:
+    chosen by the engine; more than one only when B x D is too small to fill the GPU)."""
     if method not in METHODS:
         raise ValueError(f"unknown discretization {method!r}")
     _require_gpu(u, delta, A, B, C, D, z, delta_bias, h0)
     _check_shapes(u, delta, A, B, C, D, z, delta_bias, h0)
     out, last = FusedSelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, h0, METHODS[method],
-                                           bool(delta_softplus))
+                                           bool(delta_softplus), segments or 0)
     return (out, last) if return_last_state else out
 
 

@@ -1,0 +1,91 @@
+"""Long-sequence forward (time segments) against the float64 oracle.
+
+When B x D alone cannot fill the GPU the fused forward splits time into segments (summary
+pass, carry over segment summaries, main pass) -- the structure of scan_chunked
+(models/scan.py:142-165) lifted to segments.  Checked here:
+  * forced segment counts (incl. ragged last segments) at small shapes, forward and the
+    backward that consumes the segmented forward's saved chunk states, all methods;
+  * the automatic choice at B1 D64 L8192;
+  * BASELINE config 2 at its largest length, B1 L131072 D512 N16, float32 and bf16
+    (rtol 1e-4 / atol 1e-5 float32; 2e-2 bf16), against the C fp64 oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import ssm_scan
+from oracle import c_oracle
+from ssm_inputs import baseline_inputs, np64, triton_test_inputs
+from test_gpu_fused import ATOL, ATOL_BF16, RTOL, RTOL_BF16, check_all, close, oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def run_seg(ins, dev, method, segments, D=None, z=None, bias=None, softplus=False, dout=None, dlast=None):
+    x, delta, A, Bm, Cm, h0 = ins
+    names = ["dx", "ddelta", "dA", "dB", "dC", "dD", "dz", "ddelta_bias", "dh0"]
+    gl = [None if t is None else t.to(dev).requires_grad_() for t in (x, delta, A, Bm, Cm, D, z, bias, h0)]
+    out, last = ssm_scan.selective_scan_fn(gl[0], gl[1], gl[2], gl[3], gl[4], D=gl[5], z=gl[6],
+                                           delta_bias=gl[7], delta_softplus=softplus, h0=gl[8],
+                                           method=method, return_last_state=True, segments=segments)
+    loss = (out * dout.to(dev)).sum()
+    if dlast is not None:
+        loss = loss + (last * dlast.to(dev)).sum()
+    loss.backward()
+    return out.detach(), last.detach(), {n: t.grad for n, t in zip(names, gl) if t is not None}
+
+
+@pytest.mark.parametrize("method", ["zoh", "euler", "bilinear"])
+@pytest.mark.parametrize("segments", [2, 3, 5, 100])
+def test_forced_segments_match_oracle(dev, method, segments):
+    B, L, D, N = 2, 100, 40, 16             # 7 chunks of 16 steps: ragged last segment
+    ins = triton_test_inputs(B, L, D, N, True, seed=segments)
+    g = torch.Generator().manual_seed(segments + 1)
+    dout = torch.randn(B, L, D, generator=g)
+    dlast = torch.randn(B, D, N, generator=g)
+    got = run_seg(ins, dev, method, segments, dout=dout, dlast=dlast)
+    ref = oracle(ins, method, dout=dout, dlast=dlast)
+    check_all(got, ref)
+
+
+def test_forced_segments_with_gate_bias_softplus(dev):
+    B, L, D, N = 2, 150, 24, 8
+    ins = triton_test_inputs(B, L, D, N, True, seed=21)
+    g = torch.Generator().manual_seed(22)
+    Dv, z = torch.randn(D, generator=g), torch.randn(B, L, D, generator=g)
+    bias = torch.randn(D, generator=g) * 0.5 - 3.0
+    ins = (ins[0], torch.randn(B, L, D, generator=g) * 0.5, *ins[2:])
+    dout = torch.randn(B, L, D, generator=g)
+    got = run_seg(ins, dev, "zoh", 4, D=Dv, z=z, bias=bias, softplus=True, dout=dout)
+    ref = oracle(ins, "zoh", D=Dv, z=z, bias=bias, softplus=True, dout=dout)
+    check_all(got, ref)
+
+
+def test_automatic_segments_long_sequence(dev):
+    t = baseline_inputs(1, 8192, 64, 16)
+    ins = [t[k].to(dev) for k in ("u", "delta", "A", "Bm", "Cm")]
+    h0 = torch.randn(1, 64, 16, generator=torch.Generator().manual_seed(3))
+    with torch.no_grad():
+        y, last = ssm_scan.selective_scan_hip(*ins, h0=h0.to(dev))
+    ry, _, rlast = c_oracle.fwd(*(np64(v) for v in ins), np64(h0))
+    close(y, ry, name="y")
+    close(last, rlast, name="last")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_config2_longest_forward_matches_c_oracle(dev, dtype):
+    """BASELINE config 2 at L = 131072 (B1 D512 N16), forward only."""
+    t = baseline_inputs(1, 131072, 512, 16, dtype=dtype)
+    ins = [t[k].to(dev) for k in ("u", "delta", "A", "Bm", "Cm")]
+    with torch.no_grad():
+        y, last = ssm_scan.selective_scan_hip(*ins)
+    torch.cuda.synchronize()
+    assert y.dtype == dtype and last.dtype == torch.float32
+    ry, _, rlast = c_oracle.fwd(*(np64(v) for v in ins))
+    rtol, atol = (RTOL, ATOL) if dtype == torch.float32 else (RTOL_BF16, ATOL_BF16)
+    close(y, ry, rtol, atol, "y")
+    close(last, rlast, rtol, atol, "last")
+    if dtype == torch.float32:   # the unscaled bound holds for all but 1 ppm of elements
+        bad = np.abs(np64(y) - ry) > ATOL + RTOL * np.abs(ry)
+        assert bad.sum() <= max(1, bad.size // 1_000_000), int(bad.sum())
