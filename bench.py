@@ -4,7 +4,10 @@
 Metric: selective-scan fwd+bwd Mtok/s and % HBM peak at B16 L512 D512 N16
 fp32 (config 1: z gate + D skip, upstream grad dy ~ N(0,1)).  A step is one forward and one
 backward of the fused scan over the batch, inputs resident in HBM.  W untimed warmup steps,
-then exactly K steps between two torch.cuda.synchronize() calls.
+then exactly K steps between two torch.cuda.synchronize() calls, eager (Python + autograd
+launch every step; the kernels' HIP-event timer is off in the timed loop).  With --graph the
+step is captured once in a HIP graph and replayed instead (its outputs are checked bitwise
+against the eager step's); both times are reported.
 
 Per-entry device times come from HIP events recorded on the launch stream around every
 C-ABI call (ssm_scan.KernelTimer); the dominant entry (ssm_bwd: the backward kernel plus its
@@ -122,16 +125,40 @@ def bench_c1(args, dev):
         return torch.autograd.grad(out, leaves, dy)
 
     for _ in range(args.warmup):
+        ref = step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()                 # eager: Python + autograd launch every step
+    for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
-    with ssm_scan.KernelTimer() as timer:
+    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    ms_step, graph_ok = eager_ms, None
+    if args.graph:
+        # the same step captured once in a HIP graph and replayed: no host work per step
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            gout = step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        graph_ok = all(torch.equal(a, b) for a, b in zip(gout, ref))   # deterministic kernels
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            step()
+            graph.replay()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
+        ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    with ssm_scan.KernelTimer() as timer:
+        for _ in range(args.steps):
+            step()
     times = timer.times_ms()
-    ms_step = wall * 1e3 / args.steps
     fwd_ms = statistics.mean(times["ssm_fwd"])
     bwd_ms = statistics.mean(times["ssm_bwd"])
     fb, bb = alg_bytes(B, L, D, N)
@@ -159,6 +186,8 @@ def bench_c1(args, dev):
                                "zoh, z gate + D skip, channel-major (B,D,L) storage",
                    "batch": B, "seqlen": L, "dim": D, "dstate": N, "method": "zoh"},
         "hbm_frac_step": (fb + bb) / (ms_step * 1e-3) / (HBM_PEAK_GBS * 1e9),
+        "step_mode": "hip-graph replay of the fwd+bwd step" if args.graph else "eager",
+        "eager_ms_per_step": eager_ms, "graph_matches_eager": graph_ok,
         "kernels_ms": {"ssm_fwd": fwd_ms, "ssm_bwd": bwd_ms, "ssm_fwd_cold": cold_f, "ssm_bwd_cold": cold_b},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic("ssm_bwd_c1"),
@@ -230,6 +259,7 @@ def main():
     ap.add_argument("--seqlen", type=int, default=131072)
     ap.add_argument("--segments", type=int, default=0, help="forward time segments (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true", help="time HIP-graph replays of the step")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): the hot path here is the "

@@ -87,7 +87,12 @@ k_bwd(const BwdParams p) {
   CT a_next = M1 ? (CT)0 : (CT)1;  // a (or a - 1 for ZOH) of the step after the current one
   CT h0v = 0;
   if (p.has_h0 && dval && nval) h0v = vload<CT>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
-  CT dA_acc = 0;
+  // dA = sum_t [ dL/da_t * da_t/dA + dL/db_t * db_t/dA ].  With w_t = lambda_t da_t/dz:
+  //   zoh       dt w h_{t-1} + (lambda Bx) (dt a - coef) / A     (dt^2 f(z) = (dt a - coef) / A)
+  //   euler     dt w h_{t-1}
+  //   bilinear  dt w (h_{t-1} + dt Bx / 2)                     (db/dA = dt^2 u^2 / 2 Bx)
+  // dA_acc holds the first sum, dA2_acc the zoh second sum before its 1/A factor.
+  CT dA_acc = 0, dA2_acc = 0;
   CT dD_acc = 0, db_acc = 0;  // lanes < CW: channel dw + lane
 
   const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = with_layout<UL>(p.z, p.x);
@@ -191,20 +196,29 @@ k_bwd(const BwdParams p) {
           const CT dtv = rdt[tt], xv = rx[tt], dyv = rdy[tt], Bv = rB[tt], Cv = rC[tt];
           if constexpr (M1) dh64 = fma(dh64, (double)a_next, dh64 + (double)(dyv * Cv));
           else dh64 = fma(dh64, (double)a_next, (double)(dyv * Cv));
-          const CT dh = (CT)dh64;
+          const CT lam = (CT)dh64;
           a_next = aa[t];
-          const CT at = M1 ? (CT)1 + aa[t] : aa[t];
+          const CT hp = hh[t], Bx = Bv * xv;
           const CT pC = dyv * hh[t + 1];
-          const CT da = dh * hh[t];
-          const CT dhc = dh * bcoef<METHOD>(dtv, cc_[t]);
+          const CT dhc = lam * bcoef<METHOD>(dtv, cc_[t]);
           const CT px = dhc * Bv;
           const CT pB = dhc * xv;
-          const CT dhBx = dh * (Bv * xv);
-          CT dadz, dbdd, d2f;
-          dfactors<METHOD>(dtv, ac, at, cc_[t], dadz, dbdd, d2f);
-          const CT g1 = da * dadz;
-          const CT pD = fma(g1, ac.A, dhBx * dbdd);
-          dA_acc = fma(dtv, g1, fma(dhBx, d2f, dA_acc));
+          // ddelta_t per state = lambda (da/dz A h_{t-1} + db/ddelta / (B x) B x)
+          CT pD;
+          if constexpr (METHOD == 0) {  // da/dz = db/ddelta-factor = a = 1 + am1
+            const CT w = fma(lam, aa[t], lam);
+            pD = w * fma(ac.A, hp, Bx);
+            dA_acc = fma(dtv * w, hp, dA_acc);
+            dA2_acc = fma(lam * Bx, fma(dtv, aa[t], dtv - cc_[t]), dA2_acc);
+          } else if constexpr (METHOD == 1) {  // da/dz = a, db/ddelta-factor = 1
+            const CT w = lam * aa[t];
+            pD = fma(w * ac.A, hp, lam * Bx);
+            dA_acc = fma(dtv * w, hp, dA_acc);
+          } else {  // both factors u^2 with u = 1 / (1 - z/2), held in cc_
+            const CT w = lam * (cc_[t] * cc_[t]);
+            pD = w * fma(ac.A, hp, Bx);
+            dA_acc = fma(dtv * w, fma((CT)0.5 * dtv, Bx, hp), dA_acc);
+          }
           S.pn[slot][c][n][0] = px;
           S.pn[slot][c][n][1] = pD;
           S.pd[slot][c][n][0] = pB;
@@ -304,7 +318,7 @@ k_bwd(const BwdParams p) {
     wave_lds_sync();
   }
 
-  if (dval) ((CT *)p.ws_dA)[(b * p.D + d) * NP + n] = dA_acc;
+  if (dval) ((CT *)p.ws_dA)[(b * p.D + d) * NP + n] = METHOD == 0 ? fma(dA2_acc, ac.invA, dA_acc) : dA_acc;
   if (p.has_dh0 && dval && nval)
     vstore<CT>(p.dh0, b * p.dh0.s0 + d * p.dh0.s1 + n * p.dh0.s2,
                (CT)(M1 ? fma(dh64, (double)a_next, dh64) : dh64 * (double)a_next));
