@@ -102,52 +102,85 @@ k_bwd(const BwdParams p) {
   const bool xt = vx.s1 == 1, dtt = vdt.s1 == 1, bt = vB.s1 == 1, ctt = vC.s1 == 1;
   const bool gt = vg.s1 == 1, dxt = vdx.s1 == 1, ddtt = vddt.s1 == 1;
   const CT *ypre = (const CT *)p.ypre;
+  CT biasv[WaveTile<IT, CT, CK, CW, UL>::E], dskv[WaveTile<IT, CT, CK, CW, UL>::E];
+  tile_bias<CT, CK, CW>(biasv, p.has_bias, p.bias, dw, D, dtt, lane);
+  tile_bias<CT, CK, CW>(dskv, p.has_D, p.Dsk, dw, D, dxt, lane);  // D skip in the dx store mapping
 
-  for (int k = p.nchunks - 1; k >= 0; --k) {
-    const int t0 = k * CK;
+  // Global reads run two chunks ahead (chunks are walked from the last to the first): tiles
+  // ping-pong between two register sets, each refilled as soon as its chunk is staged in LDS.
+  // Every load is unconditional (clamped addresses), so waiting for one chunk's tiles leaves
+  // the prefetches and earlier stores in flight.  A chunk k < 0 is inert (all inputs zero, no
+  // stores): chunks always run in pairs, and the loop is entered with the same memory traffic
+  // in flight as on its back edge.  In an inert chunk the adjoint first takes the step to
+  // a_0 dh_0 and then stays, which is what the dh0 epilogue expects.
+  constexpr int E1 = WaveTile<IT, CT, CK, CW, UL>::E;
+  struct Tiles {
+    WaveTile<IT, CT, CK, CW, UL> x, dt, g, z;
+    WaveTile<IT, CT, CK, NP, UL> B, C;
+    CT yp[E1];
+    CT ck;
+  };
+  const KView vzl = p.has_z ? vz : vx;
+  const int dc = dval ? d : 0;
+  auto load = [&](Tiles &T, int k) {
+    const int kc = k < 0 ? 0 : k;
+    const int t0 = kc * CK;
+    T.x.load(vx, b, t0, L, dw, D, xt, lane);
+    T.dt.load(vdt, b, t0, L, dw, D, dtt, lane);
+    T.g.load(vg, b, t0, L, dw, D, gt, lane);
+    T.z.load(vzl, b, t0, L, dw, D, gt, lane);
+    T.B.load(vB, b, t0, L, 0, N, bt, lane);
+    T.C.load(vC, b, t0, L, 0, N, ctt, lane);
+    if (p.has_z) {
+#pragma unroll
+      for (int i = 0; i < E1; ++i) {
+        int t, cc;
+        tc_of<CK, CW>(lane + i * kWave, gt, t, cc);
+        T.yp[i] = ypre[ypre_index(!xt, b, min(t0 + t, L - 1), min(dw + cc, D - 1), p.L, p.D)];
+      }
+    }
+    T.ck = ((const CT *)p.ckpt)[((b * p.nchunks + (kc > 0 ? kc - 1 : 0)) * p.D + dc) * NP + n];
+  };
+
+  auto chunk = [&](Tiles &T, int k) {
+    const bool live = k >= 0;
+    const int t0 = live ? k * CK : 0;
+    const int Lc = live ? L : 0;  // time bound of this chunk's elements (0: inert)
     const int buf = k & 1;
     // ---------------------------------------------------------------- stage
     {
-      WaveTile<IT, CT, CK, CW, UL> tx, tdt;
-      WaveTile<IT, CT, CK, NP, UL> tB, tC;
-      tx.load(vx, b, t0, L, dw, D, xt, lane);
-      tdt.load(vdt, b, t0, L, dw, D, dtt, lane);
-      tB.load(vB, b, t0, L, 0, N, bt, lane);
-      tC.load(vC, b, t0, L, 0, N, ctt, lane);
-      tx.store(S.x, xt, lane);
-      store_delta_w<IT, CT, CK, CW, WL::CKP, UL>(tdt, S.dt, S.sg, dtt, lane, p.has_bias, p.softplus, p.bias, dw, D,
-                                              t0, L);
-      tB.store(S.B, bt, lane);
-      tC.store(S.C, ctt, lane);
+      T.x.store(S.x, xt, lane, t0, Lc, dw, D);
+      store_delta_w<IT, CT, CK, CW, WL::CKP, UL>(T.dt, S.dt, S.sg, dtt, lane, p.softplus, biasv, dw, D, t0, Lc);
+      T.B.store(S.B, bt, lane, t0, Lc, 0, N);
+      T.C.store(S.C, ctt, lane, t0, Lc, 0, N);
       // dy = dout * silu(z); dz = dout * (y + D x) * silu'(z), from the saved pre-gate output
 #pragma unroll
-      for (int i = 0; i < (CK * CW + kWave - 1) / kWave; ++i) {
+      for (int i = 0; i < E1; ++i) {
         const int e = lane + i * kWave;
         if (e >= CK * CW) break;
         int t, cc;
         tc_of<CK, CW>(e, gt, t, cc);
         const int tg = t0 + t, dd = dw + cc;
         CT g = 0;
-        if (tg < L && dd < D) {
-          g = Conv<IT>::load(vp<IT>(vg) + b * vg.s0 + row_off<UL>(tg, dd, vg.s1, vg.s2));
+        if (tg < Lc && dd < D) {
+          g = T.g.v[i];
           if (p.has_z) {
-            const CT zv = Conv<IT>::load(vp<IT>(vz) + b * vz.s0 + row_off<UL>(tg, dd, vz.s1, vz.s2));
+            const CT zv = T.z.v[i];
             const CT sgz = sigmoid_ct<CT>(zv);
-            const CT yp = ypre[ypre_index(!xt, b, tg, dd, p.L, p.D)];
             Conv<IT>::store(vpw<IT>(vdz) + b * vdz.s0 + row_off<UL>(tg, dd, vdz.s1, vdz.s2),
-                            g * yp * sgz * ((CT)1 + zv * ((CT)1 - sgz)));
+                            g * T.yp[i] * sgz * ((CT)1 + zv * ((CT)1 - sgz)));
             g = g * zv * sgz;
           }
         }
         S.dy[cc][t] = g;
       }
     }
+    CT hh[CK + 1], aa[CK], cc_[CK];
+    hh[0] = k <= 0 ? h0v : T.ck;
     wave_lds_sync();
+    load(T, k - 2);
 
     // ---------------------------------------------------------------- recompute states
-    CT hh[CK + 1], aa[CK], cc_[CK];
-    if (k == 0) hh[0] = h0v;
-    else hh[0] = dval ? ((const CT *)p.ckpt)[((b * p.nchunks + (k - 1)) * p.D + d) * NP + n] : (CT)0;
     {
       CT rdt[RB], rx[RB], rB[RB];
       lds_row(&S.dt[c][0], rdt);
@@ -260,7 +293,7 @@ k_bwd(const BwdParams p) {
           sh.dbc[buf][wv][t][nn][0] = sb;
           sh.dbc[buf][wv][t][nn][1] = sc;
         } else {
-          if (t0 + t < L) {
+          if (t0 + t < Lc) {
             const int64_t off = ((b * p.ntiles + tile) * p.L + t0 + t) * NP + nn;
             ((CT *)p.ws_dB)[off] = sb;
             ((CT *)p.ws_dC)[off] = sc;
@@ -278,9 +311,9 @@ k_bwd(const BwdParams p) {
       int t, cc;
       tc_of<CK, CW>(e, dxt, t, cc);
       const int tg = t0 + t, dd = dw + cc;
-      if (tg >= L || dd >= D) continue;
+      if (tg >= Lc || dd >= D) continue;
       CT gx = S.gx[cc][t];
-      if (p.has_D) gx += S.dy[cc][t] * vload<CT>(p.Dsk, dd * p.Dsk.s0);
+      if (p.has_D) gx += S.dy[cc][t] * dskv[i];
       Conv<IT>::store(vpw<IT>(vdx) + b * vdx.s0 + row_off<UL>(tg, dd, vdx.s1, vdx.s2), gx);
     }
 #pragma unroll
@@ -290,24 +323,24 @@ k_bwd(const BwdParams p) {
       int t, cc;
       tc_of<CK, CW>(e, ddtt, t, cc);
       const int tg = t0 + t, dd = dw + cc;
-      if (tg >= L || dd >= D) continue;
+      if (tg >= Lc || dd >= D) continue;
       Conv<IT>::store(vpw<IT>(vddt) + b * vddt.s0 + row_off<UL>(tg, dd, vddt.s1, vddt.s2),
                       S.gd[cc][t] * S.sg[cc][t]);
     }
     if (lane < CW) {
 #pragma unroll
       for (int t = 0; t < CK; ++t) {
-        if (t0 + t < L) {
+        if (t0 + t < Lc) {
           dD_acc = fma(S.dy[lane][t], S.x[lane][t], dD_acc);
           db_acc = fma(S.gd[lane][t], S.sg[lane][t], db_acc);
         }
       }
     }
     if constexpr (WPB > 1) {
-      __syncthreads();  // every wavefront's (dB, dC) sums of this chunk are in sh.dbc[buf]
+      lds_barrier();  // every wavefront's (dB, dC) sums of this chunk are in sh.dbc[buf]
       for (int e = tid; e < CK * NP * 2; e += NT) {
         const int q = e % 2, nn = (e / 2) % NP, t = e / (2 * NP);
-        if (t0 + t >= L) continue;
+        if (t0 + t >= Lc) continue;
         CT v = 0;
 #pragma unroll
         for (int w = 0; w < WPB; ++w) v += sh.dbc[buf][w][t][nn][q];
@@ -316,6 +349,17 @@ k_bwd(const BwdParams p) {
       }
     }
     wave_lds_sync();
+    };
+
+  Tiles T0, T1;
+  const int K = p.nchunks;
+  load(T0, K - 1);
+  load(T1, K - 2);
+  chunk(T0, K - 1);
+  chunk(T1, K - 2);
+  for (int k = K - 3; k >= 0; k -= 2) {
+    chunk(T0, k);
+    chunk(T1, k - 1);
   }
 
   if (dval) ((CT *)p.ws_dA)[(b * p.D + d) * NP + n] = METHOD == 0 ? fma(dA2_acc, ac.invA, dA_acc) : dA_acc;

@@ -79,27 +79,43 @@ k_fwd(const FwdParams p) {
   const KView vout = with_layout<UL>(p.out, p.x), vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
   const bool xt = vx.s1 == 1, dtt = vdt.s1 == 1, bt = vB.s1 == 1, ctt = vC.s1 == 1;
   const bool ot = vout.s1 == 1;
-  WaveTile<IT, CT, CK, CW, UL> tx, tdt;
-  WaveTile<IT, CT, CK, NP, UL> tB, tC;
-  tx.load(vx, b, k0 * CK, L, dw, D, xt, lane);
-  tdt.load(vdt, b, k0 * CK, L, dw, D, dtt, lane);
-  tB.load(vB, b, k0 * CK, L, 0, N, bt, lane);
-  if (!SUM) tC.load(vC, b, k0 * CK, L, 0, N, ctt, lane);
-
-  for (int k = k0; k < k1; ++k) {
+  // Global reads run two chunks ahead of the compute: tiles ping-pong between two register
+  // sets, and a set is refilled (chunk k + 2) as soon as its chunk is staged in LDS.
+  const bool zt = p.has_z && p.write_out && !SUM;
+  struct Tiles {
+    WaveTile<IT, CT, CK, CW, UL> x, dt, z;
+    WaveTile<IT, CT, CK, NP, UL> B, C;
+  };
+  CT biasv[WaveTile<IT, CT, CK, CW, UL>::E], dskv[WaveTile<IT, CT, CK, CW, UL>::E];
+  tile_bias<CT, CK, CW>(biasv, p.has_bias, p.bias, dw, D, dtt, lane);
+  tile_bias<CT, CK, CW>(dskv, p.has_D, p.Dsk, dw, D, ot, lane);  // D skip in the output mapping
+  // Every load is unconditional (no branch around it) so that waiting for one chunk's tiles
+  // leaves the next chunk's loads and earlier stores in flight; past the segment's end the
+  // prefetch re-reads its last chunk, and without a gate the z tile reads x.
+  const KView vzl = zt ? vz : vx;
+  auto load = [&](Tiles &T, int k) {
+    const int t0 = (k < k1 ? k : k1 - 1) * CK;
+    T.x.load(vx, b, t0, L, dw, D, xt, lane);
+    T.dt.load(vdt, b, t0, L, dw, D, dtt, lane);
+    T.B.load(vB, b, t0, L, 0, N, bt, lane);
+    if (!SUM) T.C.load(vC, b, t0, L, 0, N, ctt, lane);
+    if (!SUM) T.z.load(vzl, b, t0, L, dw, D, ot, lane);  // the output phase's (t, channel) mapping
+  };
+  // A chunk k >= k1 is inert: its staged inputs are all zero (a = 1, b = 0 leaves h unchanged)
+  // and it stores nothing, so chunks always run in pairs and the loop is entered with the
+  // same loads and stores in flight as on its back edge.
+  auto chunk = [&](Tiles &T, int k) {
     const int t0 = k * CK;
-    tx.store(S.x, xt, lane);
-    store_delta_w<IT, CT, CK, CW, WL::CKP, UL>(tdt, S.dt, nullptr, dtt, lane, p.has_bias, p.softplus, p.bias, dw, D,
-                                            t0, L);
-    tB.store(S.B, bt, lane);
-    if (!SUM) tC.store(S.C, ctt, lane);
+    const int Lc = k < k1 ? L : 0;  // time bound of this chunk's elements
+    T.x.store(S.x, xt, lane, t0, Lc, dw, D);
+    store_delta_w<IT, CT, CK, CW, WL::CKP, UL>(T.dt, S.dt, nullptr, dtt, lane, p.softplus, biasv, dw, D, t0, Lc);
+    T.B.store(S.B, bt, lane, t0, Lc, 0, N);
+    if (!SUM) T.C.store(S.C, ctt, lane, t0, Lc, 0, N);
+    CT zv[WaveTile<IT, CT, CK, CW, UL>::E];
+#pragma unroll
+    for (int i = 0; i < WaveTile<IT, CT, CK, CW, UL>::E; ++i) zv[i] = T.z.v[i];
     wave_lds_sync();
-    if (k + 1 < k1) {  // next chunk's global reads overlap this chunk's compute
-      tx.load(vx, b, t0 + CK, L, dw, D, xt, lane);
-      tdt.load(vdt, b, t0 + CK, L, dw, D, dtt, lane);
-      tB.load(vB, b, t0 + CK, L, 0, N, bt, lane);
-      if (!SUM) tC.load(vC, b, t0 + CK, L, 0, N, ctt, lane);
-    }
+    load(T, k + 2);
 
     CT rdt[RB], rx[RB], rB[RB], rC[RB];
     lds_row(&S.dt[c][0], rdt);
@@ -148,9 +164,9 @@ k_fwd(const FwdParams p) {
     }
     if constexpr (SUM) {
       wave_lds_sync();
-      continue;
+      return;
     }
-    if (p.ckpt && dval)
+    if (p.ckpt && dval && k < k1)
       ((CT *)p.ckpt)[((b * p.nchunks + k) * p.D + d) * NP + n] = h;
     wave_lds_sync();
 
@@ -167,18 +183,25 @@ k_fwd(const FwdParams p) {
       CT y = 0;
 #pragma unroll
       for (int j = 0; j < NP; ++j) y += part[j];
-      if (tg >= L || dd >= D) continue;
-      const CT skip = p.has_D ? vload<CT>(p.Dsk, dd * p.Dsk.s0) * S.x[cc][t] : (CT)0;
+      if (tg >= Lc || dd >= D) continue;
+      const CT skip = p.has_D ? dskv[i] * S.x[cc][t] : (CT)0;
       if (p.ypre) ((CT *)p.ypre)[ypre_index(!xt, b, tg, dd, p.L, p.D)] = y + skip;
       if (!p.write_out) continue;
       CT o = y + skip;
-      if (p.has_z) {
-        const CT zv = Conv<IT>::load(vp<IT>(vz) + b * vz.s0 + row_off<UL>(tg, dd, vz.s1, vz.s2));
-        o *= zv * sigmoid_ct<CT>(zv);
-      }
+      if (p.has_z) o *= zv[i] * sigmoid_ct<CT>(zv[i]);
       Conv<IT>::store(vpw<IT>(vout) + b * vout.s0 + row_off<UL>(tg, dd, vout.s1, vout.s2), o);
     }
     wave_lds_sync();
+  };
+
+  Tiles T0, T1;
+  load(T0, k0);
+  load(T1, k0 + 1);
+  chunk(T0, k0);
+  chunk(T1, k0 + 1);
+  for (int k = k0 + 2; k < k1; k += 2) {
+    chunk(T0, k);
+    chunk(T1, k + 1);
   }
 
   if constexpr (SUM) {

@@ -29,6 +29,14 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Workgroup barrier ordering LDS traffic only: global loads and stores stay in flight across it
+// (a full __syncthreads() would first drain them with vmcnt(0)).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <typename CT> struct WaveCfg {
   static constexpr int CK = 16;                          // steps per chunk (checkpoint interval)
   static constexpr int CKP = CK + 16 / (int)sizeof(CT);  // padded row length
@@ -63,6 +71,10 @@ __device__ __forceinline__ KView with_layout(const KView &v, const KView &ref) {
 }
 
 // Register staging of a CK x COLS tile of a (B, L, C) view for one wavefront.
+// The loads are issued unconditionally from clamped (always valid) addresses and the
+// out-of-range elements are zeroed only when the tile is stored to LDS: no branch surrounds a
+// load, so the compiler can wait for one tile's loads (vmcnt(n)) while later prefetches and
+// stores stay in flight, instead of draining the whole memory queue (vmcnt(0)).
 template <typename IT, typename CT, int ROWS, int COLS, bool UL = false>
 struct WaveTile {
   static constexpr int E = (ROWS * COLS + kWave - 1) / kWave;
@@ -76,41 +88,62 @@ struct WaveTile {
       const int e = lane + i * kWave;
       int t, c;
       tc_of<ROWS, COLS>(e, tfast, t, c);
-      CT val = 0;
-      if (e < ROWS * COLS && t0 + t < L && c0 + c < C)
-        val = Conv<IT>::load(base + row_off<UL>(t0 + t, c0 + c, V.s1, V.s2));
-      v[i] = val;
+      const int tc = min(t0 + t, L - 1), cc = min(c0 + c, C - 1);
+      v[i] = Conv<IT>::load(base + row_off<UL>(tc, cc, V.s1, V.s2));
     }
   }
 
+  // element i of this lane is inside the (L, C) range
+  __device__ __forceinline__ static bool in_range(int i, bool tfast, int lane, int t0, int L, int c0, int C) {
+    const int e = lane + i * kWave;
+    int t, c;
+    tc_of<ROWS, COLS>(e, tfast, t, c);
+    return e < ROWS * COLS && t0 + t < L && c0 + c < C;
+  }
+
   template <int RP>
-  __device__ __forceinline__ void store(CT (*S)[RP], bool tfast, int lane) const {
+  __device__ __forceinline__ void store(CT (*S)[RP], bool tfast, int lane, int t0, int L, int c0, int C) const {
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       const int e = lane + i * kWave;
       if (e >= ROWS * COLS) break;
       int t, c;
       tc_of<ROWS, COLS>(e, tfast, t, c);
-      S[c][t] = v[i];
+      S[c][t] = (t0 + t < L && c0 + c < C) ? v[i] : (CT)0;
     }
   }
 };
+
+// Per-lane delta bias of the tile elements a lane stages (the channel of element i of a lane is
+// the same in every chunk), read once per kernel.
+template <typename CT, int ROWS, int COLS, int E>
+__device__ __forceinline__ void tile_bias(CT (&bv)[E], int has_bias, const KView &bias, int c0, int C, bool tfast,
+                                          int lane) {
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const int e = lane + i * kWave;
+    int t, c;
+    tc_of<ROWS, COLS>(e, tfast, t, c);
+    bv[i] = (has_bias && e < ROWS * COLS && c0 + c < C) ? vload<CT>(bias, (int64_t)(c0 + c) * bias.s0) : (CT)0;
+  }
+}
 
 // delta' = softplus(delta + bias) (optional parts) for in-range elements, padding stays 0;
 // `sg` (optional) receives the softplus derivative sigmoid(delta + bias) (1 without softplus).
 template <typename IT, typename CT, int ROWS, int COLS, int RP, bool UL>
 __device__ __forceinline__ void store_delta_w(const WaveTile<IT, CT, ROWS, COLS, UL> &tl, CT (*S)[RP], CT (*sg)[RP],
-                                              bool tfast, int lane, int has_bias, int softplus,
-                                              const KView &bias, int c0, int C, int t0, int L) {
+                                              bool tfast, int lane, int softplus,
+                                              const CT (&bv)[WaveTile<IT, CT, ROWS, COLS, UL>::E], int c0, int C,
+                                              int t0, int L) {
 #pragma unroll
   for (int i = 0; i < WaveTile<IT, CT, ROWS, COLS, UL>::E; ++i) {
     const int e = lane + i * kWave;
     if (e >= ROWS * COLS) break;
     int t, c;
     tc_of<ROWS, COLS>(e, tfast, t, c);
-    CT v = tl.v[i], g = 1;
+    CT v = 0, g = 1;
     if (t0 + t < L && c0 + c < C) {
-      if (has_bias) v += vload<CT>(bias, (int64_t)(c0 + c) * bias.s0);
+      v = tl.v[i] + bv[i];
       if (softplus) {
         g = sigmoid_ct<CT>(v);
         v = softplus_ct<CT>(v);
