@@ -84,7 +84,7 @@ __device__ __forceinline__ float fseries(float z) {
 
 __device__ __forceinline__ float softplusf(float v) { return v > 20.0f ? v : log1pf(__expf(v)); }
 __device__ __forceinline__ double softplusd(double v) { return v > 20.0 ? v : log1p(exp(v)); }
-__device__ __forceinline__ float sigmoidf(float v) { return 1.0f / (1.0f + __expf(-v)); }
+__device__ __forceinline__ float sigmoidf(float v) { return fast_rcp(1.0f + __expf(-v)); }
 __device__ __forceinline__ double sigmoidd(double v) { return 1.0 / (1.0 + exp(-v)); }
 
 // Per-(d, n) constants of the discretization.
