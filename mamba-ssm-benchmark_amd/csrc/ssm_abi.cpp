@@ -64,22 +64,24 @@ int check_common(int64_t B, int64_t L, int64_t D, int64_t N, int method, int dty
     if (!has(t)) return fail(SSM_EINVAL, "required tensor '%s' is missing", name); \
   } while (0)
 
-// True when every present (B,L,D) view has x's strides, Cm has Bm's, and every element offset
-// inside one batch row fits in a signed 32-bit integer (the kernels' fast addressing).
+// True when every present (B,L,D) view has x's strides, Cm has Bm's, strides are non-negative
+// and one batch row, with a chunk and a channel tile of over-reach, spans less than 2^31 bytes:
+// the kernels then address tiles with 32-bit byte offsets (raw buffer reads).
 bool same3(const ssm_tensor &a, const ssm_tensor &b) {
   return !has(a) || (a.stride[0] == b.stride[0] && a.stride[1] == b.stride[1] && a.stride[2] == b.stride[2]);
 }
-bool row_fits(const ssm_tensor &t, int64_t L, int64_t C) {
-  const int64_t lim = (int64_t)1 << 30;
-  const int64_t s1 = t.stride[1] < 0 ? -t.stride[1] : t.stride[1];
-  const int64_t s2 = t.stride[2] < 0 ? -t.stride[2] : t.stride[2];
-  return s1 < lim && s2 < lim && (L - 1) * s1 + (C - 1) * s2 + C < lim;
+bool row_fits(const ssm_tensor &t, int64_t L, int64_t C, int esize) {
+  const int64_t lim = (int64_t)1 << 31;
+  const int64_t s1 = t.stride[1], s2 = t.stride[2];
+  if (s1 < 0 || s2 < 0 || s1 >= lim || s2 >= lim) return false;
+  return ((L - 1 + 2 * kCK) * s1 + (C - 1 + 64) * s2 + 1) * esize < lim;
 }
 bool uniform_layout(const ssm_tensor *bld[], int nbld, const ssm_tensor &Bm, const ssm_tensor &Cm, int64_t L,
-                    int64_t D, int64_t N) {
+                    int64_t D, int64_t N, int dtype) {
+  const int esize = dtype == SSM_F64 ? 8 : dtype == SSM_F32 ? 4 : 2;
   for (int i = 0; i < nbld; ++i)
     if (!same3(*bld[i], *bld[0])) return false;
-  return same3(Cm, Bm) && row_fits(*bld[0], L, D) && row_fits(Bm, L, N);
+  return same3(Cm, Bm) && row_fits(*bld[0], L, D, esize) && row_fits(Bm, L, N, esize);
 }
 
 struct FwdLayout {
@@ -192,7 +194,7 @@ static void fill_fwd(FwdParams &p, const ssm_fwd_args *a, const FwdLayout &f) {
   p.Dsk = kv(a->Dskip); p.z = kv(a->z); p.bias = kv(a->delta_bias); p.h0 = kv(a->h0);
   p.out = kv(a->out); p.last = kv(a->last);
   const ssm_tensor *bld[] = {&a->x, &a->delta, &a->z, &a->out};
-  p.uniform = uniform_layout(bld, 4, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate);
+  p.uniform = uniform_layout(bld, 4, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype);
 }
 
 int ssm_fwd(const ssm_fwd_args *a, void *stream) {
@@ -293,7 +295,7 @@ int ssm_bwd(const ssm_bwd_args *a, void *stream) {
   p.dz = kv(a->dz); p.dh0 = kv(a->dh0);
   p.ckpt = ckpt; p.ypre = ypre;
   const ssm_tensor *bld[] = {&a->x, &a->delta, &a->z, &a->dout, &a->dx, &a->ddelta, &a->dz};
-  p.uniform = uniform_layout(bld, 7, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate);
+  p.uniform = uniform_layout(bld, 7, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype);
   p.ws_dB = ws + w.dB; p.ws_dC = ws + w.dC; p.ws_dA = ws + w.dA; p.ws_dD = ws + w.dD; p.ws_db = ws + w.db;
   hipError_t e = launch_bwd(p, a->dtype, a->method, w.f.np, s);
   if (e != hipSuccess) return hip_fail(e, "ssm_bwd launch");

@@ -93,13 +93,32 @@ k_fwd(const FwdParams p) {
   // leaves the next chunk's loads and earlier stores in flight; past the segment's end the
   // prefetch re-reads its last chunk, and without a gate the z tile reads x.
   const KView vzl = zt ? vz : vx;
+  // With a uniform layout x, delta, z share one set of lane offsets (and B, C another) and are
+  // read through raw buffers; otherwise through clamped global addresses.
+  constexpr int ES = (int)sizeof(IT);
+  constexpr int EX = WaveTile<IT, CT, CK, CW, UL>::E, EB = WaveTile<IT, CT, CK, NP, UL>::E;
+  uint32_t offX[EX], offB[EB];
+  tile_offsets<CK, CW>(offX, vx, dw, xt, lane, ES);
+  tile_offsets<CK, NP>(offB, vB, 0, bt, lane, ES);
+  const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES), rbdt = row_buffer(vdt, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbz = row_buffer(vzl, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbB = row_buffer(vB, b, L, N, ES), rbC = row_buffer(vC, b, L, N, ES);
   auto load = [&](Tiles &T, int k) {
     const int t0 = (k < k1 ? k : k1 - 1) * CK;
-    T.x.load(vx, b, t0, L, dw, D, xt, lane);
-    T.dt.load(vdt, b, t0, L, dw, D, dtt, lane);
-    T.B.load(vB, b, t0, L, 0, N, bt, lane);
-    if (!SUM) T.C.load(vC, b, t0, L, 0, N, ctt, lane);
-    if (!SUM) T.z.load(vzl, b, t0, L, dw, D, ot, lane);  // the output phase's (t, channel) mapping
+    if constexpr (UL) {
+      const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES), tb_ = (uint32_t)(t0 * (int)vB.s1 * ES);
+      T.x.load_buf(rbx, offX, tx_);
+      T.dt.load_buf(rbdt, offX, tx_);
+      T.B.load_buf(rbB, offB, tb_);
+      if (!SUM) T.C.load_buf(rbC, offB, tb_);
+      if (!SUM) T.z.load_buf(rbz, offX, tx_);
+    } else {
+      T.x.load(vx, b, t0, L, dw, D, xt, lane);
+      T.dt.load(vdt, b, t0, L, dw, D, dtt, lane);
+      T.B.load(vB, b, t0, L, 0, N, bt, lane);
+      if (!SUM) T.C.load(vC, b, t0, L, 0, N, ctt, lane);
+      if (!SUM) T.z.load(vzl, b, t0, L, dw, D, ot, lane);  // the output phase's (t, channel) mapping
+    }
   };
   // A chunk k >= k1 is inert: its staged inputs are all zero (a = 1, b = 0 leaves h unchanged)
   // and it stores nothing, so chunks always run in pairs and the loop is entered with the

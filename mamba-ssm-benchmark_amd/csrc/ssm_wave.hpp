@@ -70,6 +70,46 @@ __device__ __forceinline__ KView with_layout(const KView &v, const KView &ref) {
   return UL ? KView{v.p, ref.s0, ref.s1, ref.s2} : v;
 }
 
+// ------------------------------------------------------------------ raw buffer reads
+// With a uniform layout every batch row of a view spans less than 2^31 bytes (checked on the
+// host), so a tile element is addressed by a 32-bit byte offset from the row's base through a
+// buffer resource whose range is the row's extent: the per-lane offsets are computed once per
+// kernel, a chunk adds one uniform offset, and a read past the extent returns 0 instead of
+// faulting (so no clamping is needed for the ragged last chunk or channel tile).
+constexpr int kBufferFlags = 0x00020000;  // raw 32-bit data, gfx9 family
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const KView &V, int64_t b, int L, int C, int esize) {
+  const char *base = (const char *)V.p + b * V.s0 * esize;
+  const int64_t ext = ((int64_t)(L - 1) * V.s1 + (int64_t)(C - 1) * V.s2 + 1) * esize;
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)ext, kBufferFlags);
+}
+
+template <typename IT> __device__ __forceinline__ typename Conv<IT>::CT buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off);
+template <> __device__ __forceinline__ float buf_load<float>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+template <> __device__ __forceinline__ float buf_load<bf16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __uint_as_float(((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0)) << 16);
+}
+template <> __device__ __forceinline__ float buf_load<f16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return (float)__builtin_bit_cast(f16_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0));
+}
+template <> __device__ __forceinline__ double buf_load<double>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+
+// Byte offsets (at t0 = 0) of the tile elements a lane stages, for a view with element size `esize`.
+template <int ROWS, int COLS, int E>
+__device__ __forceinline__ void tile_offsets(uint32_t (&off)[E], const KView &V, int c0, bool tfast, int lane,
+                                             int esize) {
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    int t, c;
+    tc_of<ROWS, COLS>(lane + i * kWave, tfast, t, c);
+    off[i] = (uint32_t)((t * (int)V.s1 + (c0 + c) * (int)V.s2) * esize);
+  }
+}
+
 // Register staging of a CK x COLS tile of a (B, L, C) view for one wavefront.
 // The loads are issued unconditionally from clamped (always valid) addresses and the
 // out-of-range elements are zeroed only when the tile is stored to LDS: no branch surrounds a
@@ -91,6 +131,13 @@ struct WaveTile {
       const int tc = min(t0 + t, L - 1), cc = min(c0 + c, C - 1);
       v[i] = Conv<IT>::load(base + row_off<UL>(tc, cc, V.s1, V.s2));
     }
+  }
+
+  // Buffer form of load(): `off` holds this lane's byte offsets at t0 = 0 (tile_offsets) and
+  // `toff` the chunk's byte offset; reads past the row's extent return 0 and never fault.
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, const uint32_t (&off)[E], uint32_t toff) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = buf_load<IT>(r, off[i] + toff);
   }
 
   // element i of this lane is inside the (L, C) range
