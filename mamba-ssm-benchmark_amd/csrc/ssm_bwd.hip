@@ -35,7 +35,7 @@ struct BwdWaveLds {
   CT gd[CW][CKP];
   CT B[NP][CKP];
   CT C[NP][CKP];
-  CT pn[RH][CW][2][NP];  // (dx, ddelta) per-lane contributions, quantity-major
+  CT pn[RH][CW][2][np_pad((int)sizeof(CT), NP)];  // (dx, ddelta) per-lane contributions, quantity-major
   CT pd[RH][CW][NP][2];  // (dB, dC) per-lane contributions
 };
 

@@ -39,7 +39,7 @@ struct FwdWaveLds {
   CT dt[CW][CKP];
   CT B[NP][CKP];
   CT C[NP][CKP];
-  CT y[CK][CW][NP];
+  CT y[CK][CW][np_pad((int)sizeof(CT), NP)];
 };
 
 template <typename IT, int NP, int METHOD, bool UL, bool SUM>

@@ -19,13 +19,17 @@ constexpr int kCK = 16;
 constexpr int kThreads = 256;  // threads per workgroup of the simple (non-scan) kernels
 inline int chunk_steps(int) { return kCK; }
 inline int padded_n(int64_t n) { return n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32 : 64; }
+// LDS rows read with 16-byte vector loads by lanes of different rows are padded by 16 bytes,
+// which spreads the lanes of a read over distinct banks.
 __host__ __device__ constexpr int ck_pad(int s) { return kCK + 16 / s; }
+__host__ __device__ constexpr int np_pad(int s, int np) { return np + 16 / s; }
 __host__ __device__ constexpr int fwd_wave_bytes(int s, int np) {
-  return ((2 * (64 / np) + 2 * np) * ck_pad(s) + kCK * 64) * s;
+  return ((2 * (64 / np) + 2 * np) * ck_pad(s) + kCK * (64 / np) * np_pad(s, np)) * s;
 }
 __host__ __device__ constexpr int bwd_half() { return 8; }  // reverse steps per LDS reduction round
 __host__ __device__ constexpr int bwd_wave_bytes(int s, int np) {
-  return ((6 * (64 / np) + 2 * np) * ck_pad(s) + 2 * bwd_half() * 64 * 2) * s;
+  return ((6 * (64 / np) + 2 * np) * ck_pad(s) + bwd_half() * (64 / np) * 2 * np_pad(s, np) +
+          bwd_half() * 64 * 2) * s;
 }
 __host__ __device__ constexpr int bwd_shared_bytes(int s, int np, int wpb) {
   return wpb > 1 ? 2 * wpb * kCK * np * 2 * s : 0;
