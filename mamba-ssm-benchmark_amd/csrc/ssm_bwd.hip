@@ -121,21 +121,50 @@ k_bwd(const BwdParams p) {
   };
   const KView vzl = p.has_z ? vz : vx;
   const int dc = dval ? d : 0;
+  // With a uniform layout x, delta, dout, z share one set of lane offsets (B, C another), and
+  // they and the saved pre-gate output are read through raw buffers over one batch row.
+  constexpr int ES = (int)sizeof(IT), EB = WaveTile<IT, CT, CK, NP, UL>::E;
+  uint32_t offX[E1], offB[EB], offY[E1];
+  tile_offsets<CK, CW>(offX, vx, dw, xt, lane, ES);
+  tile_offsets<CK, NP>(offB, vB, 0, bt, lane, ES);
+  const KView vy{ypre, xt ? 1 : (int64_t)D, xt ? 1 : (int64_t)D, xt ? (int64_t)L : 1};  // ypre's (t, d) strides
+  tile_offsets<CK, CW>(offY, vy, dw, gt, lane, (int)sizeof(CT));
+  const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES), rbdt = row_buffer(vdt, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbg = row_buffer(vg, b, L, D, ES), rbz = row_buffer(vzl, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbB = row_buffer(vB, b, L, N, ES), rbC = row_buffer(vC, b, L, N, ES);
+  const __amdgpu_buffer_rsrc_t rby = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(ypre ? ypre + b * p.L * p.D : (const CT *)p.ckpt), (short)0, (int)(ypre ? p.L * p.D * sizeof(CT) : 0),
+      kBufferFlags);
   auto load = [&](Tiles &T, int k) {
     const int kc = k < 0 ? 0 : k;
     const int t0 = kc * CK;
-    T.x.load(vx, b, t0, L, dw, D, xt, lane);
-    T.dt.load(vdt, b, t0, L, dw, D, dtt, lane);
-    T.g.load(vg, b, t0, L, dw, D, gt, lane);
-    T.z.load(vzl, b, t0, L, dw, D, gt, lane);
-    T.B.load(vB, b, t0, L, 0, N, bt, lane);
-    T.C.load(vC, b, t0, L, 0, N, ctt, lane);
-    if (p.has_z) {
+    if constexpr (UL) {
+      const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES), tb_ = (uint32_t)(t0 * (int)vB.s1 * ES);
+      T.x.load_buf(rbx, offX, tx_);
+      T.dt.load_buf(rbdt, offX, tx_);
+      T.g.load_buf(rbg, offX, tx_);
+      T.z.load_buf(rbz, offX, tx_);
+      T.B.load_buf(rbB, offB, tb_);
+      T.C.load_buf(rbC, offB, tb_);
+      if (p.has_z) {
+        const uint32_t ty_ = (uint32_t)(t0 * (int)vy.s1 * (int)sizeof(CT));
 #pragma unroll
-      for (int i = 0; i < E1; ++i) {
-        int t, cc;
-        tc_of<CK, CW>(lane + i * kWave, gt, t, cc);
-        T.yp[i] = ypre[ypre_index(!xt, b, min(t0 + t, L - 1), min(dw + cc, D - 1), p.L, p.D)];
+        for (int i = 0; i < E1; ++i) T.yp[i] = buf_load<CT>(rby, offY[i] + ty_);
+      }
+    } else {
+      T.x.load(vx, b, t0, L, dw, D, xt, lane);
+      T.dt.load(vdt, b, t0, L, dw, D, dtt, lane);
+      T.g.load(vg, b, t0, L, dw, D, gt, lane);
+      T.z.load(vzl, b, t0, L, dw, D, gt, lane);
+      T.B.load(vB, b, t0, L, 0, N, bt, lane);
+      T.C.load(vC, b, t0, L, 0, N, ctt, lane);
+      if (p.has_z) {
+#pragma unroll
+        for (int i = 0; i < E1; ++i) {
+          int t, cc;
+          tc_of<CK, CW>(lane + i * kWave, gt, t, cc);
+          T.yp[i] = ypre[ypre_index(!xt, b, min(t0 + t, L - 1), min(dw + cc, D - 1), p.L, p.D)];
+        }
       }
     }
     T.ck = ((const CT *)p.ckpt)[((b * p.nchunks + (kc > 0 ? kc - 1 : 0)) * p.D + dc) * NP + n];
