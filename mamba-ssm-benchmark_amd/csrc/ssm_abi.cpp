@@ -587,10 +587,65 @@ int ssm_disc_bwd(const ssm_disc_args *a, void *stream) {
   return e == hipSuccess ? ok() : hip_fail(e, "ssm_disc_bwd");
 }
 
-// ------------------------------------------------------------------ not yet available
-int ssm_conv_check(const ssm_conv_args *a) { (void)a; return fail(SSM_EINVAL, "ssm_conv: not built in this library version"); }
-int64_t ssm_conv_workspace_bytes(const ssm_conv_args *a) { (void)a; return -1; }
-int ssm_conv_fwd(const ssm_conv_args *a, void *s) { (void)s; return ssm_conv_check(a); }
-int ssm_conv_bwd(const ssm_conv_args *a, void *s) { (void)s; return ssm_conv_check(a); }
+// ------------------------------------------------------------------ causal depthwise conv
+static constexpr int kConvTB = 64;  // time steps per lane
+
+static ConvParams conv_params(const ssm_conv_args *a) {
+  ConvParams p;
+  memset(&p, 0, sizeof(p));
+  p.B = a->batch; p.L = a->seqlen; p.D = a->dim; p.W = a->width;
+  p.TB = kConvTB;
+  p.nblk = (int)cdiv(a->seqlen, kConvTB);
+  p.silu = a->silu != 0;
+  p.has_bias = has(a->bias); p.has_sin = has(a->state_in); p.has_sout = has(a->state_out);
+  p.has_dbias = has(a->dbias);
+  p.x = kv(a->x); p.w = kv(a->weight); p.bias = kv(a->bias); p.sin = kv(a->state_in);
+  p.out = kv(a->out); p.sout = kv(a->state_out); p.dout = kv(a->dout); p.dx = kv(a->dx);
+  p.dw = kv(a->dweight); p.dbias = kv(a->dbias);
+  return p;
+}
+
+int ssm_conv_check(const ssm_conv_args *a) {
+  if (!a) return fail(SSM_EINVAL, "null args");
+  if (a->dtype < 0 || a->dtype > 3) return fail(SSM_EINVAL, "unsupported dtype code %d", a->dtype);
+  if (a->batch < 1 || a->seqlen < 1 || a->dim < 1)
+    return fail(SSM_EINVAL, "empty conv: batch=%lld seqlen=%lld dim=%lld", (long long)a->batch,
+                (long long)a->seqlen, (long long)a->dim);
+  if (a->width < 1 || a->width > 8) return fail(SSM_EINVAL, "conv width %lld not in 1..8", (long long)a->width);
+  if (a->seqlen >= (1LL << 30) || a->batch * a->dim * cdiv(a->seqlen, kConvTB) >= (1LL << 38))
+    return fail(SSM_EINVAL, "conv too large");
+  REQUIRE(a->x, "x");
+  REQUIRE(a->weight, "weight");
+  return ok();
+}
+
+int64_t ssm_conv_workspace_bytes(const ssm_conv_args *a) {
+  if (ssm_conv_check(a)) return -1;
+  return align256(a->batch * cdiv(a->seqlen, kConvTB) * a->dim * (a->width + 1) * state_size(a->dtype));
+}
+
+int ssm_conv_fwd(const ssm_conv_args *a, void *stream) {
+  int rc = ssm_conv_check(a);
+  if (rc) return rc;
+  REQUIRE(a->out, "out");
+  hipError_t e = launch_conv(conv_params(a), a->dtype, false, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "ssm_conv_fwd");
+}
+
+int ssm_conv_bwd(const ssm_conv_args *a, void *stream) {
+  int rc = ssm_conv_check(a);
+  if (rc) return rc;
+  REQUIRE(a->dout, "dout");
+  REQUIRE(a->dx, "dx");
+  REQUIRE(a->dweight, "dweight");
+  if (has(a->bias)) REQUIRE(a->dbias, "dbias");
+  const int64_t need = ssm_conv_workspace_bytes(a);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(SSM_ESPACE, "workspace of %lld bytes required", (long long)need);
+  ConvParams p = conv_params(a);
+  p.ws = a->workspace;
+  hipError_t e = launch_conv(p, a->dtype, true, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "ssm_conv_bwd");
+}
 
 }  // extern "C"

@@ -136,6 +136,15 @@ struct DiscParams {
   void *ws_dA;  // (ngroups, D, N) partial sums over each group of rows
 };
 
+// Causal depthwise conv over (B, L, D) views; a lane owns (b, d, one block of TB steps).
+struct ConvParams {
+  int64_t B, L, D, W;
+  int nblk, TB;
+  int silu, has_bias, has_sin, has_sout, has_dbias;
+  KView x, w, bias, sin, out, sout, dout, dx, dw, dbias;  // sin / sout: (B, D, W-1)
+  void *ws;  // backward: (B * nblk, D, W + 1) partial dweight / dbias
+};
+
 // Runs the summary and carry passes first when p.nseg > 1.
 hipError_t launch_fwd(const FwdParams &p, int dtype, int method, int np, hipStream_t s);
 hipError_t launch_bwd(const BwdParams &p, int dtype, int method, int np, hipStream_t s);
@@ -145,6 +154,7 @@ hipError_t launch_lscan(const LscanParams &p, int algo, int dtype, hipStream_t s
 hipError_t launch_lscan_grad(const LscanGradParams &p, int dtype, hipStream_t s);
 // Channels per workgroup of the discretize backward (its dB partial-sum tile).
 inline int disc_channels(int np) { return kThreads / np; }
+hipError_t launch_conv(const ConvParams &p, int dtype, bool bwd, hipStream_t s);
 hipError_t launch_disc_fwd(const DiscParams &p, int dtype, int method, int np, hipStream_t s);
 hipError_t launch_disc_bwd(const DiscParams &p, int dtype, int method, int np, hipStream_t s);
 

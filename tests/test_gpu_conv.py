@@ -1,0 +1,118 @@
+"""Causal depthwise conv1d + SiLU (ssm_conv_fwd / ssm_conv_bwd) against the float64 oracle
+and torch.nn.functional.conv1d (float64, CPU; gradients by autograd).
+
+Mirrors the conv of models/mamba.py:101-107 incl. its state handling (:104-106): a sequence
+processed in pieces with the carried state, and one token at a time, equals the whole
+sequence (the reference's decode == forward check, tests/test_models.py:36-48).
+Tolerances: float32 rtol 1e-5 / atol 1e-6 (a W-tap dot product); bf16 inputs 2e-2; float64 1e-12.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from ssm_scan.conv import causal_conv1d
+from oracle import scan_ref as R
+from ssm_inputs import np64
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.float32: (1e-5, 1e-6), torch.bfloat16: (2e-2, 2e-2), torch.float64: (1e-12, 1e-12)}
+
+
+def ref_conv(x_bld, w, bias, activation=True):
+    """torch float64 CPU reference (autograd-capable): (B, L, D) -> (B, L, D)."""
+    W = w.shape[1]
+    xc = F.pad(x_bld.transpose(1, 2), (W - 1, 0))
+    y = F.conv1d(xc, w.unsqueeze(1), bias, groups=w.shape[0])
+    if activation:
+        y = F.silu(y)
+    return y.transpose(1, 2)
+
+
+def inputs(B, L, D, W, seed, split_view=True):
+    g = torch.Generator().manual_seed(seed)
+    if split_view:   # the in_proj(u).chunk(2) view: (B, L, D) with row stride 2D
+        xz = torch.randn(B, L, 2 * D, generator=g, dtype=torch.float64)
+        x = xz[..., :D]
+    else:
+        x = torch.randn(B, L, D, generator=g, dtype=torch.float64)
+    w = torch.randn(D, W, generator=g, dtype=torch.float64) * 0.5
+    bias = torch.randn(D, generator=g, dtype=torch.float64) * 0.1
+    return x, w, bias
+
+
+@pytest.mark.parametrize("W", [1, 2, 4, 5, 8])
+@pytest.mark.parametrize("L", [1, 3, 64, 65, 200])
+def test_forward_matches_oracle(dev, W, L):
+    x, w, bias = inputs(2, L, 37, W, seed=W * 100 + L)
+    y = causal_conv1d(x.to(dev, torch.float32), w.to(dev, torch.float32), bias.to(dev, torch.float32))
+    ry, _ = R.conv1d_causal(np64(x).transpose(0, 2, 1), np64(w), np64(bias))
+    rt, at = TOL[torch.float32]
+    np.testing.assert_allclose(np64(y), ry.transpose(0, 2, 1), rtol=rt, atol=at)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize("activation,with_bias", [(True, True), (False, True), (True, False)])
+def test_forward_backward_matches_torch(dev, dtype, activation, with_bias):
+    x, w, bias = inputs(3, 150, 64, 4, seed=7)
+    if not with_bias:
+        bias = None
+    xd = x.to(dtype)                      # the reference consumes the same rounded inputs
+    leaves = [xd.to(dev).requires_grad_(), w.to(dev, torch.float32 if dtype != torch.float64 else dtype).requires_grad_()]
+    bl = None if bias is None else bias.to(dev, leaves[1].dtype).requires_grad_()
+    y = causal_conv1d(leaves[0], leaves[1], bl, activation=activation)
+    g = torch.Generator().manual_seed(8)
+    dy = torch.randn(y.shape, generator=g, dtype=torch.float64)
+    y.backward(dy.to(dev, dtype))
+    rx = xd.double().requires_grad_()
+    rw = leaves[1].detach().cpu().double().requires_grad_()
+    rb = None if bias is None else bl.detach().cpu().double().requires_grad_()
+    ry = ref_conv(rx, rw, rb, activation)
+    ry.backward(dy.to(dtype).double())
+    rt, at = TOL[dtype]
+    scale = max(1.0, float(ry.detach().abs().max()))
+    np.testing.assert_allclose(np64(y), ry.detach().numpy(), rtol=rt, atol=at * scale)
+    np.testing.assert_allclose(np64(leaves[0].grad), rx.grad.numpy(), rtol=rt, atol=at * scale)
+    gs = max(1.0, float(rw.grad.abs().max()))
+    np.testing.assert_allclose(np64(leaves[1].grad), rw.grad.numpy(), rtol=rt, atol=at * gs * 10)
+    if bias is not None:
+        np.testing.assert_allclose(np64(bl.grad), rb.grad.numpy(), rtol=rt, atol=at * gs * 10)
+
+
+def test_nn_conv1d_weight_and_contiguous_input(dev):
+    x, w, bias = inputs(2, 70, 32, 4, seed=3, split_view=False)
+    conv = torch.nn.Conv1d(32, 32, 4, groups=32, bias=True).double()
+    with torch.no_grad():
+        conv.weight.copy_(w.unsqueeze(1))
+        conv.bias.copy_(bias)
+    y = causal_conv1d(x.to(dev), conv.weight.to(dev), conv.bias.to(dev))
+    ry = F.silu(conv(F.pad(x.transpose(1, 2), (3, 0)))).transpose(1, 2)
+    np.testing.assert_allclose(np64(y), ry.detach().numpy(), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("W", [2, 4, 6])
+def test_state_streaming_and_decode_equal_full(dev, W):
+    """Pieces with the carried state, and single tokens, reproduce the full sequence."""
+    x, w, bias = inputs(2, 67, 48, W, seed=W)
+    xd, wd, bd = x.to(dev), w.to(dev), bias.to(dev)
+    full = causal_conv1d(xd, wd, bd)
+    state = torch.zeros(2, 48, W - 1, dtype=torch.float64, device=dev)
+    pieces = [causal_conv1d(xd[:, a:b_], wd, bd, state=state) for a, b_ in ((0, 2), (2, 30), (30, 67))]
+    np.testing.assert_allclose(np64(torch.cat(pieces, 1)), np64(full), rtol=1e-12, atol=1e-12)
+    ry, rstate = R.conv1d_causal(np64(x).transpose(0, 2, 1), np64(w), np64(bias))
+    np.testing.assert_allclose(np64(state), rstate, rtol=0, atol=0)
+    state2 = torch.zeros_like(state)
+    steps = [causal_conv1d(xd[:, t:t + 1], wd, bd, state=state2) for t in range(67)]
+    np.testing.assert_allclose(np64(torch.cat(steps, 1)), np64(full), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(np64(state2), rstate, rtol=0, atol=0)
+
+
+def test_conv_errors(dev):
+    x = torch.zeros(1, 4, 8, device=dev)
+    with pytest.raises(ValueError):
+        causal_conv1d(x, torch.zeros(8, 9, device=dev))           # width 9 > 8
+    with pytest.raises(ValueError):
+        causal_conv1d(x, torch.zeros(7, 4, device=dev))
+    with pytest.raises(RuntimeError):
+        causal_conv1d(x.cpu(), torch.zeros(8, 4))
