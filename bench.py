@@ -15,8 +15,9 @@ small fixed-order reduction kernel) gives the roofline: algorithmic bytes per la
 average duration, against 8 TB/s.  The CPU baseline is the torch-CPU restatement of the
 reference's CPU path (oracle/cpu_chunked.py), timed on a bounded sample of the same workload.
 
-Other workloads (--workload): c0 (forward, B1 L512), c2 (long-sequence forward), c4 (decode
-step), copy (a plain device copy of known size, for PMC counter calibration).
+Other workloads (--workload): c0 (forward, B1 L512), c2 / c2bf16 (long-sequence forward),
+c3 (10-layer Mamba LM fwd+bwd), c4 (decode latency per layer at batch 64, HIP-graph replay),
+copy (a plain device copy of known size, for PMC counter calibration).
 """
 
 import argparse
@@ -239,6 +240,104 @@ def bench_fwd(args, dev, B, L, dtype, workload):
     return rec
 
 
+def bench_lm(args, dev):
+    """Config 3: the 10-layer byte-level Mamba LM (d_model 256, d_inner 512, N 16), forward +
+    backward of the next-byte cross-entropy at B16 L512, float32, random init and random bytes.
+    Scan and conv1d run in the engine's kernels, the projections in torch."""
+    import ssm_scan
+    from ssm_scan.block import MambaLM
+    torch.manual_seed(0)
+    model = MambaLM(n_layers=10).to(dev)
+    g = torch.Generator().manual_seed(1)
+    idx = torch.randint(0, 256, (16, 513), generator=g).to(dev)
+    inp, tgt = idx[:, :-1], idx[:, 1:]
+    params = list(model.parameters())
+
+    def step():
+        logits = model(inp)
+        loss = torch.nn.functional.cross_entropy(logits.reshape(-1, 256), tgt.reshape(-1))
+        return torch.autograd.grad(loss, params)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    with ssm_scan.KernelTimer() as timer:
+        for _ in range(min(args.steps, 10)):
+            step()
+    tt = {k: sum(v) / len(v) for k, v in timer.times_ms().items()}
+    per_step = {k: tt[k] * 10 for k in tt}   # ten layers call each entry once per step
+    return {"metric": "Mamba LM (10 layers, d_model 256) fwd+bwd tokens/s, B16 L512 fp32", "value": 16 * 512 / (ms * 1e-3),
+            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (uniform random bytes, random-init weights)",
+            "config": {"workload": "config 3: byte-level Mamba LM fwd+bwd", "layers": 10, "batch": 16, "seqlen": 512,
+                       "d_model": 256, "d_inner": 512, "dstate": 16, "params_non_embedding": model.num_params()},
+            "engine_ms_per_step": per_step}
+
+
+def bench_decode(args, dev):
+    """Config 4: recurrent decode of the config-3 model at batch 64 (fp32 state ~ N(0,1), one
+    random byte per step).  The token step (10 layers: projections in torch, conv step and
+    scan step in the engine) is captured once in a HIP graph and replayed; 256 steps timed."""
+    from ssm_scan.block import MambaLM
+    torch.manual_seed(0)
+    model = MambaLM(n_layers=10).to(dev).eval()
+    B = 64
+    states = model.init_state(B, 1, dev)
+    g = torch.Generator().manual_seed(2)
+    for s in states:
+        s.ssm.copy_(torch.randn(s.ssm.shape, generator=g))
+        s.conv.copy_(torch.randn(s.conv.shape, generator=g))
+    tok = torch.zeros(B, 1, dtype=torch.long, device=dev)
+    toks = torch.randint(0, 256, (args.decode_steps + 64, B, 1), generator=g).to(dev)
+
+    def step():
+        with torch.no_grad():
+            return model(tok, states, 0)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.decode_steps):
+        tok.copy_(toks[i])
+        step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / args.decode_steps
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for i in range(20):
+        tok.copy_(toks[i])
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.decode_steps):
+        tok.copy_(toks[i])
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.decode_steps
+    return {"metric": "Mamba LM decode latency per token per layer, batch 64 (10 layers)", "value": ms * 1e3 / 10,
+            "unit": "us/layer", "n_gpus": 1, "steps": args.decode_steps, "warmup": 20, "ms_per_step": ms,
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (random bytes, random-init weights, N(0,1) states)",
+            "config": {"workload": "config 4: recurrent decode step, HIP-graph replay of the 10-layer token step",
+                       "batch": B, "layers": 10, "d_model": 256, "d_inner": 512, "dstate": 16, "conv_width": 4},
+            "ms_per_token_model": ms, "eager_ms_per_token_model": eager_ms,
+            "tokens_per_s": B / (ms * 1e-3)}
+
+
 def bench_copy(args, dev):
     """A plain device copy of 256 MiB (reads 256 MiB, writes 256 MiB): PMC calibration."""
     src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
@@ -255,7 +354,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "copy"])
+    ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "c3", "c4", "copy"])
+    ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--seqlen", type=int, default=131072)
     ap.add_argument("--segments", type=int, default=0, help="forward time segments (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -276,6 +376,10 @@ def main():
     elif args.workload in ("c2", "c2bf16"):
         dt = torch.bfloat16 if args.workload == "c2bf16" else torch.float32
         rec = bench_fwd(args, dev, 1, args.seqlen, dt, f"config 2: fwd B1 L{args.seqlen} D512 N16")
+    elif args.workload == "c3":
+        rec = bench_lm(args, dev)
+    elif args.workload == "c4":
+        rec = bench_decode(args, dev)
     else:
         rec = bench_copy(args, dev)
     print(json.dumps(rec), flush=True)

@@ -1,0 +1,167 @@
+"""The Mamba (S6) mixer of models/mamba.py on the HIP engine, and the byte-level LM of
+models/lm.py restricted to Mamba layers -- the callers of the scan path.
+
+Same parameters (names, shapes, initialization) and the same forward / decode interface as
+the reference, so a state_dict moves between the two.  The projections are torch GEMMs; the
+scan-path work runs in the engine's kernels:
+  conv + SiLU                   ssm_scan.conv.causal_conv1d          (models/mamba.py:101-107)
+  dt_proj bias + softplus,      fused into the scan / step kernels   (models/mamba.py:76)
+  selective scan, D skip, gate  ssm_scan.selective_scan_fn           (models/mamba.py:120-124)
+  decode step                   ssm_scan.ssm_step (state in place)   (models/mamba.py:113-123)
+"""
+
+import math
+from types import SimpleNamespace
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .conv import causal_conv1d
+from .hip_scan import selective_scan_fn
+from .step import ssm_step
+
+
+class Mamba(nn.Module):
+    """models/mamba.py:26-126 (Mamba) with the scan path on the HIP engine."""
+
+    def __init__(self, d_model, d_state=16, expand=2, d_conv=4, dt_rank=None, selective=True,
+                 discretization="zoh", dt_min=1e-3, dt_max=0.1, a_mode="s4d"):
+        super().__init__()
+        self.d_inner = d_inner = expand * d_model
+        self.d_state, self.d_conv = d_state, d_conv
+        self.dt_rank = dt_rank or math.ceil(d_model / 16)
+        self.selective, self.discretization = selective, discretization
+
+        self.in_proj = nn.Linear(d_model, 2 * d_inner, bias=False)
+        self.conv = nn.Conv1d(d_inner, d_inner, d_conv, groups=d_inner, bias=True)
+        # dt initialized log-uniform in [dt_min, dt_max], stored as softplus^-1 (models/mamba.py:40-42)
+        dt = torch.exp(torch.rand(d_inner) * (math.log(dt_max) - math.log(dt_min)) + math.log(dt_min))
+        dt = dt.clamp(min=1e-4)
+        inv_softplus_dt = dt + torch.log(-torch.expm1(-dt))
+        if selective:
+            self.x_proj = nn.Linear(d_inner, self.dt_rank + 2 * d_state, bias=False)
+            self.dt_proj = nn.Linear(self.dt_rank, d_inner, bias=True)
+            self.dt_proj._no_reinit = True
+            std = self.dt_rank ** -0.5
+            with torch.no_grad():
+                nn.init.uniform_(self.dt_proj.weight, -std, std)
+                self.dt_proj.bias.copy_(inv_softplus_dt)
+        else:
+            self.dt_bias = nn.Parameter(inv_softplus_dt)
+            self.B = nn.Parameter(torch.randn(d_state) / math.sqrt(d_state))
+            self.C = nn.Parameter(torch.randn(d_state) / math.sqrt(d_state))
+        if a_mode not in ("s4d", "scalar"):
+            raise ValueError(f"unknown a_mode {a_mode!r}")
+        self.a_mode = a_mode
+        if a_mode == "s4d":   # S4D-real: A_n = -(n + 1) for every channel (models/mamba.py:61)
+            A = torch.arange(1, d_state + 1, dtype=torch.float32).repeat(d_inner, 1)
+        else:                 # one decay per channel shared by the states
+            A = torch.empty(d_inner, 1).uniform_(1.0, 16.0)
+        self.A_log = nn.Parameter(torch.log(A))
+        self.D = nn.Parameter(torch.ones(d_inner))
+        self.out_proj = nn.Linear(d_inner, d_model, bias=False)
+        self.out_proj._residual_out = True
+
+    def ssm_inputs(self, x):
+        """x (B, L, d_inner) -> raw delta (pre bias/softplus), delta bias, A, B, C (views)."""
+        Bsz, L, _ = x.shape
+        ct = torch.promote_types(x.dtype, torch.float32)
+        if self.selective:
+            dt, Bm, Cm = self.x_proj(x).split([self.dt_rank, self.d_state, self.d_state], dim=-1)
+            delta = F.linear(dt, self.dt_proj.weight)          # bias + softplus run in the kernel
+            bias = self.dt_proj.bias
+        else:
+            delta = x.new_zeros(()).expand(Bsz, L, self.d_inner)
+            bias = self.dt_bias
+            Bm = self.B.to(x.dtype).expand(Bsz, L, -1)
+            Cm = self.C.to(x.dtype).expand(Bsz, L, -1)
+        A = -torch.exp(self.A_log.to(ct))
+        if self.a_mode == "scalar":
+            A = A.expand(-1, self.d_state)
+        return delta, bias.to(ct), A, Bm, Cm
+
+    def init_state(self, batch, max_len, device, dtype):
+        return SimpleNamespace(
+            conv=torch.zeros(batch, self.d_inner, self.d_conv - 1, device=device, dtype=dtype),
+            ssm=torch.zeros(batch, self.d_inner, self.d_state, device=device,
+                            dtype=torch.promote_types(dtype, torch.float32)),
+        )
+
+    def forward(self, u, state=None, pos=0):
+        Bsz, L, _ = u.shape
+        x, z = self.in_proj(u).chunk(2, dim=-1)
+        x = causal_conv1d(x, self.conv.weight, self.conv.bias, state=None if state is None else state.conv)
+        delta, bias, A, Bm, Cm = self.ssm_inputs(x)
+        if state is not None and L == 1:                          # recurrent decode step
+            y = ssm_step(state.ssm, x[:, 0], delta[:, 0], A, Bm[:, 0], Cm[:, 0], D=self.D, z=z[:, 0],
+                         delta_bias=bias, delta_softplus=True, method=self.discretization)
+            return self.out_proj(y.unsqueeze(1))
+        h0 = None if state is None else state.ssm
+        y, last = selective_scan_fn(x, delta, A, Bm, Cm, D=self.D, z=z, delta_bias=bias, delta_softplus=True,
+                                    h0=h0, method=self.discretization, return_last_state=True)
+        if state is not None:
+            state.ssm.copy_(last)
+        return self.out_proj(y)
+
+
+class RMSNorm(nn.Module):
+    """models/common.py RMSNorm: x / rms(x) * weight."""
+
+    def __init__(self, d, eps=1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(d))
+
+    def forward(self, x):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)).to(x.dtype) * self.weight
+
+
+class Block(nn.Module):
+    """Pre-norm residual Mamba block (models/lm.py Block with kind "M")."""
+
+    def __init__(self, d_model, **kw):
+        super().__init__()
+        self.norm1 = RMSNorm(d_model)
+        self.mixer = Mamba(d_model, **kw)
+
+    def forward(self, x, state=None, pos=0):
+        return x + self.mixer(self.norm1(x), state, pos)
+
+
+class MambaLM(nn.Module):
+    """The byte-level LM of models/lm.py with n_layers Mamba blocks and tied embeddings."""
+
+    def __init__(self, n_layers=10, vocab_size=256, d_model=256, d_state=16, expand=2, d_conv=4, **kw):
+        super().__init__()
+        self.n_layers = n_layers
+        self.embed = nn.Embedding(vocab_size, d_model)
+        self.blocks = nn.ModuleList([Block(d_model, d_state=d_state, expand=expand, d_conv=d_conv, **kw)
+                                     for _ in range(n_layers)])
+        self.norm_f = RMSNorm(d_model)
+        self.head = nn.Linear(d_model, vocab_size, bias=False)
+        self.head.weight = self.embed.weight
+        self.apply(self._init)
+
+    def _init(self, m):   # models/lm.py:_init
+        if isinstance(m, nn.Linear) and not getattr(m, "_no_reinit", False):
+            std = 0.02 / math.sqrt(2 * self.n_layers) if getattr(m, "_residual_out", False) else 0.02
+            nn.init.normal_(m.weight, 0.0, std)
+            if m.bias is not None:
+                nn.init.zeros_(m.bias)
+        elif isinstance(m, nn.Embedding):
+            nn.init.normal_(m.weight, 0.0, 0.02)
+
+    def num_params(self, non_embedding=True):
+        n = sum(p.numel() for p in self.parameters())
+        return n - self.embed.weight.numel() if non_embedding else n
+
+    def init_state(self, batch, max_len, device, dtype=torch.float32):
+        return [b.mixer.init_state(batch, max_len, device, dtype) for b in self.blocks]
+
+    def forward(self, idx, states=None, pos=0):
+        x = self.embed(idx)
+        for i, block in enumerate(self.blocks):
+            x = block(x, None if states is None else states[i], pos)
+        return self.head(self.norm_f(x))

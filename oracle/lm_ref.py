@@ -1,0 +1,68 @@
+"""torch-CPU float64 restatement of the reference's Mamba LM (test infrastructure only).
+
+Restates models/mamba.py:93-126 (Mamba.forward: in_proj, causal depthwise conv + SiLU,
+x_proj / dt_proj / softplus, selective scan, D skip, SiLU(z) gate, out_proj; the recurrent
+decode step of :113-118 and the state updates of :104-106, :122-123) and models/lm.py
+(pre-norm residual blocks, RMSNorm of models/common.py:8-16, tied head), with the scan as the
+textbook time loop of models/scan.py:264-274, so autograd gives every gradient.  It reads the
+parameters of a model's state_dict by the reference's names.  Used by tests only.
+"""
+
+import torch
+import torch.nn.functional as F
+
+
+def rmsnorm(x, w, eps=1e-5):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+
+
+def discretize(delta, A, Bm, x, method):
+    """models/scan.py:39-55 on (B, D) inputs -> (B, D, N)."""
+    dA = delta.unsqueeze(-1) * A
+    Bx = x.unsqueeze(-1) * Bm.unsqueeze(1)
+    if method == "zoh":
+        return torch.exp(dA), torch.expm1(dA) / A * Bx
+    if method == "euler":
+        return torch.exp(dA), delta.unsqueeze(-1) * Bx
+    inv = 1.0 / (1.0 - 0.5 * dA)
+    return (1.0 + 0.5 * dA) * inv, delta.unsqueeze(-1) * inv * Bx
+
+
+def mamba_layer(p, pre, u, d_state, dt_rank, d_conv, state=None, method="zoh"):
+    """One Mamba mixer on u (B, L, d_model); p maps parameter names (prefix `pre`) to tensors.
+    With `state` (dict conv (B, D, W-1), ssm (B, D, N)) it continues a sequence and updates it."""
+    Bsz, L, _ = u.shape
+    x, z = F.linear(u, p[pre + "in_proj.weight"]).chunk(2, dim=-1)
+    D = x.shape[-1]
+    xc = x.transpose(1, 2)
+    if state is None:
+        xc = F.pad(xc, (d_conv - 1, 0))
+    else:
+        xc = torch.cat([state["conv"], xc], dim=-1)
+        state["conv"] = xc[..., -(d_conv - 1):].clone()
+    x = F.silu(F.conv1d(xc, p[pre + "conv.weight"], p[pre + "conv.bias"], groups=D)).transpose(1, 2)
+    dt, Bm, Cm = F.linear(x, p[pre + "x_proj.weight"]).split([dt_rank, d_state, d_state], dim=-1)
+    delta = F.softplus(F.linear(dt, p[pre + "dt_proj.weight"], p[pre + "dt_proj.bias"]))
+    A = -torch.exp(p[pre + "A_log"])
+    h = torch.zeros(Bsz, D, d_state, dtype=u.dtype) if state is None else state["ssm"]
+    ys = []
+    for t in range(L):
+        a, b = discretize(delta[:, t], A, Bm[:, t], x[:, t], method)
+        h = a * h + b
+        ys.append((h * Cm[:, t].unsqueeze(1)).sum(-1))
+    if state is not None:
+        state["ssm"] = h
+    y = torch.stack(ys, 1)
+    y = (y + x * p[pre + "D"]) * F.silu(z)
+    return F.linear(y, p[pre + "out_proj.weight"])
+
+
+def lm_forward(p, idx, n_layers, d_state=16, dt_rank=16, d_conv=4, states=None, method="zoh"):
+    """Logits (B, L, V) of the Mamba LM (models/lm.py:LM.forward with kind-"M" blocks)."""
+    x = F.embedding(idx, p["embed.weight"])
+    for i in range(n_layers):
+        pre = f"blocks.{i}."
+        h = rmsnorm(x, p[pre + "norm1.weight"])
+        x = x + mamba_layer(p, pre + "mixer.", h, d_state, dt_rank, d_conv,
+                            None if states is None else states[i], method)
+    return F.linear(rmsnorm(x, p["norm_f.weight"]), p["embed.weight"])

@@ -1,0 +1,90 @@
+"""The Mamba LM of models/lm.py (10 Mamba layers, d_model 256, BASELINE config 3's architecture)
+with the scan path on the engine's kernels, against the float64 torch restatement of the
+reference model (oracle/lm_ref.py) on identical weights: logits, loss and every parameter
+gradient; and the recurrent decode path (prefill + one token at a time) against the full
+forward (tests/test_models.py:36-48 of the reference).
+
+Tolerances: float32 through 10 layers -- logits rtol 1e-4 / atol 1e-5 x max|logit|,
+gradients rtol 1e-3 / atol 1e-4 x max|grad| per parameter.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from ssm_scan.block import MambaLM
+from oracle import lm_ref
+from ssm_inputs import np64
+
+pytestmark = pytest.mark.gpu
+
+
+def build(seed=0, n_layers=10):
+    torch.manual_seed(seed)
+    return MambaLM(n_layers=n_layers)
+
+
+def ref_params(model):
+    return {k: v.detach().cpu().double().requires_grad_() for k, v in model.state_dict().items()}
+
+
+def test_lm_forward_backward_matches_reference(dev):
+    model = build(0).to(dev)
+    g = torch.Generator().manual_seed(1)
+    idx = torch.randint(0, 256, (2, 48), generator=g)
+    tgt = torch.randint(0, 256, (2, 48), generator=g)
+    logits = model(idx.to(dev))
+    loss = F.cross_entropy(logits.reshape(-1, 256), tgt.to(dev).reshape(-1))
+    loss.backward()
+    p = ref_params(model)
+    rlogits = lm_ref.lm_forward(p, idx, n_layers=10)
+    rloss = F.cross_entropy(rlogits.reshape(-1, 256), tgt.reshape(-1))
+    rloss.backward()
+    scale = float(rlogits.detach().abs().max())
+    np.testing.assert_allclose(np64(logits), rlogits.detach().numpy(), rtol=1e-4, atol=1e-5 * scale)
+    assert abs(loss.item() - rloss.item()) < 1e-5 * rloss.item()
+    named = dict(model.named_parameters())
+    assert len(named) == len([k for k in p if k != "head.weight"])
+    for name, prm in named.items():
+        ref = p[name].grad.numpy()
+        gs = max(float(np.abs(ref).max()), 1e-12)
+        np.testing.assert_allclose(np64(prm.grad), ref, rtol=1e-3, atol=1e-4 * gs, err_msg=name)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_prefill_and_decode_match_full_forward(dev, batch):
+    model = build(2, n_layers=4).to(dev).eval()
+    g = torch.Generator().manual_seed(3)
+    idx = torch.randint(0, 256, (batch, 40), generator=g).to(dev)
+    with torch.no_grad():
+        full = model(idx)
+        states = model.init_state(batch, 40, dev)
+        out = [model(idx[:, :25], states, 0)]
+        for t in range(25, 40):
+            out.append(model(idx[:, t:t + 1], states, t))
+    got = torch.cat(out, 1)
+    scale = float(full.abs().max())
+    np.testing.assert_allclose(np64(got), np64(full), rtol=1e-4, atol=1e-5 * scale)
+
+
+def test_decode_state_matches_reference(dev):
+    """Token-by-token decode from a random state equals the reference recurrence."""
+    model = build(4, n_layers=2).to(dev).eval()
+    p = {k: v.detach().cpu().double() for k, v in model.state_dict().items()}
+    g = torch.Generator().manual_seed(5)
+    states = model.init_state(4, 8, dev)
+    rstates = []
+    for s in states:
+        s.ssm.copy_(torch.randn(s.ssm.shape, generator=g).to(dev))
+        s.conv.copy_(torch.randn(s.conv.shape, generator=g).to(dev))
+        rstates.append({"conv": s.conv.detach().cpu().double().clone(), "ssm": s.ssm.detach().cpu().double().clone()})
+    idx = torch.randint(0, 256, (4, 6), generator=g)
+    with torch.no_grad():
+        got = torch.cat([model(idx[:, t:t + 1].to(dev), states, t) for t in range(6)], 1)
+    ref = torch.cat([lm_ref.lm_forward(p, idx[:, t:t + 1], n_layers=2, states=rstates) for t in range(6)], 1)
+    scale = float(ref.abs().max())
+    np.testing.assert_allclose(np64(got), ref.numpy(), rtol=1e-4, atol=1e-5 * scale)
+    for s, r in zip(states, rstates):
+        np.testing.assert_allclose(np64(s.ssm), r["ssm"].numpy(), rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(np64(s.conv), r["conv"].numpy(), rtol=1e-6, atol=1e-6)

@@ -375,3 +375,40 @@ def test_discretize_vjp_matches_torch_autograd(method, tiny):
     ((a * torch.tensor(ga)).sum() + (b * torch.tensor(gb)).sum()).backward()
     for got, t in zip(ours, tt):
         np.testing.assert_allclose(got, t.grad.numpy(), rtol=1e-9, atol=1e-12)
+
+
+# --------------------------------------------------------------------------- LM restatement
+
+def test_lm_ref_layer_composes_pinned_oracle_pieces():
+    """oracle/lm_ref.mamba_layer equals in_proj -> conv1d_causal -> selective_scan_fwd (D skip,
+    SiLU gate) -> out_proj built from the pinned numpy oracle; its decode path (state carried
+    one token at a time) equals its full-sequence path."""
+    from oracle import lm_ref
+    g = torch.Generator().manual_seed(0)
+    dm, D, N, R_, W = 8, 16, 4, 2, 4
+    p = {"m.in_proj.weight": torch.randn(2 * D, dm, generator=g, dtype=torch.float64) * 0.3,
+         "m.conv.weight": torch.randn(D, 1, W, generator=g, dtype=torch.float64) * 0.5,
+         "m.conv.bias": torch.randn(D, generator=g, dtype=torch.float64) * 0.1,
+         "m.x_proj.weight": torch.randn(R_ + 2 * N, D, generator=g, dtype=torch.float64) * 0.3,
+         "m.dt_proj.weight": torch.randn(D, R_, generator=g, dtype=torch.float64) * 0.3,
+         "m.dt_proj.bias": torch.randn(D, generator=g, dtype=torch.float64) * 0.3 - 2.0,
+         "m.A_log": torch.log(torch.arange(1, N + 1, dtype=torch.float64).repeat(D, 1)),
+         "m.D": torch.randn(D, generator=g, dtype=torch.float64),
+         "m.out_proj.weight": torch.randn(dm, D, generator=g, dtype=torch.float64) * 0.3}
+    u = torch.randn(2, 11, dm, generator=g, dtype=torch.float64)
+    out = lm_ref.mamba_layer(p, "m.", u, N, R_, W)
+    # the same layer from the numpy oracle pieces
+    xz = u.numpy() @ p["m.in_proj.weight"].numpy().T
+    x, z = xz[..., :D], xz[..., D:]
+    xc, _ = R.conv1d_causal(x.transpose(0, 2, 1), p["m.conv.weight"].numpy()[:, 0], p["m.conv.bias"].numpy())
+    xc = xc.transpose(0, 2, 1)
+    proj = xc @ p["m.x_proj.weight"].numpy().T
+    dt, Bm, Cm = proj[..., :R_], proj[..., R_:R_ + N], proj[..., R_ + N:]
+    delta = np.log1p(np.exp(dt @ p["m.dt_proj.weight"].numpy().T + p["m.dt_proj.bias"].numpy()))
+    A = -np.exp(p["m.A_log"].numpy())
+    o, _, _ = R.selective_scan_fwd(xc, delta, A, Bm, Cm, None, "zoh", p["m.D"].numpy(), z)
+    ref = o @ p["m.out_proj.weight"].numpy().T
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-11, atol=1e-12)
+    state = {"conv": torch.zeros(2, D, W - 1, dtype=torch.float64), "ssm": torch.zeros(2, D, N, dtype=torch.float64)}
+    steps = torch.cat([lm_ref.mamba_layer(p, "m.", u[:, t:t + 1], N, R_, W, state=state) for t in range(11)], 1)
+    np.testing.assert_allclose(steps.numpy(), out.numpy(), rtol=1e-11, atol=1e-12)
