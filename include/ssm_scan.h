@@ -133,6 +133,37 @@ typedef struct ssm_step_args {
   ssm_tensor out;          /* (B,D) dtype */
 } ssm_step_args;
 
+/* ------------------------------------------------------------------ fused decode layer
+ * The scan-path part of one Mamba layer's recurrent decode step (models/mamba.py:93-124 at
+ * L = 1 with a state, preceded by the block's RMSNorm, models/lm.py Block / models/common.py:8-16),
+ * in one launch per layer.  The caller runs the two large projections as GEMMs:
+ *   xz = u @ (W_in diag(norm_w))^T        (in_proj with the RMSNorm weight folded in)
+ * and, after this call, u += y @ W_out^T (out_proj + residual).  Per batch row this step
+ *   s = rsqrt(mean(u^2) + eps);  x = s xz[:, :D], z = s xz[:, D:]      (the RMSNorm scale)
+ *   x = silu(conv(conv_state, x) + conv_bias);  conv_state <- shifted  (models/mamba.py:104-107)
+ *   dt, B, C = x_proj(x);  delta = softplus(dt_proj(dt) + dt_bias)     (:75-76)
+ *   h <- a h + b (ssm_state, in place);  y = (C h + Dskip x) silu(z)   (:113-118, :124)
+ * All tensors float32 and row-major; dstate <= 64; one workgroup per batch row. */
+typedef struct ssm_decode_args {
+  int64_t batch, dim, dstate, width, dt_rank, d_model;
+  int32_t method;          /* SSM_ZOH / SSM_EULER / SSM_BILINEAR */
+  int32_t reserved0;
+  float eps;               /* RMSNorm epsilon */
+  float reserved1;
+  const float *u;          /* (B, d_model) block input (the residual stream) */
+  const float *xz;         /* (B, 2*dim) = u @ (W_in diag(norm_w))^T */
+  const float *conv_w;     /* (dim, width) */
+  const float *conv_b;     /* (dim,) */
+  float *conv_state;       /* (B, dim, width-1), updated in place */
+  const float *x_proj_wt;  /* (dim, dt_rank + 2*dstate): x_proj's weight transposed */
+  const float *dt_proj_w;  /* (dim, dt_rank) */
+  const float *dt_bias;    /* (dim,) */
+  const float *A_log;      /* (dim, dstate): A = -exp(A_log) */
+  const float *Dskip;      /* (dim,) */
+  float *ssm_state;        /* (B, dim, dstate), updated in place */
+  float *y;                /* (B, dim) output, the input of out_proj */
+} ssm_decode_args;
+
 /* ------------------------------------------------------------------ linear scans
  * Replaces the scan algorithms of models/scan.py:70-165 (scan_sequential,
  * scan_hillis_steele, scan_blelloch, scan_chunked) on (a, b) of shape (B, L, M):
@@ -219,6 +250,7 @@ const char *ssm_last_error(void);
 int ssm_fwd_check(const ssm_fwd_args *args);
 int ssm_bwd_check(const ssm_bwd_args *args);
 int ssm_step_check(const ssm_step_args *args);
+int ssm_decode_check(const ssm_decode_args *args);
 int ssm_lscan_check(const ssm_lscan_args *args);
 int ssm_lscan_bwd_check(const ssm_lscan_bwd_args *args);
 int ssm_disc_check(const ssm_disc_args *args);
@@ -237,6 +269,7 @@ int64_t ssm_conv_workspace_bytes(const ssm_conv_args *args);
 int ssm_fwd(const ssm_fwd_args *args, void *stream);
 int ssm_bwd(const ssm_bwd_args *args, void *stream);
 int ssm_step(const ssm_step_args *args, void *stream);
+int ssm_decode_step(const ssm_decode_args *args, void *stream);
 int ssm_lscan(const ssm_lscan_args *args, void *stream);
 int ssm_lscan_bwd(const ssm_lscan_bwd_args *args, void *stream);
 int ssm_disc_fwd(const ssm_disc_args *args, void *stream);

@@ -587,6 +587,39 @@ int ssm_disc_bwd(const ssm_disc_args *a, void *stream) {
   return e == hipSuccess ? ok() : hip_fail(e, "ssm_disc_bwd");
 }
 
+// ------------------------------------------------------------------ fused decode layer
+int ssm_decode_check(const ssm_decode_args *a) {
+  if (!a) return fail(SSM_EINVAL, "null args");
+  if (a->method < 0 || a->method > 2)
+    return fail(SSM_EINVAL, "unknown discretization %d (expected zoh=0, euler=1, bilinear=2)", a->method);
+  if (a->batch < 1 || a->dim < 1 || a->dstate < 1 || a->d_model < 1 || a->dt_rank < 1)
+    return fail(SSM_EINVAL, "empty decode layer");
+  if (a->batch > 65535 * 32767LL) return fail(SSM_EINVAL, "batch too large");
+  if (a->width < 1 || a->width > 8) return fail(SSM_EINVAL, "conv width %lld not in 1..8", (long long)a->width);
+  if (a->dstate > 64 || a->dt_rank > 256 || a->dim > 8192)
+    return fail(SSM_EINVAL, "decode layer dims out of range (dim <= 8192, dstate <= 64, dt_rank <= 256)");
+  if (!a->u || !a->xz || !a->conv_w || !a->conv_b || !a->conv_state || !a->x_proj_wt || !a->dt_proj_w ||
+      !a->dt_bias || !a->A_log || !a->Dskip || !a->ssm_state || !a->y)
+    return fail(SSM_EINVAL, "a required decode tensor is missing");
+  return ok();
+}
+
+int ssm_decode_step(const ssm_decode_args *a, void *stream) {
+  int rc = ssm_decode_check(a);
+  if (rc) return rc;
+  DecodeParams p;
+  memset(&p, 0, sizeof(p));
+  p.B = a->batch; p.dim = a->dim; p.N = a->dstate; p.W = a->width; p.R = a->dt_rank; p.dm = a->d_model;
+  p.P = a->dt_rank + 2 * a->dstate;
+  p.eps = a->eps;
+  p.u = a->u; p.xz = a->xz; p.conv_w = a->conv_w; p.conv_b = a->conv_b; p.x_proj_wt = a->x_proj_wt;
+  p.dt_proj_w = a->dt_proj_w; p.dt_bias = a->dt_bias; p.A_log = a->A_log; p.Dskip = a->Dskip;
+  p.conv_state = a->conv_state; p.ssm_state = a->ssm_state; p.y = a->y;
+  if (decode_shared_bytes(p) > 64 * 1024) return fail(SSM_EINVAL, "decode layer too wide for one workgroup");
+  hipError_t e = launch_decode(p, a->method, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "ssm_decode_step");
+}
+
 // ------------------------------------------------------------------ causal depthwise conv
 static constexpr int kConvTB = 64;  // time steps per lane
 

@@ -145,6 +145,14 @@ struct ConvParams {
   void *ws;  // backward: (B * nblk, D, W + 1) partial dweight / dbias
 };
 
+// Fused decode layer (float32, row-major); one workgroup per batch row.
+struct DecodeParams {
+  int64_t B, dim, N, W, R, dm, P;  // P = R + 2 N
+  float eps;
+  const float *u, *xz, *conv_w, *conv_b, *x_proj_wt, *dt_proj_w, *dt_bias, *A_log, *Dskip;
+  float *conv_state, *ssm_state, *y;
+};
+
 // Runs the summary and carry passes first when p.nseg > 1.
 hipError_t launch_fwd(const FwdParams &p, int dtype, int method, int np, hipStream_t s);
 hipError_t launch_bwd(const BwdParams &p, int dtype, int method, int np, hipStream_t s);
@@ -155,6 +163,8 @@ hipError_t launch_lscan_grad(const LscanGradParams &p, int dtype, hipStream_t s)
 // Channels per workgroup of the discretize backward (its dB partial-sum tile).
 inline int disc_channels(int np) { return kThreads / np; }
 hipError_t launch_conv(const ConvParams &p, int dtype, bool bwd, hipStream_t s);
+size_t decode_shared_bytes(const DecodeParams &p);
+hipError_t launch_decode(const DecodeParams &p, int method, hipStream_t s);
 hipError_t launch_disc_fwd(const DiscParams &p, int dtype, int method, int np, hipStream_t s);
 hipError_t launch_disc_bwd(const DiscParams &p, int dtype, int method, int np, hipStream_t s);
 

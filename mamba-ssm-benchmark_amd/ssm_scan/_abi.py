@@ -59,6 +59,15 @@ class StepArgs(ctypes.Structure):
                 ("h", Tensor), ("out", Tensor)]
 
 
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [("batch", c_i64), ("dim", c_i64), ("dstate", c_i64), ("width", c_i64), ("dt_rank", c_i64),
+                ("d_model", c_i64), ("method", c_i32), ("reserved0", c_i32),
+                ("eps", ctypes.c_float), ("reserved1", ctypes.c_float),
+                ("u", c_vp), ("xz", c_vp), ("conv_w", c_vp), ("conv_b", c_vp), ("conv_state", c_vp),
+                ("x_proj_wt", c_vp), ("dt_proj_w", c_vp), ("dt_bias", c_vp), ("A_log", c_vp), ("Dskip", c_vp),
+                ("ssm_state", c_vp), ("y", c_vp)]
+
+
 class LscanArgs(ctypes.Structure):
     _fields_ = [("batch", c_i64), ("seqlen", c_i64), ("width", c_i64),
                 ("algo", c_i32), ("dtype", c_i32), ("reverse", c_i32), ("reserved0", c_i32),
@@ -101,6 +110,7 @@ _SIGS = {
     "ssm_fwd_check": (c_i32, [ctypes.POINTER(FwdArgs)]),
     "ssm_bwd_check": (c_i32, [ctypes.POINTER(BwdArgs)]),
     "ssm_step_check": (c_i32, [ctypes.POINTER(StepArgs)]),
+    "ssm_decode_check": (c_i32, [ctypes.POINTER(DecodeArgs)]),
     "ssm_lscan_check": (c_i32, [ctypes.POINTER(LscanArgs)]),
     "ssm_lscan_bwd_check": (c_i32, [ctypes.POINTER(LscanBwdArgs)]),
     "ssm_disc_check": (c_i32, [ctypes.POINTER(DiscArgs)]),
@@ -115,6 +125,7 @@ _SIGS = {
     "ssm_fwd": (c_i32, [ctypes.POINTER(FwdArgs), c_vp]),
     "ssm_bwd": (c_i32, [ctypes.POINTER(BwdArgs), c_vp]),
     "ssm_step": (c_i32, [ctypes.POINTER(StepArgs), c_vp]),
+    "ssm_decode_step": (c_i32, [ctypes.POINTER(DecodeArgs), c_vp]),
     "ssm_lscan": (c_i32, [ctypes.POINTER(LscanArgs), c_vp]),
     "ssm_lscan_bwd": (c_i32, [ctypes.POINTER(LscanBwdArgs), c_vp]),
     "ssm_disc_fwd": (c_i32, [ctypes.POINTER(DiscArgs), c_vp]),

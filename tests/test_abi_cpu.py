@@ -44,7 +44,7 @@ def test_library_exports_every_declared_function():
 
 def test_ctypes_layout_matches_c_header(tmp_path):
     structs = {"ssm_tensor": _abi.Tensor, "ssm_fwd_args": _abi.FwdArgs, "ssm_bwd_args": _abi.BwdArgs,
-               "ssm_step_args": _abi.StepArgs, "ssm_lscan_args": _abi.LscanArgs,
+               "ssm_step_args": _abi.StepArgs, "ssm_decode_args": _abi.DecodeArgs, "ssm_lscan_args": _abi.LscanArgs,
                "ssm_lscan_bwd_args": _abi.LscanBwdArgs,
                "ssm_disc_args": _abi.DiscArgs, "ssm_conv_args": _abi.ConvArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]

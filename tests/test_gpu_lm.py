@@ -88,3 +88,70 @@ def test_decode_state_matches_reference(dev):
     for s, r in zip(states, rstates):
         np.testing.assert_allclose(np64(s.ssm), r["ssm"].numpy(), rtol=1e-4, atol=1e-5)
         np.testing.assert_allclose(np64(s.conv), r["conv"].numpy(), rtol=1e-6, atol=1e-6)
+
+
+def _random_states(model, B, dev, seed):
+    g = torch.Generator().manual_seed(seed)
+    states = model.init_state(B, 1, dev)
+    for s in states:
+        s.ssm.copy_(torch.randn(s.ssm.shape, generator=g))
+        s.conv.copy_(torch.randn(s.conv.shape, generator=g))
+    return states
+
+
+def _clone(states):
+    from types import SimpleNamespace
+    return [SimpleNamespace(conv=s.conv.clone(), ssm=s.ssm.clone()) for s in states]
+
+
+def test_fused_decode_layer_matches_module_decode(dev):
+    """ssm_decode_step (one fused launch per layer) == the module's decode path, incl. states."""
+    from ssm_scan.decode import FastDecoder
+    model = build(6, n_layers=10).to(dev).eval()
+    fast = FastDecoder(model)
+    s_ref = _random_states(model, 64, dev, 7)
+    s_fast = _clone(s_ref)
+    toks = torch.randint(0, 256, (8, 64, 1), generator=torch.Generator().manual_seed(8)).to(dev)
+    with torch.no_grad():
+        for t in range(8):
+            ref = model(toks[t], s_ref, t)[:, 0]
+            got = fast.step(toks[t], s_fast)
+            scale = float(ref.abs().max())
+            np.testing.assert_allclose(np64(got), np64(ref), rtol=1e-4, atol=1e-5 * scale)
+    for a, b_ in zip(s_fast, s_ref):
+        np.testing.assert_allclose(np64(a.ssm), np64(b_.ssm), rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(np64(a.conv), np64(b_.conv), rtol=1e-5, atol=1e-6)
+
+
+def test_fused_decode_graph_replays_match_eager(dev):
+    """The token step captured in a HIP graph: every replay (with eager work between) equals the
+    eager step from the same states and token."""
+    from ssm_scan.decode import FastDecoder
+    model = build(9, n_layers=3).to(dev).eval()
+    fast = FastDecoder(model)
+    states = _random_states(model, 16, dev, 10)
+    tok = torch.zeros(16, 1, dtype=torch.long, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        snap = _clone(states)
+        fast.step(tok, states)                       # warm-up on the side stream
+        for s, c in zip(states, snap):
+            s.conv.copy_(c.conv)
+            s.ssm.copy_(c.ssm)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fast.step(tok, states)
+    g = torch.Generator().manual_seed(11)
+    for r in range(4):
+        before = _clone(states)
+        tok.copy_(torch.randint(0, 256, (16, 1), generator=g))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager_states = before
+        ref = fast.step(tok, eager_states)           # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), r
+        for a, b_ in zip(states, eager_states):
+            assert torch.equal(a.ssm, b_.ssm) and torch.equal(a.conv, b_.conv)
