@@ -134,9 +134,170 @@ __global__ void __launch_bounds__(kDecThreads) k_decode(const DecodeParams p) {
   }
 }
 
+// Row-resident variant for the Mamba LM shapes: dim <= 512, dstate 8 or 16, dt_rank 8, 16 or
+// 32, d_model <= 1024, conv width <= 4.  Every global read of the row is issued at entry,
+// unconditionally and in the order of use (raw buffer reads: past an array's end they return
+// 0), so the row costs one memory round trip; the phases after it meet only at LDS barriers and
+// every global store comes last.  Thread roles: norm element tid; conv channel tid; x_proj
+// wavefront g = channels g, g + 16, ..., lane = output; state pair (2 d, 2 d + 1) = channel d's
+// two halves of the states and of the dt rank.
+constexpr int kRowGroupCh = 32;  // channels per x_proj wavefront (dim <= 16 * 32)
+
+template <int W, int NPH, int RHALF, int METHOD>
+__global__ void __launch_bounds__(kDecThreads) k_decode_row(const DecodeParams p) {
+  constexpr int NW = kDecThreads / kWave, N = 2 * NPH, R = 2 * RHALF;
+  __shared__ float xs[NW * kRowGroupCh];
+  __shared__ float part[NW][kWave];
+  __shared__ float proj[kWave];
+  __shared__ float red[NW];
+  const int tid = threadIdx.x, lane = tid % kWave, wv = tid / kWave;
+  const int64_t b = blockIdx.x;
+  const int Dm = (int)p.dim, dm = (int)p.dm, P = (int)p.P;
+
+  // raw buffer views (32-bit lane offsets, reads past an extent return 0)
+  auto view = [](const float *q, int64_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)q, (short)0, (int)(n * 4), kBufferFlags);
+  };
+  const auto ru = view(p.u + b * dm, dm), rxz = view(p.xz + b * 2 * Dm, 2 * Dm);
+  const auto rcs = view(p.conv_state + b * Dm * (W - 1), Dm * (W - 1)), rcw = view(p.conv_w, Dm * W);
+  const auto rcb = view(p.conv_b, Dm), rxp = view(p.x_proj_wt, (int64_t)Dm * P);
+  const auto rdt = view(p.dt_proj_w, (int64_t)Dm * R), rdb = view(p.dt_bias, Dm), rds = view(p.Dskip, Dm);
+  const auto rh = view(p.ssm_state + b * Dm * N, Dm * N), ral = view(p.A_log, Dm * N);
+  auto ld = [](__amdgpu_buffer_rsrc_t r, int idx) { return buf_load<float>(r, (uint32_t)idx * 4u); };
+
+  const float uv = ld(ru, tid);  // 0 past d_model
+  const float xin = ld(rxz, tid);
+  float cw[W], st[W > 1 ? W - 1 : 1];
+#pragma unroll
+  for (int j = 0; j < W; ++j) cw[j] = ld(rcw, tid * W + j);
+#pragma unroll
+  for (int j = 0; j < W - 1; ++j) st[j] = ld(rcs, tid * (W - 1) + j);
+  const float cb = ld(rcb, tid);
+
+  // x_proj weight rows g + 16 k (rows past dim read 0; lanes past P read unused values)
+  const int g = __builtin_amdgcn_readfirstlane(wv);
+  float wx[kRowGroupCh];
+#pragma unroll
+  for (int k = 0; k < kRowGroupCh; ++k) wx[k] = ld(rxp, (g + NW * k) * P + lane);
+
+  const int ds = tid >> 1, half = tid & 1, n0 = half * NPH, r0 = half * RHALF;
+  float wdt[RHALF];
+#pragma unroll
+  for (int i = 0; i < RHALF; ++i) wdt[i] = ld(rdt, ds * R + r0 + i);
+  const float dtb = ld(rdb, ds), dsk = ld(rds, ds), zin = ld(rxz, Dm + ds);
+  float hr[NPH], lr[NPH];
+#pragma unroll
+  for (int i = 0; i < NPH; ++i) hr[i] = ld(rh, ds * N + n0 + i);
+#pragma unroll
+  for (int i = 0; i < NPH; ++i) lr[i] = ld(ral, ds * N + n0 + i);
+
+  // RMSNorm scale of the block input (its weight is folded into in_proj by the caller)
+  float ss = uv * uv;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  if (lane == 0) red[wv] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) tot += red[w];
+  const float s = rsqrtf(tot / (float)dm + p.eps);
+
+  // conv step + SiLU (models/mamba.py:104-107); channels past dim hold 0 for x_proj
+  const float x = s * xin;
+  float acc = fmaf(cw[W - 1], x, cb);
+#pragma unroll
+  for (int j = 0; j < W - 1; ++j) acc = fmaf(cw[j], st[j], acc);
+  if (tid < NW * kRowGroupCh) xs[tid] = tid < Dm ? acc * sigmoidf(acc) : 0.f;
+  __syncthreads();
+
+  // x_proj partial sums per channel group, then the groups in a fixed order
+  float pa = 0.f;
+#pragma unroll
+  for (int k = 0; k < kRowGroupCh; ++k) pa = fmaf(wx[k], xs[g + NW * k], pa);
+  part[wv][lane] = pa;
+  __syncthreads();
+  if (tid < kWave) {
+    float a = 0.f;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) a += part[q][tid];
+    proj[tid] = a;
+  }
+  __syncthreads();
+
+  // dt_proj (each lane of the pair takes half of the rank) + bias + softplus
+  float dp = 0.f;
+#pragma unroll
+  for (int i = 0; i < RHALF; ++i) dp = fmaf(wdt[i], proj[r0 + i], dp);
+  const float dt = softplusf(dtb + (dp + __shfl_xor(dp, 1)));
+
+  // state update, C h, skip and gate
+  const float xc = xs[min(ds, Dm - 1)];
+  const float *Bv = proj + R + n0, *Cv = proj + R + N + n0;
+  float y = 0.f;
+#pragma unroll
+  for (int i = 0; i < NPH; ++i) {
+    AConst<float> ac;
+    ac.A = -__expf(lr[i]);
+    ac.A2 = ac.A * 1.4426950408889634f;
+    ac.invA = fast_rcp(ac.A);
+    float a, coef, hv = hr[i];
+    const float bx = Bv[i] * xc;
+    if constexpr (METHOD == 0) {
+      disc_zoh_m1(dt, ac, a, coef);  // a holds a - 1
+      hv = fmaf(a, hv, fmaf(coef, bx, hv));
+    } else {
+      disc<METHOD>(dt, ac, a, coef);
+      hv = fmaf(a, hv, bcoef<METHOD>(dt, coef) * bx);
+    }
+    hr[i] = hv;
+    y = fmaf(Cv[i], hv, y);
+  }
+  y += __shfl_xor(y, 1);
+
+  if (ds < Dm) {
+    float *h = p.ssm_state + (b * Dm + ds) * N + n0;
+#pragma unroll
+    for (int i = 0; i < NPH; ++i) h[i] = hr[i];
+    if (half == 0) {
+      const float zv = s * zin;
+      p.y[b * Dm + ds] = fmaf(dsk, xc, y) * (zv * sigmoidf(zv));
+    }
+  }
+  if (tid < Dm) {
+    float *cst = p.conv_state + (b * Dm + tid) * (W - 1);
+#pragma unroll
+    for (int j = 0; j + 1 < W - 1; ++j) cst[j] = st[j + 1];
+    if constexpr (W > 1) cst[W - 2] = x;
+  }
+}
+
+bool decode_row_fits(const DecodeParams &p) {
+  return p.dim <= kDecThreads / 2 && p.dim <= (int64_t)(kDecThreads / kWave) * kRowGroupCh &&
+         (p.N == 8 || p.N == 16) && (p.R == 8 || p.R == 16 || p.R == 32) && p.P <= kWave &&
+         p.dm <= kDecThreads && p.W <= 4;
+}
+
+template <int W, int NPH, int RHALF>
+static void launch_row(const DecodeParams &p, int method, hipStream_t s) {
+  const dim3 grid((unsigned)p.B), block(kDecThreads);
+  switch (method) {
+    case 0: hipLaunchKernelGGL((k_decode_row<W, NPH, RHALF, 0>), grid, block, 0, s, p); break;
+    case 1: hipLaunchKernelGGL((k_decode_row<W, NPH, RHALF, 1>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((k_decode_row<W, NPH, RHALF, 2>), grid, block, 0, s, p); break;
+  }
+}
+
 template <int W, int NP>
 static hipError_t decode_m(const DecodeParams &p, int method, size_t shmem, hipStream_t s) {
   const dim3 grid((unsigned)p.B), block(kDecThreads);
+  if constexpr (NP <= 16 && W <= 4) {
+    if (decode_row_fits(p) && p.N == NP) {
+      if (p.R == 8) launch_row<W, NP / 2, 4>(p, method, s);
+      else if (p.R == 16) launch_row<W, NP / 2, 8>(p, method, s);
+      else launch_row<W, NP / 2, 16>(p, method, s);
+      return hipGetLastError();
+    }
+  }
   switch (method) {
     case 0: hipLaunchKernelGGL((k_decode<W, NP, 0>), grid, block, shmem, s, p); break;
     case 1: hipLaunchKernelGGL((k_decode<W, NP, 1>), grid, block, shmem, s, p); break;

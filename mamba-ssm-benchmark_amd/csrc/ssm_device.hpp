@@ -82,7 +82,23 @@ __device__ __forceinline__ float fseries(float z) {
                   1.0f / 3.0f), 0.5f);
 }
 
-__device__ __forceinline__ float softplusf(float v) { return v > 20.0f ? v : log1pf(__expf(v)); }
+// softplus(v) = max(v, 0) + log1p(w), w = exp(-|v|) in (0, 1], with log1p(w) = 2 atanh(s),
+// s = w / (2 + w) <= 1/3, summed as 2 s (1 + s^2/3 + ... + s^14/15) (truncation < 2e-9 relative).
+// Within 5 ulp of the exact value over all v (float32 emulation, worst-case rcp rounding); equals
+// v for v > 20 like the thresholded softplus of the reference (models/mamba.py:76).
+__device__ __forceinline__ float softplusf(float v) {
+  const float w = __expf(-fabsf(v));
+  const float s = w * fast_rcp(2.0f + w);
+  const float t = s * s;
+  float q = fmaf(t, 1.0f / 15.0f, 1.0f / 13.0f);
+  q = fmaf(q, t, 1.0f / 11.0f);
+  q = fmaf(q, t, 1.0f / 9.0f);
+  q = fmaf(q, t, 1.0f / 7.0f);
+  q = fmaf(q, t, 1.0f / 5.0f);
+  q = fmaf(q, t, 1.0f / 3.0f);
+  q = fmaf(q, t, 1.0f);
+  return fmaxf(v, 0.0f) + 2.0f * s * q;
+}
 __device__ __forceinline__ double softplusd(double v) { return v > 20.0 ? v : log1p(exp(v)); }
 __device__ __forceinline__ float sigmoidf(float v) { return fast_rcp(1.0f + __expf(-v)); }
 __device__ __forceinline__ double sigmoidd(double v) { return 1.0 / (1.0 + exp(-v)); }

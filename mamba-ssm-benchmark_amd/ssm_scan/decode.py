@@ -5,7 +5,7 @@ Per layer the token step is
     ssm_decode_step(...)                    one fused launch: RMSNorm scale, conv step + SiLU
                                             with the conv state, x_proj, dt_proj + softplus, the
                                             state update, D skip and SiLU(z) gate
-    u = u + y @ W_out^T                     one GEMM with the residual (addmm)
+    u += y @ W_out^T                        one GEMM with the residual, in place (addmm_)
 which computes what models/mamba.py:93-124 (L = 1 with a state) and the pre-norm residual
 block of models/lm.py compute, in place of ~20 small launches per layer.  The step is
 allocation-free apart from torch's caching allocator, so it can be captured in a HIP graph.
@@ -64,7 +64,7 @@ class FastDecoder:
         a.ssm_state, a.y = state.ssm.data_ptr(), y.data_ptr()
         rc = _abi.lib().ssm_decode_step(ctypes.byref(a), _abi.stream_handle(u.device))
         _abi.check(rc, "ssm_decode_step")
-        return torch.addmm(u, y, L["w_out_t"])
+        return u.addmm_(y, L["w_out_t"])     # residual in place: u is this step's own buffer
 
     @torch.no_grad()
     def step(self, tok, states):
@@ -80,7 +80,7 @@ class FastDecoder:
         prev = torch.backends.cuda.preferred_blas_library()
         torch.backends.cuda.preferred_blas_library("cublas")   # rocBLAS on ROCm
         try:
-            u = self.model.embed(tok.reshape(-1))
+            u = self.model.embed(tok.reshape(-1))          # a fresh buffer, updated in place
             for L, s in zip(self.layers, states):
                 u = self._layer(L, u, s)
             return self.model.head(self.model.norm_f(u))

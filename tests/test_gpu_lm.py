@@ -104,10 +104,23 @@ def _clone(states):
     return [SimpleNamespace(conv=s.conv.clone(), ssm=s.ssm.clone()) for s in states]
 
 
-def test_fused_decode_layer_matches_module_decode(dev):
+# the LM shape and dstate 8 / bilinear, dim 256 / dt_rank 8 / width 2 (row-resident kernel);
+# dstate 12 and a wider layer (dim 768, dt_rank 24), which take the general kernel
+DECODE_SHAPES = [
+    dict(n_layers=10),
+    dict(n_layers=3, d_state=8, discretization="bilinear"),
+    dict(n_layers=3, d_state=12, d_conv=3, discretization="euler"),
+    dict(n_layers=2, d_model=384),
+    dict(n_layers=2, d_model=128, d_conv=2, discretization="euler"),
+]
+
+
+@pytest.mark.parametrize("shape", DECODE_SHAPES, ids=lambda s: "-".join(f"{k}{v}" for k, v in s.items()))
+def test_fused_decode_layer_matches_module_decode(dev, shape):
     """ssm_decode_step (one fused launch per layer) == the module's decode path, incl. states."""
     from ssm_scan.decode import FastDecoder
-    model = build(6, n_layers=10).to(dev).eval()
+    torch.manual_seed(6)
+    model = MambaLM(**shape).to(dev).eval()
     fast = FastDecoder(model)
     s_ref = _random_states(model, 64, dev, 7)
     s_fast = _clone(s_ref)
