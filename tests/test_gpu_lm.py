@@ -168,3 +168,109 @@ def test_fused_decode_graph_replays_match_eager(dev):
         assert torch.equal(out, ref), r
         for a, b_ in zip(states, eager_states):
             assert torch.equal(a.ssm, b_.ssm) and torch.equal(a.conv, b_.conv)
+
+
+def test_streaming_prefill_matches_one_call(dev):
+    """Prefill in pieces (conv and SSM states carried, pieces of length 1 take the decode step)
+    equals one prefill call over the whole input, logits and final states
+    (analysis/length_generalization.py:110-116 streams inputs this way)."""
+    model = build(12, n_layers=3).to(dev).eval()
+    g = torch.Generator().manual_seed(13)
+    idx = torch.randint(0, 256, (2, 60), generator=g).to(dev)
+    with torch.no_grad():
+        s_one = model.init_state(2, 60, dev)
+        full = model(idx, s_one, 0)
+        s_str = model.init_state(2, 60, dev)
+        parts, p0 = [], 0
+        for n in (7, 16, 1, 1, 20, 3, 12):
+            parts.append(model(idx[:, p0:p0 + n], s_str, p0))
+            p0 += n
+    assert p0 == 60
+    scale = float(full.abs().max())
+    np.testing.assert_allclose(np64(torch.cat(parts, 1)), np64(full), rtol=1e-4, atol=1e-5 * scale)
+    for a, b_ in zip(s_str, s_one):
+        np.testing.assert_allclose(np64(a.ssm), np64(b_.ssm), rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(np64(a.conv), np64(b_.conv), rtol=1e-5, atol=1e-6)
+    assert torch.equal(s_str[0].conv, s_one[0].conv)      # first layer: the same in_proj inputs
+
+
+def test_streaming_prefill_under_bf16_autocast(dev):
+    """The reference streams under torch.autocast(bf16) with float32 states; the pieces equal
+    one autocast call over the whole input to bf16 accuracy (2e-2 x max|logit|)."""
+    model = build(14, n_layers=2).to(dev).eval()
+    idx = torch.randint(0, 256, (1, 48), generator=torch.Generator().manual_seed(15)).to(dev)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        full = model(idx).float()
+        st = model.init_state(1, 48, dev, torch.float32)
+        parts = [model(idx[:, p0:p0 + 16], st, p0).float() for p0 in range(0, 48, 16)]
+    scale = float(full.abs().max())
+    np.testing.assert_allclose(np64(torch.cat(parts, 1)), np64(full), rtol=0, atol=2e-2 * scale)
+    assert all(s.ssm.dtype == torch.float32 and s.conv.dtype == torch.float32 for s in st)
+
+
+@pytest.mark.parametrize("scan", ["chunked", "blelloch"])
+def test_named_scan_algorithm_matches_fused(dev, scan):
+    """Mamba(scan=<algorithm of models/scan.py>) runs that algorithm on the engine; forward
+    and gradients equal the fused kernel's (models/lm.py:70-71 passes cfg.scan through)."""
+    torch.manual_seed(16)
+    fused = MambaLM(n_layers=2).to(dev)
+    named = MambaLM(n_layers=2, scan=scan, chunk_size=8).to(dev)
+    named.load_state_dict(fused.state_dict())
+    idx = torch.randint(0, 256, (2, 40), generator=torch.Generator().manual_seed(17)).to(dev)
+    outs = []
+    for m in (fused, named):
+        logits = m(idx)
+        logits.square().mean().backward()
+        outs.append((logits, {k: p.grad for k, p in m.named_parameters()}))
+    scale = float(outs[0][0].detach().abs().max())
+    np.testing.assert_allclose(np64(outs[1][0]), np64(outs[0][0]), rtol=1e-4, atol=1e-5 * scale)
+    for k, g0 in outs[0][1].items():
+        gs = max(float(g0.abs().max()), 1e-12)
+        np.testing.assert_allclose(np64(outs[1][1][k]), np64(g0), rtol=1e-3, atol=1e-4 * gs, err_msg=k)
+
+
+def test_lti_ablation_has_constant_delta(dev):
+    """selective=False freezes delta to a learned constant (tests/test_models.py:60-64)."""
+    torch.manual_seed(18)
+    m = MambaLM(n_layers=1, d_model=32, selective=False).to(dev)
+    u = torch.randn(2, 10, 32, device=dev)
+    _, delta = m.blocks[0].mixer(u, return_delta=True)
+    assert torch.equal(delta, delta[:, :1].expand_as(delta))
+
+
+def test_scalar_decay_shares_decay_and_decodes_consistently(dev):
+    """a_mode="scalar": one decay per channel; prefill + decode equals the full forward
+    (tests/test_models.py:144-155)."""
+    torch.manual_seed(19)
+    m = MambaLM(n_layers=2, d_model=64, a_mode="scalar").to(dev).eval()
+    mixer = m.blocks[0].mixer
+    _, A, _, _ = mixer.ssm_params(torch.randn(1, 3, mixer.d_inner, device=dev))
+    assert torch.equal(A, A[:, :1].expand_as(A))
+    x = torch.randint(0, 256, (2, 25), generator=torch.Generator().manual_seed(20)).to(dev)
+    with torch.no_grad():
+        full = m(x)
+        st = m.init_state(2, 25, dev)
+        parts = [m(x[:, :9], st, 0)] + [m(x[:, t:t + 1], st, t) for t in range(9, 25)]
+    scale = float(full.abs().max())
+    np.testing.assert_allclose(np64(torch.cat(parts, 1)), np64(full), rtol=1e-4, atol=1e-5 * scale)
+
+
+def test_generate_and_checkpoint_round_trip(dev):
+    """generate() (models/lm.py:130-147) is reproducible under a seed, and a checkpoint in the
+    training script's format reloads to the same logits."""
+    import io
+    from ssm_scan.block import load_checkpoint
+    model = build(21, n_layers=2).to(dev).eval()
+    prompt = torch.randint(0, 256, (2, 5), generator=torch.Generator().manual_seed(22)).to(dev)
+    torch.manual_seed(23)
+    a = model.generate(prompt, 6, temperature=0.8, top_k=20)
+    torch.manual_seed(23)
+    b = model.generate(prompt, 6, temperature=0.8, top_k=20)
+    assert a.shape == (2, 11) and torch.equal(a, b) and torch.equal(a[:, :5], prompt)
+    buf = io.BytesIO()
+    cfg = dict(layers="MM", vocab_size=256, d_model=256, d_state=16, expand=2, d_conv=4)
+    torch.save({"cfg": cfg, "state_dict": model.state_dict()}, buf)
+    buf.seek(0)
+    again = load_checkpoint(buf, dev)
+    with torch.no_grad():
+        assert torch.equal(again(prompt), model(prompt))
