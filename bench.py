@@ -4,12 +4,13 @@
 Metric: selective-scan fwd+bwd Mtok/s and % HBM peak at B16 L512 D512 N16
 fp32 (config 1: z gate + D skip, upstream grad dy ~ N(0,1)).  A step is one forward and one
 backward of the fused scan over the batch, inputs resident in HBM.  W untimed warmup steps,
-then exactly K steps between two torch.cuda.synchronize() calls.  The step is timed twice:
-eager (Python + autograd launch every step; the kernels' HIP-event timer is off in the timed
-loop) and captured once in a HIP graph and replayed (the replayed outputs are checked bitwise
-against the eager step's).  `value` is the graph replay, which does not depend on how fast the
-host issues launches (the eager step is host-bound on a busy host); `--eager` reports the
-eager step instead.  Both times are in the record.
+then exactly K steps between two torch.cuda.synchronize() calls.  The step is timed in two
+launch modes in the same run: eager (Python + autograd launch every step; the kernels' HIP-event
+timer is off in the timed loop) and captured once in a HIP graph and replayed (the replayed
+outputs are checked bitwise against the eager step's).  `value` is the faster of the two and
+`step_mode` names it: the eager step is host-bound when the host is busy, while a graph replay
+adds a fixed launch gap of several microseconds.  `--eager` times the eager step only.  Both
+times are in the record.
 
 Per-entry device times come from HIP events recorded on the launch stream around every
 C-ABI call (ssm_scan.KernelTimer); the dominant entry (ssm_bwd: the backward kernel plus its
@@ -113,6 +114,42 @@ def flush_buffer(dev):
     return torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
 
 
+def time_steps(step, args):
+    """(eager ms/step, graph-replay ms/step or None, replay outputs == eager outputs or None).
+
+    Eager: W warmup steps, then K steps between two synchronizations.  Graph: the step captured
+    once on a side stream and replayed W + K times; the replay's outputs are compared bitwise
+    with the eager step's (the kernels are deterministic)."""
+    for _ in range(args.warmup):
+        ref = step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    if args.eager:
+        return eager_ms, None, None
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout = step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ok = all(torch.equal(a, b) for a, b in zip(gout, ref))
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return eager_ms, (time.perf_counter() - t0) * 1e3 / args.steps, ok
+
+
 def bench_c1(args, dev):
     import ssm_scan
     from ssm_scan.synthetic import baseline_inputs
@@ -127,38 +164,8 @@ def bench_c1(args, dev):
                                          D=leaves[5], z=leaves[6])
         return torch.autograd.grad(out, leaves, dy)
 
-    for _ in range(args.warmup):
-        ref = step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()                 # eager: Python + autograd launch every step
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-
-    ms_step, graph_ok, graph_ms = eager_ms, None, None
-    if not args.eager:
-        # the same step captured once in a HIP graph and replayed: no host work per step
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for _ in range(2):
-                step()
-        torch.cuda.current_stream().wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            gout = step()
-        for _ in range(args.warmup):
-            graph.replay()
-        torch.cuda.synchronize()
-        graph_ok = all(torch.equal(a, b) for a, b in zip(gout, ref))   # deterministic kernels
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            graph.replay()
-        torch.cuda.synchronize()
-        graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-        if graph_ok:
-            ms_step = graph_ms
+    eager_ms, graph_ms, graph_ok = time_steps(step, args)
+    ms_step = min(eager_ms, graph_ms) if graph_ok else eager_ms
 
     with ssm_scan.KernelTimer() as timer:
         for _ in range(args.steps):
@@ -191,7 +198,7 @@ def bench_c1(args, dev):
                                "zoh, z gate + D skip, channel-major (B,D,L) storage",
                    "batch": B, "seqlen": L, "dim": D, "dstate": N, "method": "zoh"},
         "hbm_frac_step": (fb + bb) / (ms_step * 1e-3) / (HBM_PEAK_GBS * 1e9),
-        "step_mode": "hip-graph replay of the fwd+bwd step" if ms_step != eager_ms else "eager",
+        "step_mode": "hip-graph replay of the fwd+bwd step" if ms_step != eager_ms else "eager launches",
         "eager_ms_per_step": eager_ms, "graph_ms_per_step": graph_ms, "graph_matches_eager": graph_ok,
         "kernels_ms": {"ssm_fwd": fwd_ms, "ssm_bwd": bwd_ms, "ssm_fwd_cold": cold_f, "ssm_bwd_cold": cold_b},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -214,19 +221,14 @@ def bench_fwd(args, dev, B, L, dtype, workload):
         with torch.no_grad():
             return ssm_scan.selective_scan_fn(*ins, return_last_state=True, segments=args.segments)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    eager_ms, graph_ms, graph_ok = time_steps(step, args)
+    ms = min(eager_ms, graph_ms) if graph_ok else eager_ms
     with ssm_scan.KernelTimer() as timer:
-        t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
     fwd_ms = statistics.mean(timer.times_ms()["ssm_fwd"])
     s = torch.tensor([], dtype=dtype).element_size()
     fb, _ = alg_bytes(B, L, D, N, s=s, gate=False, skip=False)
-    ms = wall * 1e3 / args.steps
     achieved = fb / (fwd_ms * 1e-3) / 1e9
     rec = {"metric": f"selective-scan fwd Mtok/s, {workload}", "value": B * L / (ms * 1e-3) / 1e6,
             "unit": "Mtok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
@@ -236,7 +238,9 @@ def bench_fwd(args, dev, B, L, dtype, workload):
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "ssm_fwd",
                          "alg_bytes_per_launch": fb},
-           "segments": args.segments or "auto"}
+           "segments": args.segments or "auto",
+           "step_mode": "hip-graph replay" if ms != eager_ms else "eager launches", "eager_ms_per_step": eager_ms,
+           "graph_ms_per_step": graph_ms, "graph_matches_eager": graph_ok, "kernel_ms": fwd_ms}
     if L >= 4096 and not args.no_cpu_baseline:
         cb = cpu_baseline_c2(L)
         rec["cpu_baseline"] = cb
