@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 1
+#define SSM_ABI_VERSION 2
 
 enum { SSM_OK = 0, SSM_EINVAL = 1, SSM_EKEY = 2, SSM_ESPACE = 3, SSM_EHIP = 4 };
 
@@ -86,6 +86,13 @@ typedef struct ssm_fwd_args {
                               states and, with a gate, the pre-gate output) */
   void *workspace;         /* scratch of ssm_fwd_workspace_bytes() (long-sequence path) */
   int64_t workspace_bytes;
+  /* Optional low-rank delta: the dt_proj GEMM of models/mamba.py:76 done while the delta
+   * tiles are staged.  With delta_rank R in 1..16, `delta` is the (B,L,R) input dt (dtype)
+   * and the delta the scan uses is delta @ delta_proj^T, delta_proj (D,R) in the state type,
+   * before delta_bias / softplus; no (B,L,D) delta is read.  delta_rank = 0: off.  Needs
+   * dstate <= 16 and a 16- or 32-bit dtype. */
+  ssm_tensor delta_proj;
+  int64_t delta_rank;
 } ssm_fwd_args;
 
 /* ------------------------------------------------------------------ fused backward
@@ -113,6 +120,11 @@ typedef struct ssm_bwd_args {
   ssm_tensor dh0;          /* (B,D,N) state type, optional (gradient of h0) */
   void *workspace;         /* ssm_bwd_workspace_bytes() */
   int64_t workspace_bytes;
+  /* Low-rank delta as in ssm_fwd_args; ddelta is then the (B,L,D) gradient of the projected
+   * delta (before bias / softplus), from which the caller's GEMMs form the gradients of the
+   * (B,L,R) input and of delta_proj. */
+  ssm_tensor delta_proj;
+  int64_t delta_rank;
 } ssm_bwd_args;
 
 /* ------------------------------------------------------------------ decode step

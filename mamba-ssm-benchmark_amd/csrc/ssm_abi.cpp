@@ -131,6 +131,24 @@ int ssm_abi_version(void) { return SSM_ABI_VERSION; }
 const char *ssm_last_error(void) { return g_err; }
 
 // ------------------------------------------------------------------ fused forward
+// Low-rank delta: rank 1..kLR with a (D, R) weight, and the (B, L, R) input's row offsets in
+// 32 bits (the kernels read it through raw buffers over one batch row).
+static int check_lowrank(int64_t rank, const ssm_tensor &proj, const ssm_tensor &delta, int64_t L, int64_t N,
+                         int dtype) {
+  if (rank == 0) return ok();
+  if (rank < 0 || rank > kLR)
+    return fail(SSM_EINVAL, "delta_rank=%lld must be in 0..%d", (long long)rank, kLR);
+  if (N > 16 || dtype == SSM_F64)
+    return fail(SSM_EINVAL, "a low-rank delta needs dstate <= 16 and 16- or 32-bit inputs");
+  REQUIRE(proj, "delta_proj");
+  const int esize = dtype == SSM_F64 ? 8 : dtype == SSM_F32 ? 4 : 2;
+  if (delta.stride[1] < 0 || delta.stride[2] < 0 || proj.stride[0] < 0 || proj.stride[1] < 0)
+    return fail(SSM_EINVAL, "low-rank delta and delta_proj need non-negative strides");
+  if (((L - 1 + kCK) * delta.stride[1] + (rank - 1) * delta.stride[2] + 1) * esize >= ((int64_t)1 << 31))
+    return fail(SSM_EINVAL, "a batch row of the low-rank delta spans more than 2 GiB");
+  return ok();
+}
+
 int ssm_fwd_check(const ssm_fwd_args *a) {
   if (!a) return fail(SSM_EINVAL, "null args");
   int rc = check_common(a->batch, a->seqlen, a->dim, a->dstate, a->method, a->dtype);
@@ -142,7 +160,7 @@ int ssm_fwd_check(const ssm_fwd_args *a) {
   REQUIRE(a->Cm, "Cm");
   REQUIRE(a->out, "out");
   if (a->segments < 0) return fail(SSM_EINVAL, "segments=%d must be >= 0", a->segments);
-  return ok();
+  return check_lowrank(a->delta_rank, a->delta_proj, a->delta, a->seqlen, a->dstate, a->dtype);
 }
 
 int64_t ssm_fwd_saved_bytes(const ssm_fwd_args *a) {
@@ -193,7 +211,11 @@ static void fill_fwd(FwdParams &p, const ssm_fwd_args *a, const FwdLayout &f) {
   p.x = kv(a->x); p.dt = kv(a->delta); p.A = kv(a->A); p.Bm = kv(a->Bm); p.Cm = kv(a->Cm);
   p.Dsk = kv(a->Dskip); p.z = kv(a->z); p.bias = kv(a->delta_bias); p.h0 = kv(a->h0);
   p.out = kv(a->out); p.last = kv(a->last);
-  const ssm_tensor *bld[] = {&a->x, &a->delta, &a->z, &a->out};
+  if (a->delta_rank > 0) {  // the (B, L, D) delta view aliases x: its tiles are never used
+    p.lowrank = (int)a->delta_rank;
+    p.dtl = kv(a->delta); p.dtw = kv(a->delta_proj); p.dt = kv(a->x);
+  }
+  const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->z, &a->out};
   p.uniform = uniform_layout(bld, 4, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype);
 }
 
@@ -243,7 +265,7 @@ int ssm_bwd_check(const ssm_bwd_args *a) {
   if (has(a->z)) REQUIRE(a->dz, "dz");
   if (has(a->delta_bias)) REQUIRE(a->ddelta_bias, "ddelta_bias");
   if (has(a->dh0) && !has(a->h0)) return fail(SSM_EINVAL, "dh0 given without h0");
-  return ok();
+  return check_lowrank(a->delta_rank, a->delta_proj, a->delta, a->seqlen, a->dstate, a->dtype);
 }
 
 int64_t ssm_bwd_workspace_bytes(const ssm_bwd_args *a) {
@@ -270,6 +292,7 @@ int ssm_bwd(const ssm_bwd_args *a, void *stream) {
     fa.x = a->x; fa.delta = a->delta; fa.A = a->A; fa.Bm = a->Bm; fa.Cm = a->Cm;
     fa.Dskip = a->Dskip; fa.z = a->z; fa.delta_bias = a->delta_bias;
     fa.delta_softplus = a->delta_softplus; fa.h0 = a->h0;
+    fa.delta_proj = a->delta_proj; fa.delta_rank = a->delta_rank;
     fa.out = a->x;  // placeholder with x's layout, never written (write_out = 0)
     FwdParams fp;
     fill_fwd(fp, &fa, w.f);
@@ -294,7 +317,11 @@ int ssm_bwd(const ssm_bwd_args *a, void *stream) {
   p.dout = kv(a->dout); p.dlast = kv(a->dlast); p.dx = kv(a->dx); p.ddt = kv(a->ddelta);
   p.dz = kv(a->dz); p.dh0 = kv(a->dh0);
   p.ckpt = ckpt; p.ypre = ypre;
-  const ssm_tensor *bld[] = {&a->x, &a->delta, &a->z, &a->dout, &a->dx, &a->ddelta, &a->dz};
+  if (a->delta_rank > 0) {  // as in the forward: the (B, L, D) delta view aliases x
+    p.lowrank = (int)a->delta_rank;
+    p.dtl = kv(a->delta); p.dtw = kv(a->delta_proj); p.dt = kv(a->x);
+  }
+  const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->z, &a->dout, &a->dx, &a->ddelta, &a->dz};
   p.uniform = uniform_layout(bld, 7, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype);
   p.ws_dB = ws + w.dB; p.ws_dC = ws + w.dC; p.ws_dA = ws + w.dA; p.ws_dD = ws + w.dD; p.ws_db = ws + w.db;
   hipError_t e = launch_bwd(p, a->dtype, a->method, w.f.np, s);

@@ -37,6 +37,8 @@ struct BwdWaveLds {
   CT C[NP][CKP];
   CT pn[RH][CW][2][np_pad((int)sizeof(CT), NP)];  // (dx, ddelta) per-lane contributions, quantity-major
   CT pd[RH][CW][NP][2];  // (dB, dC) per-lane contributions
+  CT lr[CK][lr_pad((int)sizeof(CT))];  // low-rank delta input rows of the chunk
+  CT wr[CW][lr_pad((int)sizeof(CT))];  // low-rank weight rows of the wavefront's channels
 };
 
 template <typename CT, int NP, int WPB>
@@ -46,7 +48,7 @@ struct BwdShared {
 template <typename CT, int NP>
 struct BwdShared<CT, NP, 1> {};
 
-template <typename IT, int NP, int METHOD, bool UL>
+template <typename IT, int NP, int METHOD, bool UL, bool LR>
 __global__ void __launch_bounds__(kWave * bwd_waves(sizeof(typename Conv<IT>::CT), NP))
 k_bwd(const BwdParams p) {
   typedef typename Conv<IT>::CT CT;
@@ -116,6 +118,7 @@ k_bwd(const BwdParams p) {
   struct Tiles {
     WaveTile<IT, CT, CK, CW, UL> x, dt, g, z;
     WaveTile<IT, CT, CK, NP, UL> B, C;
+    LowRankTile<IT, CT, CK> lr;
     CT yp[E1];
     CT ck;
   };
@@ -129,7 +132,18 @@ k_bwd(const BwdParams p) {
   tile_offsets<CK, NP>(offB, vB, 0, bt, lane, ES);
   const KView vy{ypre, xt ? 1 : (int64_t)D, xt ? 1 : (int64_t)D, xt ? (int64_t)L : 1};  // ypre's (t, d) strides
   tile_offsets<CK, CW>(offY, vy, dw, gt, lane, (int)sizeof(CT));
-  const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES), rbdt = row_buffer(vdt, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t empty = __builtin_amdgcn_make_buffer_rsrc((void *)p.x.p, (short)0, 0, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbdt = LR ? empty : row_buffer(vdt, b, L, D, ES);
+  // low-rank delta: input block reads and the weight rows in LDS
+  __amdgpu_buffer_rsrc_t rblr = empty;
+  uint32_t offLR = 0, tstepLR = 0;
+  bool rvLR = false;
+  if constexpr (LR) {
+    rblr = row_buffer(p.dtl, b, L, p.lowrank, ES);
+    lowrank_offsets(p.dtl, p.lowrank, lane, ES, offLR, tstepLR, rvLR);
+    lowrank_weights<CT, CW>(S.wr, p.dtw, p.lowrank, dw, D, lane);
+  }
   const __amdgpu_buffer_rsrc_t rbg = row_buffer(vg, b, L, D, ES), rbz = row_buffer(vzl, b, L, D, ES);
   const __amdgpu_buffer_rsrc_t rbB = row_buffer(vB, b, L, N, ES), rbC = row_buffer(vC, b, L, N, ES);
   const __amdgpu_buffer_rsrc_t rby = __builtin_amdgcn_make_buffer_rsrc(
@@ -138,6 +152,7 @@ k_bwd(const BwdParams p) {
   auto load = [&](Tiles &T, int k) {
     const int kc = k < 0 ? 0 : k;
     const int t0 = kc * CK;
+    if constexpr (LR) T.lr.load(rblr, offLR + (uint32_t)(t0 * (int)p.dtl.s1 * ES), tstepLR, rvLR);
     if constexpr (UL) {
       const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES), tb_ = (uint32_t)(t0 * (int)vB.s1 * ES);
       T.x.load_buf(rbx, offX, tx_);
@@ -178,6 +193,11 @@ k_bwd(const BwdParams p) {
     // ---------------------------------------------------------------- stage
     {
       T.x.store(S.x, xt, lane, t0, Lc, dw, D);
+      if constexpr (LR) {
+        T.lr.store(S.lr, lane);
+        wave_lds_sync();
+        lowrank_delta<IT, CT, CK, CW, UL>(T.dt, S.lr, S.wr, dtt, lane);
+      }
       store_delta_w<IT, CT, CK, CW, WL::CKP, UL>(T.dt, S.dt, S.sg, dtt, lane, p.softplus, biasv, dw, D, t0, Lc);
       T.B.store(S.B, bt, lane, t0, Lc, 0, N);
       T.C.store(S.C, ctt, lane, t0, Lc, 0, N);
@@ -440,8 +460,16 @@ static hipError_t launch_bwd_t(const BwdParams &p, hipStream_t s) {
   constexpr int DT = WPB * (kWave / NP);
   if (p.ntiles != (int)((p.D + DT - 1) / DT)) return hipErrorInvalidValue;
   dim3 grid((unsigned)p.ntiles, (unsigned)p.B);
-  if (p.uniform) hipLaunchKernelGGL((k_bwd<IT, NP, M, true>), grid, dim3(WPB * kWave), 0, s, p);
-  else hipLaunchKernelGGL((k_bwd<IT, NP, M, false>), grid, dim3(WPB * kWave), 0, s, p);
+  if constexpr (NP <= 16 && sizeof(IT) <= 4) {  // the low-rank delta kernels (see launch_fwd)
+    if (p.lowrank) {
+      if (p.uniform) hipLaunchKernelGGL((k_bwd<IT, NP, M, true, true>), grid, dim3(WPB * kWave), 0, s, p);
+      else hipLaunchKernelGGL((k_bwd<IT, NP, M, false, true>), grid, dim3(WPB * kWave), 0, s, p);
+      return hipGetLastError();
+    }
+  }
+  if (p.lowrank) return hipErrorInvalidValue;
+  if (p.uniform) hipLaunchKernelGGL((k_bwd<IT, NP, M, true, false>), grid, dim3(WPB * kWave), 0, s, p);
+  else hipLaunchKernelGGL((k_bwd<IT, NP, M, false, false>), grid, dim3(WPB * kWave), 0, s, p);
   return hipGetLastError();
 }
 

@@ -40,9 +40,11 @@ struct FwdWaveLds {
   CT B[NP][CKP];
   CT C[NP][CKP];
   CT y[CK][CW][np_pad((int)sizeof(CT), NP)];
+  CT lr[CK][lr_pad((int)sizeof(CT))];  // low-rank delta input rows of the chunk
+  CT wr[CW][lr_pad((int)sizeof(CT))];  // low-rank weight rows of the wavefront's channels
 };
 
-template <typename IT, int NP, int METHOD, bool UL, bool SUM>
+template <typename IT, int NP, int METHOD, bool UL, bool SUM, bool LR>
 __global__ void __launch_bounds__(kWave * fwd_waves(sizeof(typename Conv<IT>::CT), NP))
 k_fwd(const FwdParams p) {
   typedef typename Conv<IT>::CT CT;
@@ -85,6 +87,7 @@ k_fwd(const FwdParams p) {
   struct Tiles {
     WaveTile<IT, CT, CK, CW, UL> x, dt, z;
     WaveTile<IT, CT, CK, NP, UL> B, C;
+    LowRankTile<IT, CT, CK> lr;
   };
   CT biasv[WaveTile<IT, CT, CK, CW, UL>::E], dskv[WaveTile<IT, CT, CK, CW, UL>::E];
   tile_bias<CT, CK, CW>(biasv, p.has_bias, p.bias, dw, D, dtt, lane);
@@ -100,11 +103,23 @@ k_fwd(const FwdParams p) {
   uint32_t offX[EX], offB[EB];
   tile_offsets<CK, CW>(offX, vx, dw, xt, lane, ES);
   tile_offsets<CK, NP>(offB, vB, 0, bt, lane, ES);
-  const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES), rbdt = row_buffer(vdt, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t empty = __builtin_amdgcn_make_buffer_rsrc((void *)p.x.p, (short)0, 0, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbdt = LR ? empty : row_buffer(vdt, b, L, D, ES);
   const __amdgpu_buffer_rsrc_t rbz = row_buffer(vzl, b, L, D, ES);
   const __amdgpu_buffer_rsrc_t rbB = row_buffer(vB, b, L, N, ES), rbC = row_buffer(vC, b, L, N, ES);
+  // low-rank delta: input block reads and the weight rows in LDS
+  __amdgpu_buffer_rsrc_t rblr = empty;
+  uint32_t offLR = 0, tstepLR = 0;
+  bool rvLR = false;
+  if constexpr (LR) {
+    rblr = row_buffer(p.dtl, b, L, p.lowrank, ES);
+    lowrank_offsets(p.dtl, p.lowrank, lane, ES, offLR, tstepLR, rvLR);
+    lowrank_weights<CT, CW>(S.wr, p.dtw, p.lowrank, dw, D, lane);
+  }
   auto load = [&](Tiles &T, int k) {
     const int t0 = (k < k1 ? k : k1 - 1) * CK;
+    if constexpr (LR) T.lr.load(rblr, offLR + (uint32_t)(t0 * (int)p.dtl.s1 * ES), tstepLR, rvLR);
     if constexpr (UL) {
       const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES), tb_ = (uint32_t)(t0 * (int)vB.s1 * ES);
       T.x.load_buf(rbx, offX, tx_);
@@ -127,6 +142,11 @@ k_fwd(const FwdParams p) {
     const int t0 = k * CK;
     const int Lc = k < k1 ? L : 0;  // time bound of this chunk's elements
     T.x.store(S.x, xt, lane, t0, Lc, dw, D);
+    if constexpr (LR) {
+      T.lr.store(S.lr, lane);
+      wave_lds_sync();
+      lowrank_delta<IT, CT, CK, CW, UL>(T.dt, S.lr, S.wr, dtt, lane);
+    }
     store_delta_w<IT, CT, CK, CW, WL::CKP, UL>(T.dt, S.dt, nullptr, dtt, lane, p.softplus, biasv, dw, D, t0, Lc);
     T.B.store(S.B, bt, lane, t0, Lc, 0, N);
     if (!SUM) T.C.store(S.C, ctt, lane, t0, Lc, 0, N);
@@ -250,30 +270,45 @@ __global__ void __launch_bounds__(kThreads) k_fwd_carry(const FwdParams p) {
   }
 }
 
-template <typename IT, int NP, int M>
+template <typename IT, int NP, int M, bool SUM, bool LR>
+static void fwd_pass(const FwdParams &p, dim3 grid, dim3 block, hipStream_t s) {
+  if (p.uniform) hipLaunchKernelGGL((k_fwd<IT, NP, M, true, SUM, LR>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((k_fwd<IT, NP, M, false, SUM, LR>), grid, block, 0, s, p);
+}
+
+template <typename IT, int NP, int M, bool LR>
 static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
   typedef typename Conv<IT>::CT CT;
   constexpr int WPB = fwd_waves(sizeof(CT), NP);
   constexpr int DT = WPB * (kWave / NP);
   dim3 grid((unsigned)((p.D + DT - 1) / DT), (unsigned)(p.B * p.nseg));
   if (p.nseg > 1) {
-    if (p.uniform) hipLaunchKernelGGL((k_fwd<IT, NP, M, true, true>), grid, dim3(WPB * kWave), 0, s, p);
-    else hipLaunchKernelGGL((k_fwd<IT, NP, M, false, true>), grid, dim3(WPB * kWave), 0, s, p);
+    fwd_pass<IT, NP, M, true, LR>(p, grid, dim3(WPB * kWave), s);
     const int64_t lanes = p.B * p.D * NP;
     hipLaunchKernelGGL((k_fwd_carry<CT, NP>), dim3((unsigned)((lanes + kThreads - 1) / kThreads)), dim3(kThreads), 0,
                        s, p);
   }
-  if (p.uniform) hipLaunchKernelGGL((k_fwd<IT, NP, M, true, false>), grid, dim3(WPB * kWave), 0, s, p);
-  else hipLaunchKernelGGL((k_fwd<IT, NP, M, false, false>), grid, dim3(WPB * kWave), 0, s, p);
+  fwd_pass<IT, NP, M, false, LR>(p, grid, dim3(WPB * kWave), s);
   return hipGetLastError();
+}
+
+// The low-rank delta kernels exist for dstate <= 16 and 16/32-bit inputs (the ABI rejects the
+// other combinations).
+template <typename IT, int NP, int M>
+static hipError_t launch_fwd_lr(const FwdParams &p, hipStream_t s) {
+  if constexpr (NP <= 16 && sizeof(IT) <= 4) {
+    if (p.lowrank) return launch_fwd_t<IT, NP, M, true>(p, s);
+  }
+  if (p.lowrank) return hipErrorInvalidValue;
+  return launch_fwd_t<IT, NP, M, false>(p, s);
 }
 
 template <typename IT, int NP>
 static hipError_t launch_fwd_m(const FwdParams &p, int method, hipStream_t s) {
   switch (method) {
-    case 0: return launch_fwd_t<IT, NP, 0>(p, s);
-    case 1: return launch_fwd_t<IT, NP, 1>(p, s);
-    default: return launch_fwd_t<IT, NP, 2>(p, s);
+    case 0: return launch_fwd_lr<IT, NP, 0>(p, s);
+    case 1: return launch_fwd_lr<IT, NP, 1>(p, s);
+    default: return launch_fwd_lr<IT, NP, 2>(p, s);
   }
 }
 

@@ -23,13 +23,18 @@ inline int padded_n(int64_t n) { return n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32
 // which spreads the lanes of a read over distinct banks.
 __host__ __device__ constexpr int ck_pad(int s) { return kCK + 16 / s; }
 __host__ __device__ constexpr int np_pad(int s, int np) { return np + 16 / s; }
+// Low-rank delta (the dt_proj GEMM fused into the staging): a chunk's (CK, R <= kLR) input
+// rows and the wavefront's channels' weight rows, padded like the other LDS rows.
+constexpr int kLR = 16;
+__host__ __device__ constexpr int lr_pad(int s) { return kLR + 16 / s; }
+__host__ __device__ constexpr int lr_wave_bytes(int s, int np) { return (kCK + 64 / np) * lr_pad(s) * s; }
 __host__ __device__ constexpr int fwd_wave_bytes(int s, int np) {
-  return ((2 * (64 / np) + 2 * np) * ck_pad(s) + kCK * (64 / np) * np_pad(s, np)) * s;
+  return ((2 * (64 / np) + 2 * np) * ck_pad(s) + kCK * (64 / np) * np_pad(s, np)) * s + lr_wave_bytes(s, np);
 }
 __host__ __device__ constexpr int bwd_half() { return 8; }  // reverse steps per LDS reduction round
 __host__ __device__ constexpr int bwd_wave_bytes(int s, int np) {
   return ((6 * (64 / np) + 2 * np) * ck_pad(s) + bwd_half() * (64 / np) * 2 * np_pad(s, np) +
-          bwd_half() * 64 * 2) * s;
+          bwd_half() * 64 * 2) * s + lr_wave_bytes(s, np);
 }
 __host__ __device__ constexpr int bwd_shared_bytes(int s, int np, int wpb) {
   return wpb > 1 ? 2 * wpb * kCK * np * 2 * s : 0;
@@ -66,6 +71,10 @@ struct FwdParams {
   int nseg, seg_chunks;
   void *seg_P, *seg_E, *seg_hin;
   KView x, dt, A, Bm, Cm, Dsk, z, bias, h0, out, last;
+  // Low-rank delta: lowrank = R > 0 means delta = dtl (B, L, R) @ dtw (D, R)^T; dt then
+  // aliases x (never read in the uniform layout) so that every tile load stays in bounds.
+  int lowrank;
+  KView dtl, dtw;
   void *ckpt;  // (B, nchunks, D, NP) state type: state at the end of each chunk
   void *ypre;  // y + D x before the gate (iff gate and saving), state type; laid out
                // (B, L, D) when x is D-contiguous, else (B, D, L) -- see ypre_index()
@@ -84,6 +93,8 @@ struct BwdParams {
   int has_D, has_z, has_bias, has_h0, has_dlast, has_dh0;
   int uniform;  // as in FwdParams
   KView x, dt, A, Bm, Cm, Dsk, z, bias, h0, dout, dlast, dx, ddt, dz, dh0;
+  int lowrank;  // as in FwdParams
+  KView dtl, dtw;
   const void *ckpt;
   const void *ypre;
   void *ws_dB, *ws_dC;  // (B, ntiles, L, NP) partial sums over the tile's channels

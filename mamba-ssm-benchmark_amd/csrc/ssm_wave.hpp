@@ -201,6 +201,77 @@ __device__ __forceinline__ void store_delta_w(const WaveTile<IT, CT, ROWS, COLS,
   }
 }
 
+// Low-rank delta (the dt_proj GEMM of models/mamba.py:76 done in the staging).  A chunk's
+// (CK, kLR) block of the (B, L, R) input, zero past R, is read E values per lane through a raw
+// buffer over the batch row (reads past the row return 0; with lowrank off the buffer is empty
+// and nothing is read), staged in LDS, and every staged (t, c) element of the delta tile is the
+// dot product of input row t with channel c's weight row (in LDS for the whole kernel).
+template <typename IT, typename CT, int CK>
+struct LowRankTile {
+  static constexpr int E = CK * kLR / kWave;
+  static_assert(kWave % kLR == 0 && (CK * kLR) % kWave == 0, "low-rank tile shape");
+  CT v[E];
+
+  // lane element i is (t, r) = (lane / kLR + i * kWave / kLR, lane % kLR)
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rb, uint32_t off0, uint32_t tstep, bool rvalid) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const CT x = buf_load<IT>(rb, off0 + (uint32_t)i * tstep);
+      v[i] = rvalid ? x : (CT)0;
+    }
+  }
+  template <int RP>
+  __device__ __forceinline__ void store(CT (*S)[RP], int lane) const {
+#pragma unroll
+    for (int i = 0; i < E; ++i) S[lane / kLR + i * (kWave / kLR)][lane % kLR] = v[i];
+  }
+};
+
+// The lane's byte offset of element 0 of its low-rank block at t0 = 0, the step between its
+// elements, and whether its rank index is below R.
+__device__ __forceinline__ void lowrank_offsets(const KView &V, int R, int lane, int esize, uint32_t &off0,
+                                                uint32_t &tstep, bool &rvalid) {
+  const int r = lane % kLR, t = lane / kLR;
+  rvalid = r < R;
+  off0 = (uint32_t)((t * V.s1 + (r < R ? r : 0) * V.s2) * esize);
+  tstep = (uint32_t)((kWave / kLR) * V.s1 * esize);
+}
+
+// The wavefront's channels' weight rows (D, R) into LDS, zero past R and past D.
+template <typename CT, int COLS, int RP>
+__device__ __forceinline__ void lowrank_weights(CT (*W)[RP], const KView &V, int R, int c0, int C, int lane) {
+#pragma unroll
+  for (int e = lane; e < COLS * kLR; e += kWave) {
+    const int c = e / kLR, r = e % kLR;
+    CT w = 0;
+    if (r < R && c0 + c < C) w = vload<CT>(V, (int64_t)(c0 + c) * V.s0 + (int64_t)r * V.s1);
+    W[c][r] = w;
+  }
+}
+
+// Replaces the staged delta tile values by the projections: element (t, c) = sum_r in[t][r] W[c][r].
+template <typename IT, typename CT, int ROWS, int COLS, bool UL, int RP>
+__device__ __forceinline__ void lowrank_delta(WaveTile<IT, CT, ROWS, COLS, UL> &tl, const CT (*in)[RP],
+                                              const CT (*W)[RP], bool tfast, int lane) {
+#pragma unroll
+  for (int i = 0; i < WaveTile<IT, CT, ROWS, COLS, UL>::E; ++i) {
+    const int e = lane + i * kWave;
+    if (e >= ROWS * COLS) break;
+    int t, c;
+    tc_of<ROWS, COLS>(e, tfast, t, c);
+    CT a[kLR], w[kLR];
+#pragma unroll
+    for (int r = 0; r < kLR; ++r) {
+      a[r] = in[t][r];
+      w[r] = W[c][r];
+    }
+    CT acc = 0;
+#pragma unroll
+    for (int r = 0; r < kLR; ++r) acc = fma(a[r], w[r], acc);
+    tl.v[i] = acc;
+  }
+}
+
 // Waves per workgroup so that WPB copies of a per-wave LDS struct fit in 64 KiB.
 template <int BYTES_PER_WAVE, int EXTRA = 0>
 struct WavesPerBlock {

@@ -2,10 +2,11 @@
 models/lm.py restricted to Mamba layers -- the callers of the scan path.
 
 Same parameters (names, shapes, initialization) and the same forward / decode interface as
-the reference, so a state_dict moves between the two.  The projections are torch GEMMs; the
+the reference, so a state_dict moves between the two.  in_proj, x_proj and out_proj are torch GEMMs; the
 scan-path work runs in the engine's kernels:
   conv + SiLU                   ssm_scan.conv.causal_conv1d          (models/mamba.py:101-107)
-  dt_proj bias + softplus,      fused into the scan / step kernels   (models/mamba.py:76)
+  dt_proj (+ bias, softplus)    fused into the scan kernels' delta   (models/mamba.py:75-76)
+                                staging (the step kernel: bias + softplus)
   selective scan, D skip, gate  ssm_scan.selective_scan_fn           (models/mamba.py:120-124)
   decode step                   ssm_scan.ssm_step (state in place)   (models/mamba.py:113-123)
 
@@ -74,13 +75,16 @@ class Mamba(nn.Module):
         self.out_proj = nn.Linear(d_inner, d_model, bias=False)
         self.out_proj._residual_out = True
 
-    def ssm_inputs(self, x):
-        """x (B, L, d_inner) -> raw delta (pre bias/softplus), delta bias, A, B, C (views)."""
+    def ssm_inputs(self, x, lowrank=False):
+        """x (B, L, d_inner) -> raw delta (pre bias/softplus), delta bias, A, B, C (views).
+        With lowrank (selective only) the raw delta is the pair (dt (B, L, dt_rank), dt_proj
+        weight): the fused kernels apply the projection while they stage delta."""
         Bsz, L, _ = x.shape
         ct = torch.promote_types(x.dtype, torch.float32)
         if self.selective:
             dt, Bm, Cm = self.x_proj(x).split([self.dt_rank, self.d_state, self.d_state], dim=-1)
-            delta = F.linear(dt, self.dt_proj.weight)          # bias + softplus run in the kernel
+            # bias + softplus run in the kernel
+            delta = (dt, self.dt_proj.weight) if lowrank else F.linear(dt, self.dt_proj.weight)
             bias = self.dt_proj.bias
         else:
             delta = x.new_zeros(()).expand(Bsz, L, self.d_inner)
@@ -94,7 +98,7 @@ class Mamba(nn.Module):
 
     def ssm_params(self, x):
         """models/mamba.py:70-84: x (B, L, d_inner) -> delta (softplus applied), A, B, C.  For
-        inspection; the forward passes the raw delta and applies bias + softplus in the kernel."""
+        inspection; the forward hands the projection, bias and softplus to the kernels."""
         delta, bias, A, Bm, Cm = self.ssm_inputs(x)
         return F.softplus(delta.to(bias.dtype) + bias), A, Bm, Cm
 
@@ -125,18 +129,23 @@ class Mamba(nn.Module):
         Bsz, L, _ = u.shape
         x, z = self.in_proj(u).chunk(2, dim=-1)
         x = self._conv(x, state)
-        delta, bias, A, Bm, Cm = self.ssm_inputs(x)
+        decode = state is not None and L == 1
+        fused = not decode and self.scan in ("auto", "triton")
+        delta, bias, A, Bm, Cm = self.ssm_inputs(x, lowrank=fused and self.selective)
         if return_delta or getattr(self, "record_delta", False):   # models/mamba.py:109-110
-            full_delta = F.softplus(delta.to(bias.dtype) + bias)
+            raw = F.linear(*delta) if isinstance(delta, tuple) else delta
+            full_delta = F.softplus(raw.to(bias.dtype) + bias)
             if getattr(self, "record_delta", False):
                 self.last_delta = full_delta.detach()
         h0 = None if state is None else state.ssm
-        if state is not None and L == 1:                          # recurrent decode step
+        if decode:                                                # recurrent decode step
             y = ssm_step(state.ssm, x[:, 0], delta[:, 0], A, Bm[:, 0], Cm[:, 0], D=self.D, z=z[:, 0],
                          delta_bias=bias, delta_softplus=True, method=self.discretization).unsqueeze(1)
-        elif self.scan in ("auto", "triton"):
-            y, last = selective_scan_fn(x, delta, A, Bm, Cm, D=self.D, z=z, delta_bias=bias, delta_softplus=True,
-                                        h0=h0, method=self.discretization, return_last_state=True)
+        elif fused:
+            dt, proj = delta if isinstance(delta, tuple) else (delta, None)
+            y, last = selective_scan_fn(x, dt, A, Bm, Cm, D=self.D, z=z, delta_bias=bias, delta_softplus=True,
+                                        h0=h0, method=self.discretization, return_last_state=True,
+                                        delta_proj=proj)
         else:
             y, last = selective_scan(x, F.softplus(delta.to(bias.dtype) + bias), A, Bm, Cm, h0=h0,
                                      method=self.discretization, scan=self.scan, d_block=self.d_block,

@@ -79,14 +79,19 @@ def _fill_common(args, x, delta, A, Bm, Cm, D, z, bias, softplus, h0, method, io
     args.h0 = _abi.view(h0)
 
 
-def _check_shapes(x, delta, A, Bm, Cm, D, z, bias, h0):
+def _check_shapes(x, delta, A, Bm, Cm, D, z, bias, h0, delta_proj=None):
     if x.dim() != 3:
         raise ValueError(f"x must be (B, L, D), got {tuple(x.shape)}")
     Bsz, L, Dm = x.shape
     if A.dim() != 2 or A.shape[0] != Dm:
         raise ValueError(f"A must be (D, N) = ({Dm}, N), got {tuple(A.shape)}")
     N = A.shape[1]
-    for name, t, shp in (("delta", delta, (Bsz, L, Dm)), ("Bm", Bm, (Bsz, L, N)), ("Cm", Cm, (Bsz, L, N)),
+    dshape = (Bsz, L, Dm)
+    if delta_proj is not None:
+        if delta_proj.dim() != 2 or delta_proj.shape[0] != Dm:
+            raise ValueError(f"delta_proj must be (D, R) = ({Dm}, R), got {tuple(delta_proj.shape)}")
+        dshape = (Bsz, L, delta_proj.shape[1])
+    for name, t, shp in (("delta", delta, dshape), ("Bm", Bm, (Bsz, L, N)), ("Cm", Cm, (Bsz, L, N)),
                          ("D", D, (Dm,)), ("z", z, (Bsz, L, Dm)), ("delta_bias", bias, (Dm,)),
                          ("h0", h0, (Bsz, Dm, N))):
         if t is not None and tuple(t.shape) != shp:
@@ -97,10 +102,11 @@ class FusedSelectiveScanFn(torch.autograd.Function):
     """out, last = fused scan; gradients for x, delta, A, Bm, Cm, D, z, delta_bias, h0."""
 
     @staticmethod
-    def forward(ctx, x, delta, A, Bm, Cm, D, z, delta_bias, h0, method, delta_softplus, segments=0):
+    def forward(ctx, x, delta, A, Bm, Cm, D, z, delta_bias, h0, method, delta_softplus, segments=0,
+                delta_proj=None):
         io, ct = _dtypes(x, (delta, Bm, Cm, z))
         xs, ds, Bs, Cs, zs = (_cast_keep(t, io) for t in (x, delta, Bm, Cm, z))
-        As, Dv, bv, h0v = (_cast_keep(t, ct) for t in (A, D, delta_bias, h0))
+        As, Dv, bv, h0v, Wv = (_cast_keep(t, ct) for t in (A, D, delta_bias, h0, delta_proj))
         Bsz, L, Dm = x.shape
         N = A.shape[1]
         dev = x.device
@@ -110,6 +116,8 @@ class FusedSelectiveScanFn(torch.autograd.Function):
         _fill_common(args, xs, ds, As, Bs, Cs, Dv, zs, bv, delta_softplus, h0v, method, io)
         args.out, args.last = _abi.view(out), _abi.view(last)
         args.segments = int(segments or 0)
+        if Wv is not None:
+            args.delta_proj, args.delta_rank = _abi.view(Wv), Wv.shape[1]
         lib = _abi.lib()
         wbytes = lib.ssm_fwd_workspace_bytes(ctypes.byref(args))
         if wbytes < 0:
@@ -117,7 +125,7 @@ class FusedSelectiveScanFn(torch.autograd.Function):
         ws = torch.empty(wbytes, dtype=torch.uint8, device=dev) if wbytes else None
         if ws is not None:
             args.workspace, args.workspace_bytes = ws.data_ptr(), wbytes
-        need_bwd = any(ctx.needs_input_grad[:9])
+        need_bwd = any(ctx.needs_input_grad[:9]) or (Wv is not None and ctx.needs_input_grad[12])
         saved = None
         if need_bwd:
             nbytes = lib.ssm_fwd_saved_bytes(ctypes.byref(args))
@@ -129,17 +137,18 @@ class FusedSelectiveScanFn(torch.autograd.Function):
             rc = timed_launch("ssm_fwd", stream, lambda: lib.ssm_fwd(ctypes.byref(args), stream))
         _abi.check(rc, "ssm_fwd")
         if need_bwd:
-            ctx.save_for_backward(xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, saved)
+            ctx.save_for_backward(xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, Wv, saved)
         ctx.set_materialize_grads(False)   # an unused `last` passes dlast = None (no zero fill)
         ctx.method, ctx.softplus, ctx.io, ctx.ct = method, delta_softplus, io, ct
         ctx.in_dtypes = [None if t is None else t.dtype for t in (x, delta, A, Bm, Cm, D, z, delta_bias, h0)]
+        ctx.proj_dtype = None if delta_proj is None else delta_proj.dtype
         if out.dtype != x.dtype:
             out = out.to(x.dtype)
         return out, last
 
     @staticmethod
     def backward(ctx, dout, dlast):
-        xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, saved = ctx.saved_tensors
+        xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, Wv, saved = ctx.saved_tensors
         io, ct = ctx.io, ctx.ct
         if dout is None:
             dout = torch.zeros(xs.shape, dtype=io, device=xs.device)
@@ -150,7 +159,7 @@ class FusedSelectiveScanFn(torch.autograd.Function):
         dev = xs.device
 
         like = empty_like_layout
-        dx, dd = like(xs, io), like(ds, io)
+        dx, dd = like(xs, io), like(ds if Wv is None else xs, io)
         dA = torch.empty((Dm, N), dtype=ct, device=dev)
         dB, dC = like(Bs, io), like(Cs, io)
         dD = torch.empty((Dm,), dtype=ct, device=dev) if Dv is not None else None
@@ -164,6 +173,8 @@ class FusedSelectiveScanFn(torch.autograd.Function):
         args.dx, args.ddelta, args.dA = _abi.view(dx), _abi.view(dd), _abi.view(dA)
         args.dBm, args.dCm, args.dD = _abi.view(dB), _abi.view(dC), _abi.view(dD)
         args.dz, args.ddelta_bias, args.dh0 = _abi.view(dz), _abi.view(db), _abi.view(dh0)
+        if Wv is not None:
+            args.delta_proj, args.delta_rank = _abi.view(Wv), Wv.shape[1]
         lib = _abi.lib()
         nbytes = lib.ssm_bwd_workspace_bytes(ctypes.byref(args))
         if nbytes < 0:
@@ -174,27 +185,43 @@ class FusedSelectiveScanFn(torch.autograd.Function):
             stream = _abi.stream_handle(dev)
             rc = timed_launch("ssm_bwd", stream, lambda: lib.ssm_bwd(ctypes.byref(args), stream))
         _abi.check(rc, "ssm_bwd")
+        dW = None
+        if Wv is not None:
+            # the projection's gradients: the two small GEMMs of F.linear's backward, in torch
+            ddc = dd.to(ct)
+            dW = ddc.reshape(-1, Dm).t() @ ds.to(ct).reshape(-1, Wv.shape[1])
+            dd = torch.matmul(ddc, Wv)
         grads = [dx, dd, dA, dB, dC, dD, dz, db, dh0]
         out = []
         for g, dt in zip(grads, ctx.in_dtypes):
             out.append(None if g is None or dt is None else _cast_keep(g, dt))
-        return (*out, None, None, None)
+        return (*out, None, None, None, None if dW is None else _cast_keep(dW, ctx.proj_dtype))
+
+
+LOWRANK_MAX = 16  # rank of a delta projection the kernels apply while staging delta
 
 
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                      h0=None, method="zoh", return_last_state=False, segments=None):
+                      h0=None, method="zoh", return_last_state=False, segments=None, delta_proj=None):
     """out = (scan(u, delta', A, B, C) + D u) * silu(z), delta' = softplus(delta + bias).
 
     Logical layouts as the reference: u, delta, z (B, L, D); A (D, N); B, C (B, L, N);
     h0 (B, D, N).  Pass ``x.transpose(1, 2)`` for channel-major (B, D, L) storage.
     ``segments`` forces the number of time segments the forward scans in parallel (default:
-    chosen by the engine; more than one only when B x D is too small to fill the GPU)."""
+    chosen by the engine; more than one only when B x D is too small to fill the GPU).
+    ``delta_proj`` (D, R): ``delta`` is then the low-rank (B, L, R) input and the scan uses
+    delta @ delta_proj^T -- the dt_proj GEMM of models/mamba.py:76, done by the kernels while
+    they stage delta for R <= 16 and dstate <= 16 with 16/32-bit inputs (no (B, L, D) delta in
+    memory), by a torch GEMM otherwise.  Gradients flow to both."""
     if method not in METHODS:
         raise ValueError(f"unknown discretization {method!r}")
-    _require_gpu(u, delta, A, B, C, D, z, delta_bias, h0)
-    _check_shapes(u, delta, A, B, C, D, z, delta_bias, h0)
+    _require_gpu(u, delta, A, B, C, D, z, delta_bias, h0, delta_proj)
+    _check_shapes(u, delta, A, B, C, D, z, delta_bias, h0, delta_proj)
+    if delta_proj is not None and (delta_proj.shape[1] > LOWRANK_MAX or A.shape[1] > 16
+                                   or torch.promote_types(u.dtype, torch.float32) == torch.float64):
+        delta, delta_proj = torch.nn.functional.linear(delta, delta_proj), None
     out, last = FusedSelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, h0, METHODS[method],
-                                           bool(delta_softplus), segments or 0)
+                                           bool(delta_softplus), segments or 0, delta_proj)
     return (out, last) if return_last_state else out
 
 

@@ -176,3 +176,32 @@ def test_dense_layout_helper():
     out = hip_scan.empty_like_layout(torch.zeros(2, 7, 5).transpose(1, 2), torch.bfloat16)
     assert out.stride() == (35, 1, 5) and out.dtype == torch.bfloat16
     assert hip_scan.empty_like_layout(torch.zeros(2, 5, 14)[..., :7], torch.float32).is_contiguous()
+
+
+@pytest.mark.parametrize("rank,with_proj,ok", [(0, False, True), (16, True, True), (1, True, True),
+                                                (17, True, False), (-1, True, False), (4, False, False)])
+def test_lowrank_delta_validation(rank, with_proj, ok):
+    """delta_rank 0 (off) or 1..16 with a (D, R) delta_proj; anything else is rejected."""
+    a = _fwd_args(B=2, L=8, D=4, N=16)
+    W = torch.zeros(4, max(rank, 1))
+    low = torch.zeros(2, 8, max(rank, 1))
+    a.delta = _abi.view(low)
+    if with_proj:
+        a.delta_proj = _abi.view(W)
+    a.delta_rank = rank
+    a._keep2 = (W, low)
+    rc = _abi.lib().ssm_fwd_check(ctypes.byref(a))
+    if ok:
+        assert rc == 0
+    else:
+        with pytest.raises(ValueError):
+            _abi.check(rc, "ssm_fwd")
+
+
+def test_lowrank_delta_needs_small_dstate():
+    a = _fwd_args(B=2, L=8, D=4, N=32)
+    W, low = torch.zeros(4, 8), torch.zeros(2, 8, 8)
+    a.delta, a.delta_proj, a.delta_rank = _abi.view(low), _abi.view(W), 8
+    a._keep2 = (W, low)
+    with pytest.raises(ValueError):
+        _abi.check(_abi.lib().ssm_fwd_check(ctypes.byref(a)), "ssm_fwd")

@@ -1,0 +1,156 @@
+"""The dt_proj projection fused into the scan kernels (selective_scan_fn(..., delta_proj=W)):
+delta is the low-rank (B, L, R) input dt and the scan uses dt @ W^T + bias, softplus
+(models/mamba.py:75-76).  Checked against the float64 oracle on delta = dt @ W^T computed in
+float64, including the gradients of dt and W (the GEMM backward of F.linear), and against the
+engine's own path with the projection done by a torch GEMM first.
+
+Tolerances as the fused tests: float32 rtol 1e-4 / atol 1e-5 x max(1, RMS) on every output and
+gradient; bf16 inputs rtol 2e-2.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import ssm_scan
+from oracle import scan_ref as R
+from ssm_inputs import np64
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-4, 1e-5
+
+
+def close(got, ref, rtol=RTOL, atol=ATOL, name=""):
+    got = np64(got) if isinstance(got, torch.Tensor) else got
+    scale = max(1.0, float(np.sqrt(np.mean(np.square(ref))))) if np.size(ref) else 1.0
+    np.testing.assert_allclose(got, ref, rtol=rtol, atol=atol * scale, err_msg=name)
+
+
+def make(B, L, D, N, Rk, seed, channel_major=False, dtype=torch.float32):
+    """x (optionally channel-major storage), dt as the split view of an x_proj-like output
+    (B, L, R + 2N) with B, C beside it, W (D, R), gate, skip, bias, A = S4D-real."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, L, D, generator=g)
+    if channel_major:
+        x = x.transpose(1, 2).contiguous().transpose(1, 2)
+    proj = torch.randn(B, L, Rk + 2 * N, generator=g)
+    W = torch.randn(D, Rk, generator=g) * (0.5 / Rk ** 0.5)
+    A = -torch.arange(1, N + 1, dtype=torch.float32).repeat(D, 1)
+    Dv = torch.randn(D, generator=g)
+    z = torch.randn(B, L, D, generator=g)
+    bias = torch.rand(D, generator=g) * 2.0 - 4.0
+    dout = torch.randn(B, L, D, generator=g)
+    if dtype != torch.float32:
+        x, proj, z = x.to(dtype), proj.to(dtype), z.to(dtype)
+    return x, proj, W, A, Dv, z, bias, dout
+
+
+def run(dev, x, proj, W, A, Dv, z, bias, dout, Rk, N, method, lowrank=True, segments=None):
+    leaves = [t.to(dev).requires_grad_() for t in (x, proj, W, A, Dv, z, bias)]
+    xg, pg, Wg, Ag, Dg, zg, bg = leaves
+    dt, Bm, Cm = pg[..., :Rk], pg[..., Rk:Rk + N], pg[..., Rk + N:]
+    if lowrank:
+        out, last = ssm_scan.selective_scan_fn(xg, dt, Ag, Bm, Cm, D=Dg, z=zg, delta_bias=bg, delta_softplus=True,
+                                               method=method, return_last_state=True, segments=segments,
+                                               delta_proj=Wg)
+    else:
+        out, last = ssm_scan.selective_scan_fn(xg, torch.nn.functional.linear(dt, Wg), Ag, Bm, Cm, D=Dg, z=zg,
+                                               delta_bias=bg, delta_softplus=True, method=method,
+                                               return_last_state=True, segments=segments)
+    (out.float() * dout.to(dev)).sum().backward()
+    grads = {n: t.grad for n, t in zip(("dx", "dproj", "dW", "dA", "dD", "dz", "dbias"), leaves)}
+    return out.detach(), last.detach(), grads
+
+
+def oracle(x, proj, W, A, Dv, z, bias, dout, Rk, N, method):
+    x, proj, W, A, Dv, z, bias, dout = (np64(t) for t in (x, proj, W, A, Dv, z, bias, dout))
+    dt, Bm, Cm = proj[..., :Rk], proj[..., Rk:Rk + N], proj[..., Rk + N:]
+    raw = dt @ W.T + bias
+    delta = np.log1p(np.exp(raw))
+    out, _, last = R.selective_scan_fwd(x, delta, A, Bm, Cm, None, method, Dv, z)
+    g = R.selective_scan_bwd(x, delta, A, Bm, Cm, dout, None, method, Dv, z, None)
+    draw = g["ddelta"] / (1.0 + np.exp(-raw))
+    dproj = np.concatenate([draw @ W, g["dB"], g["dC"]], -1)
+    dW = draw.reshape(-1, W.shape[0]).T @ dt.reshape(-1, Rk)
+    return out, last, {"dx": g["dx"], "dproj": dproj, "dW": dW, "dA": g["dA"], "dD": g["dD"], "dz": g["dz"],
+                       "dbias": draw.sum(axis=(0, 1))}
+
+
+@pytest.mark.parametrize("method", ["zoh", "euler", "bilinear"])
+@pytest.mark.parametrize("Rk,N,channel_major", [(16, 16, True), (5, 16, False), (1, 8, True), (12, 32, False)])
+def test_lowrank_delta_matches_oracle(dev, method, Rk, N, channel_major):
+    B, L, D = 2, 83, 40
+    ins = make(B, L, D, N, Rk, seed=Rk * 7 + N, channel_major=channel_major)
+    out, last, grads = run(dev, *ins, Rk, N, method)
+    rout, rlast, rg = oracle(*ins, Rk, N, method)
+    close(out, rout, name="out")
+    close(last, rlast, name="last")
+    for k, v in grads.items():
+        close(v, rg[k], name=k)
+
+
+def test_lowrank_equals_projected_delta_at_config1_shape(dev):
+    """B16 L512 D512 N16 R16 (the config-3 layer's scan shape): the fused projection and a
+    torch GEMM before the scan give the same outputs and gradients (to float32 rounding)."""
+    B, L, D, N, Rk = 16, 512, 512, 16, 16
+    ins = make(B, L, D, N, Rk, seed=3, channel_major=True)
+    a = run(dev, *ins, Rk, N, "zoh", lowrank=True)
+    b = run(dev, *ins, Rk, N, "zoh", lowrank=False)
+    for u, v, name in ((a[0], b[0], "out"), (a[1], b[1], "last")):
+        close(u, np64(v), name=name)
+    for k in a[2]:
+        close(a[2][k], np64(b[2][k]), rtol=1e-4, atol=1e-5, name=k)
+
+
+def test_lowrank_long_sequence_segments(dev):
+    """The segmented long-sequence forward (summary, carry and main passes all stage delta
+    through the projection) equals the unsegmented one."""
+    B, L, D, N, Rk = 1, 4096, 64, 16, 16
+    x, proj, W, A, Dv, z, bias, dout = (t.to(dev) for t in make(B, L, D, N, Rk, seed=5))
+    dt, Bm, Cm = proj[..., :Rk], proj[..., Rk:Rk + N], proj[..., Rk + N:]
+    with torch.no_grad():
+        res = [ssm_scan.selective_scan_fn(x, dt, A, Bm, Cm, D=Dv, z=z, delta_bias=bias, delta_softplus=True,
+                                          return_last_state=True, segments=s, delta_proj=W) for s in (1, 8)]
+        ref = ssm_scan.selective_scan_fn(x, torch.nn.functional.linear(dt, W), A, Bm, Cm, D=Dv, z=z,
+                                         delta_bias=bias, delta_softplus=True, return_last_state=True, segments=1)
+    for y, last in res:
+        close(y, np64(ref[0]), name="y")
+        close(last, np64(ref[1]), name="last")
+
+
+def test_lowrank_rank_above_capacity_uses_a_gemm(dev):
+    """R = 24 (> 16) takes a torch GEMM first; results and gradients still match the oracle."""
+    B, L, D, N, Rk = 2, 40, 32, 16, 24
+    ins = make(B, L, D, N, Rk, seed=9)
+    out, last, grads = run(dev, *ins, Rk, N, "zoh")
+    rout, rlast, rg = oracle(*ins, Rk, N, "zoh")
+    close(out, rout, name="out")
+    close(last, rlast, name="last")
+    for k, v in grads.items():
+        close(v, rg[k], name=k)
+
+
+def test_lowrank_mixed_layouts(dev):
+    """x channel-major with a time-major gate: not a uniform layout, so the kernels take the
+    strided-address path; the projection is staged the same way."""
+    B, L, D, N, Rk = 2, 50, 48, 16, 16
+    x, proj, W, A, Dv, z, bias, dout = make(B, L, D, N, Rk, seed=13, channel_major=True)
+    ins = (x, proj, W, A, Dv, z.contiguous(), bias, dout)
+    out, last, grads = run(dev, *ins, Rk, N, "zoh")
+    rout, rlast, rg = oracle(*ins, Rk, N, "zoh")
+    close(out, rout, name="out")
+    for k, v in grads.items():
+        close(v, rg[k], name=k)
+
+
+def test_lowrank_bf16_inputs(dev):
+    """bf16 x, dt, B, C, z (state float32): rtol 2e-2 against the oracle on the rounded inputs."""
+    B, L, D, N, Rk = 2, 64, 32, 16, 16
+    ins = make(B, L, D, N, Rk, seed=17, dtype=torch.bfloat16)
+    out, last, grads = run(dev, *ins, Rk, N, "zoh")
+    assert out.dtype == torch.bfloat16
+    rout, rlast, rg = oracle(*ins, Rk, N, "zoh")
+    close(out, rout, 2e-2, 2e-2, "out")
+    close(last, rlast, 2e-2, 2e-2, "last")
+    close(grads["dW"], rg["dW"], 2e-2, 2e-2, "dW")
