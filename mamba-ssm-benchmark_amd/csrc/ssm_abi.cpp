@@ -76,12 +76,15 @@ bool row_fits(const ssm_tensor &t, int64_t L, int64_t C, int esize) {
   if (s1 < 0 || s2 < 0 || s1 >= lim || s2 >= lim) return false;
   return ((L - 1 + 2 * kCK) * s1 + (C - 1 + 64) * s2 + 1) * esize < lim;
 }
+// The gate z is read through its own lane offsets, so it only needs to fit (the in_proj split
+// of models/mamba.py:100 has twice x's row stride).
 bool uniform_layout(const ssm_tensor *bld[], int nbld, const ssm_tensor &Bm, const ssm_tensor &Cm, int64_t L,
-                    int64_t D, int64_t N, int dtype) {
+                    int64_t D, int64_t N, int dtype, const ssm_tensor &z) {
   const int esize = dtype == SSM_F64 ? 8 : dtype == SSM_F32 ? 4 : 2;
   for (int i = 0; i < nbld; ++i)
     if (!same3(*bld[i], *bld[0])) return false;
-  return same3(Cm, Bm) && row_fits(*bld[0], L, D, esize) && row_fits(Bm, L, N, esize);
+  return same3(Cm, Bm) && row_fits(*bld[0], L, D, esize) && row_fits(Bm, L, N, esize) &&
+         (!has(z) || row_fits(z, L, D, esize));
 }
 
 struct FwdLayout {
@@ -215,8 +218,8 @@ static void fill_fwd(FwdParams &p, const ssm_fwd_args *a, const FwdLayout &f) {
     p.lowrank = (int)a->delta_rank;
     p.dtl = kv(a->delta); p.dtw = kv(a->delta_proj); p.dt = kv(a->x);
   }
-  const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->z, &a->out};
-  p.uniform = uniform_layout(bld, 4, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype);
+  const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->out};
+  p.uniform = uniform_layout(bld, 3, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype, a->z);
 }
 
 int ssm_fwd(const ssm_fwd_args *a, void *stream) {
@@ -321,8 +324,8 @@ int ssm_bwd(const ssm_bwd_args *a, void *stream) {
     p.lowrank = (int)a->delta_rank;
     p.dtl = kv(a->delta); p.dtw = kv(a->delta_proj); p.dt = kv(a->x);
   }
-  const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->z, &a->dout, &a->dx, &a->ddelta, &a->dz};
-  p.uniform = uniform_layout(bld, 7, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype);
+  const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->dout, &a->dx, &a->ddelta, &a->dz};
+  p.uniform = uniform_layout(bld, 6, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype, a->z);
   p.ws_dB = ws + w.dB; p.ws_dC = ws + w.dC; p.ws_dA = ws + w.dA; p.ws_dD = ws + w.dD; p.ws_db = ws + w.db;
   hipError_t e = launch_bwd(p, a->dtype, a->method, w.f.np, s);
   if (e != hipSuccess) return hip_fail(e, "ssm_bwd launch");
@@ -648,13 +651,13 @@ int ssm_decode_step(const ssm_decode_args *a, void *stream) {
 }
 
 // ------------------------------------------------------------------ causal depthwise conv
-static constexpr int kConvTB = 64;  // time steps per lane
+static constexpr int kConvTB = kConvTT * kConvTG;  // time steps per workgroup
 
 static ConvParams conv_params(const ssm_conv_args *a) {
   ConvParams p;
   memset(&p, 0, sizeof(p));
   p.B = a->batch; p.L = a->seqlen; p.D = a->dim; p.W = a->width;
-  p.TB = kConvTB;
+  p.TB = kConvTT;
   p.nblk = (int)cdiv(a->seqlen, kConvTB);
   p.silu = a->silu != 0;
   p.has_bias = has(a->bias); p.has_sin = has(a->state_in); p.has_sout = has(a->state_out);
@@ -672,8 +675,8 @@ int ssm_conv_check(const ssm_conv_args *a) {
     return fail(SSM_EINVAL, "empty conv: batch=%lld seqlen=%lld dim=%lld", (long long)a->batch,
                 (long long)a->seqlen, (long long)a->dim);
   if (a->width < 1 || a->width > 8) return fail(SSM_EINVAL, "conv width %lld not in 1..8", (long long)a->width);
-  if (a->seqlen >= (1LL << 30) || a->batch * a->dim * cdiv(a->seqlen, kConvTB) >= (1LL << 38))
-    return fail(SSM_EINVAL, "conv too large");
+  if (cdiv(a->seqlen, kConvTB) > 65535 || a->batch > 65535 || cdiv(a->dim, kConvDG) > (1LL << 31) - 1)
+    return fail(SSM_EINVAL, "conv too large (seqlen <= %d, batch <= 65535)", 65535 * kConvTB);
   REQUIRE(a->x, "x");
   REQUIRE(a->weight, "weight");
   return ok();

@@ -96,7 +96,7 @@ k_bwd(const BwdParams p) {
   CT dA_acc = 0;
   CT dD_acc = 0, db_acc = 0;  // lanes < CW: channel dw + lane
 
-  const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = with_layout<UL>(p.z, p.x);
+  const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = p.z;  // z keeps its own strides
   const KView vg = with_layout<UL>(p.dout, p.x), vdz = with_layout<UL>(p.dz, p.x);
   const KView vdx = with_layout<UL>(p.dx, p.x), vddt = with_layout<UL>(p.ddt, p.x);
   const KView vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
@@ -127,8 +127,9 @@ k_bwd(const BwdParams p) {
   // With a uniform layout x, delta, dout, z share one set of lane offsets (B, C another), and
   // they and the saved pre-gate output are read through raw buffers over one batch row.
   constexpr int ES = (int)sizeof(IT), EB = WaveTile<IT, CT, CK, NP, UL>::E;
-  uint32_t offX[E1], offB[EB], offY[E1];
+  uint32_t offX[E1], offB[EB], offY[E1], offZ[E1];
   tile_offsets<CK, CW>(offX, vx, dw, xt, lane, ES);
+  tile_offsets<CK, CW>(offZ, vzl, dw, gt, lane, ES);  // the gate (e.g. the in_proj split) may differ
   tile_offsets<CK, NP>(offB, vB, 0, bt, lane, ES);
   const KView vy{ypre, xt ? 1 : (int64_t)D, xt ? 1 : (int64_t)D, xt ? (int64_t)L : 1};  // ypre's (t, d) strides
   tile_offsets<CK, CW>(offY, vy, dw, gt, lane, (int)sizeof(CT));
@@ -158,7 +159,7 @@ k_bwd(const BwdParams p) {
       T.x.load_buf(rbx, offX, tx_);
       T.dt.load_buf(rbdt, offX, tx_);
       T.g.load_buf(rbg, offX, tx_);
-      T.z.load_buf(rbz, offX, tx_);
+      T.z.load_buf(rbz, offZ, (uint32_t)(t0 * (int)vzl.s1 * ES));
       T.B.load_buf(rbB, offB, tb_);
       T.C.load_buf(rbC, offB, tb_);
       if (p.has_z) {

@@ -2,12 +2,17 @@
 // block, models/mamba.py:101-107:
 //   xc = pad_left(x, W-1) (or [state, x]);  out = silu(conv1d(xc, w, bias, groups=D));
 //   state <- the last W-1 columns of xc.
-// x and out are (B, L, D) views (the in_proj split of models/mamba.py:100 is D-contiguous),
-// read and written with lanes along D.  One lane owns (b, d, a block of TB steps) and slides a
-// register window of the W-1 previous inputs; the block's first window comes from the inputs
-// before it (or from the carried state / zeros at t = 0).  The backward recomputes the conv
-// output for the SiLU derivative, forms dx with the transposed taps, and writes per-block
-// partial sums of dweight / dbias that a second kernel adds in a fixed order.
+// x and out are (B, L, D) views (the in_proj split of models/mamba.py:100 is D-contiguous).
+// A workgroup covers 64 channels x 32 time steps; a lane owns one channel and kConvTT = 8
+// consecutive steps, reads the W-1 inputs before them as well (neighbouring lanes along D make
+// every read coalesced; the overlap between time blocks is served from cache), and all its
+// reads are issued before any arithmetic, so the kernel is bound by HBM rather than by a chain
+// of dependent loads.  Because kConvTT >= W-1, only a lane of the first time block reads the
+// carried state, and that lane also writes the new state (after reading), so the update can
+// be in place.  The backward recomputes the pre-activation for the SiLU derivative, forms dx
+// with the transposed taps, and reduces dweight / dbias over the workgroup's 4 time blocks in
+// LDS before writing one partial row per workgroup; a second kernel adds the rows in a fixed
+// order.
 #include "ssm_device.hpp"
 #include "ssm_internal.hpp"
 #include "ssm_tiles.hpp"
@@ -19,146 +24,164 @@ __device__ __forceinline__ CT silu_ct(CT v) {
   return v * sigmoid_ct<CT>(v);
 }
 
+constexpr int kConvThreads = kConvDG * kConvTG;
+
+// input at time s of [state, x] for channel d of batch row b (0 past the end)
 template <typename IT, int W>
-__global__ void __launch_bounds__(kThreads) k_conv_fwd(const ConvParams p) {
+__device__ __forceinline__ typename Conv<IT>::CT conv_in(const ConvParams &p, int64_t b, int64_t d, int s) {
   typedef typename Conv<IT>::CT CT;
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= p.B * p.D * p.nblk) return;
-  const int64_t d = i % p.D, blk = (i / p.D) % p.nblk, b = i / (p.D * p.nblk);
+  if (s >= 0) return s < (int)p.L ? Conv<IT>::load(vp<IT>(p.x) + b * p.x.s0 + (int64_t)s * p.x.s1 + d * p.x.s2) : (CT)0;
+  if (!p.has_sin) return (CT)0;
+  return Conv<IT>::load(vp<IT>(p.sin) + b * p.sin.s0 + d * p.sin.s1 + (int64_t)(W - 1 + s) * p.sin.s2);
+}
+
+template <typename IT, int W>
+__global__ void __launch_bounds__(kConvThreads) k_conv_fwd(const ConvParams p) {
+  typedef typename Conv<IT>::CT CT;
+  constexpr int TT = kConvTT, NX = TT + W - 1;
+  const int64_t d = (int64_t)blockIdx.x * kConvDG + threadIdx.x % kConvDG;
+  const int t0 = ((int)blockIdx.y * kConvTG + (int)threadIdx.x / kConvDG) * TT;
+  const int64_t b = blockIdx.z;
   const int L = (int)p.L;
-  const int t0 = (int)blk * p.TB, t1 = t0 + p.TB < L ? t0 + p.TB : L;
-  const IT *xb = vp<IT>(p.x) + b * p.x.s0 + d * p.x.s2;
-  CT w[W];
+  if (d >= p.D || t0 >= L) return;
+  CT w[W], xin[NX];  // xin[k]: input at time t0 - (W-1) + k
 #pragma unroll
   for (int j = 0; j < W; ++j) w[j] = vload<CT>(p.w, d * p.w.s0 + j * p.w.s1);
   const CT bias = p.has_bias ? vload<CT>(p.bias, d * p.bias.s0) : (CT)0;
-  // win[j] = input at time t - (W-1) + j for the next output t
-  CT win[W > 1 ? W - 1 : 1];
 #pragma unroll
-  for (int j = 0; j < W - 1; ++j) {
-    const int s = t0 - (W - 1) + j;
-    if (s >= 0) win[j] = Conv<IT>::load(xb + (int64_t)s * p.x.s1);
-    else win[j] = p.has_sin ? Conv<IT>::load(vp<IT>(p.sin) + b * p.sin.s0 + d * p.sin.s1 + (W - 1 + s) * p.sin.s2) : (CT)0;
-  }
-  if (p.has_sout && blk == 0) {
-    // the new state: inputs L-(W-1) .. L-1 of [state, x]; written by the block that reads the
-    // old state, so an in-place update (sout == sin) is safe
+  for (int k = 0; k < NX; ++k) xin[k] = conv_in<IT, W>(p, b, d, t0 - (W - 1) + k);
+  if (p.has_sout && t0 == 0) {
+    // the new state: inputs L-(W-1) .. L-1 of [state, x]; this lane is the only reader of the
+    // old state, and it reads before it writes
+    CT ns[W > 1 ? W - 1 : 1];
 #pragma unroll
-    for (int j = 0; j < W - 1; ++j) {
-      const int s = L - (W - 1) + j;
-      CT v;
-      if (s >= 0) v = Conv<IT>::load(xb + (int64_t)s * p.x.s1);
-      else v = p.has_sin ? Conv<IT>::load(vp<IT>(p.sin) + b * p.sin.s0 + d * p.sin.s1 + (W - 1 + s) * p.sin.s2) : (CT)0;
-      Conv<IT>::store(vpw<IT>(p.sout) + b * p.sout.s0 + d * p.sout.s1 + j * p.sout.s2, v);
-    }
+    for (int j = 0; j < W - 1; ++j) ns[j] = conv_in<IT, W>(p, b, d, L - (W - 1) + j);
+#pragma unroll
+    for (int j = 0; j < W - 1; ++j) Conv<IT>::store(vpw<IT>(p.sout) + b * p.sout.s0 + d * p.sout.s1 + j * p.sout.s2, ns[j]);
   }
   IT *ob = vpw<IT>(p.out) + b * p.out.s0 + d * p.out.s2;
-  for (int t = t0; t < t1; ++t) {
-    const CT xv = Conv<IT>::load(xb + (int64_t)t * p.x.s1);
-    CT acc = fma(w[W - 1], xv, bias);
 #pragma unroll
-    for (int j = 0; j < W - 1; ++j) acc = fma(w[j], win[j], acc);
+  for (int tt = 0; tt < TT; ++tt) {
+    CT acc = bias;
 #pragma unroll
-    for (int j = 0; j + 1 < W - 1; ++j) win[j] = win[j + 1];
-    if constexpr (W > 1) win[W - 2] = xv;
-    Conv<IT>::store(ob + (int64_t)t * p.out.s1, p.silu ? silu_ct(acc) : acc);
+    for (int j = 0; j < W; ++j) acc = fma(w[j], xin[tt + j], acc);
+    if (t0 + tt < L) Conv<IT>::store(ob + (int64_t)(t0 + tt) * p.out.s1, p.silu ? silu_ct(acc) : acc);
   }
 }
 
 template <typename IT, int W>
-__global__ void __launch_bounds__(kThreads) k_conv_bwd(const ConvParams p) {
+__global__ void __launch_bounds__(kConvThreads) k_conv_bwd(const ConvParams p) {
   typedef typename Conv<IT>::CT CT;
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= p.B * p.D * p.nblk) return;
-  const int64_t d = i % p.D, blk = (i / p.D) % p.nblk, b = i / (p.D * p.nblk);
+  constexpr int TT = kConvTT, NG = TT + W - 1, NX = TT + 2 * (W - 1);
+  __shared__ CT red[kConvTG][W + 1][kConvDG];
+  const int dl = threadIdx.x % kConvDG, tg = threadIdx.x / kConvDG;
+  const int64_t d = (int64_t)blockIdx.x * kConvDG + dl;
+  const int t0 = ((int)blockIdx.y * kConvTG + tg) * TT;
+  const int64_t b = blockIdx.z;
   const int L = (int)p.L;
-  const int t0 = (int)blk * p.TB, t1 = t0 + p.TB < L ? t0 + p.TB : L;
-  const IT *xb = vp<IT>(p.x) + b * p.x.s0 + d * p.x.s2;
-  const IT *gb = vp<IT>(p.dout) + b * p.dout.s0 + d * p.dout.s2;
-  IT *dxb = vpw<IT>(p.dx) + b * p.dx.s0 + d * p.dx.s2;
-  CT w[W];
+  const bool live = d < p.D && t0 < L;
+  const int64_t dc = live ? d : 0;
+  CT dwp[W + 1];  // dweight taps, then dbias
 #pragma unroll
-  for (int j = 0; j < W; ++j) w[j] = vload<CT>(p.w, d * p.w.s0 + j * p.w.s1);
-  const CT bias = p.has_bias ? vload<CT>(p.bias, d * p.bias.s0) : (CT)0;
-  auto xat = [&](int s) -> CT {  // input at time s of [state, x]
-    if (s >= 0) return s < L ? Conv<IT>::load(xb + (int64_t)s * p.x.s1) : (CT)0;
-    return p.has_sin ? Conv<IT>::load(vp<IT>(p.sin) + b * p.sin.s0 + d * p.sin.s1 + (W - 1 + s) * p.sin.s2) : (CT)0;
-  };
-  // xw[j]: input at time t' - (W-1) + j for the conv output at t'; gw[j]: g at time t' - j
-  CT xw[W > 1 ? W - 1 : 1], gw[W];
+  for (int j = 0; j <= W; ++j) dwp[j] = 0;
+  if (live) {
+    CT w[W], xin[NX], g[NG];  // xin[k]: input at t0 - (W-1) + k; g[k]: dout x silu' at t0 + k
 #pragma unroll
-  for (int j = 0; j < W - 1; ++j) xw[j] = xat(t0 - (W - 1) + j);
+    for (int j = 0; j < W; ++j) w[j] = vload<CT>(p.w, dc * p.w.s0 + j * p.w.s1);
+    const CT bias = p.has_bias ? vload<CT>(p.bias, dc * p.bias.s0) : (CT)0;
 #pragma unroll
-  for (int j = 0; j < W; ++j) gw[j] = 0;
-  CT dwp[W], dbp = 0;
+    for (int k = 0; k < NX; ++k) xin[k] = conv_in<IT, W>(p, b, dc, t0 - (W - 1) + k);
+    const IT *gb = vp<IT>(p.dout) + b * p.dout.s0 + dc * p.dout.s2;
 #pragma unroll
-  for (int j = 0; j < W; ++j) dwp[j] = 0;
-  const int tend = t1 + W - 1 < L ? t1 + W - 1 : L;  // g is needed up to t1 + W - 2
-  for (int tp = t0; tp < t1 + W - 1; ++tp) {
-    CT g = 0, xv = 0;
-    if (tp < tend) {
-      xv = Conv<IT>::load(xb + (int64_t)tp * p.x.s1);
-      CT pre = fma(w[W - 1], xv, bias);
+    for (int k = 0; k < NG; ++k)
+      g[k] = t0 + k < L ? Conv<IT>::load(gb + (int64_t)(t0 + k) * p.dout.s1) : (CT)0;
 #pragma unroll
-      for (int j = 0; j < W - 1; ++j) pre = fma(w[j], xw[j], pre);
-      g = Conv<IT>::load(gb + (int64_t)tp * p.dout.s1);
+    for (int k = 0; k < NG; ++k) {
       if (p.silu) {
-        const CT sg = sigmoid_ct<CT>(pre);
-        g *= sg * ((CT)1 + pre * ((CT)1 - sg));
-      }
-      if (tp < t1) {  // this block's own steps feed dweight / dbias
+        CT pre = bias;
 #pragma unroll
-        for (int j = 0; j < W - 1; ++j) dwp[j] = fma(g, xw[j], dwp[j]);
-        dwp[W - 1] = fma(g, xv, dwp[W - 1]);
-        dbp += g;
+        for (int j = 0; j < W; ++j) pre = fma(w[j], xin[k + j], pre);
+        const CT sg = sigmoid_ct<CT>(pre);
+        g[k] *= sg * ((CT)1 + pre * ((CT)1 - sg));
       }
     }
+    IT *dxb = vpw<IT>(p.dx) + b * p.dx.s0 + dc * p.dx.s2;
 #pragma unroll
-    for (int j = W - 1; j > 0; --j) gw[j] = gw[j - 1];
-    gw[0] = g;
-#pragma unroll
-    for (int j = 0; j + 1 < W - 1; ++j) xw[j] = xw[j + 1];
-    if constexpr (W > 1) xw[W - 2] = xv;
-    const int t = tp - (W - 1);  // dx[t] = sum_j w[j] g[t + W-1 - j] = sum_j w[j] gw[j]
-    if (t >= t0) {
+    for (int tt = 0; tt < TT; ++tt) {
+      // dx[t] = sum_j w[j] g[t + W-1 - j]
       CT acc = 0;
 #pragma unroll
-      for (int j = 0; j < W; ++j) acc = fma(w[j], gw[j], acc);
-      Conv<IT>::store(dxb + (int64_t)t * p.dx.s1, acc);
+      for (int j = 0; j < W; ++j) acc = fma(w[j], g[tt + W - 1 - j], acc);
+      if (t0 + tt < L) {
+        Conv<IT>::store(dxb + (int64_t)(t0 + tt) * p.dx.s1, acc);
+#pragma unroll
+        for (int j = 0; j < W; ++j) dwp[j] = fma(g[tt], xin[tt + j], dwp[j]);
+        dwp[W] += g[tt];
+      }
     }
   }
-  CT *ws = (CT *)p.ws;
-  const int64_t row = b * p.nblk + blk;
 #pragma unroll
-  for (int j = 0; j < W; ++j) ws[(row * p.D + d) * (W + 1) + j] = dwp[j];
-  ws[(row * p.D + d) * (W + 1) + W] = dbp;
+  for (int j = 0; j <= W; ++j) red[tg][j][dl] = dwp[j];
+  __syncthreads();
+  // one partial row per workgroup: the 4 time blocks in order
+  const int64_t row = b * p.nblk + blockIdx.y;
+  for (int e = threadIdx.x; e < (W + 1) * kConvDG; e += kConvThreads) {
+    const int j = e / kConvDG, l = e % kConvDG;
+    const int64_t dd = (int64_t)blockIdx.x * kConvDG + l;
+    if (dd >= p.D) continue;
+    CT sum = 0;
+#pragma unroll
+    for (int q = 0; q < kConvTG; ++q) sum += red[q][j][l];
+    ((CT *)p.ws)[(row * p.D + dd) * (W + 1) + j] = sum;
+  }
 }
 
-template <typename CT>
-__global__ void __launch_bounds__(kThreads) k_conv_fin(const ConvParams p) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  const int W = (int)p.W;
-  if (i >= p.D * (W + 1)) return;
-  const int64_t d = i / (W + 1);
-  const int j = (int)(i % (W + 1));
+// dweight / dbias: the B * nblk partial rows summed in a fixed order.  A workgroup owns 64
+// channels; its 16 row groups sum rows r = g, g + 16, ... (independent loads in flight), and
+// the groups are added in order.
+constexpr int kConvFinGroups = 16;
+
+template <typename CT, int W>
+__global__ void __launch_bounds__(kConvDG * kConvFinGroups) k_conv_fin(const ConvParams p) {
+  __shared__ CT red[kConvFinGroups][W + 1][kConvDG];
+  const int dl = threadIdx.x % kConvDG, g = threadIdx.x / kConvDG;
+  const int64_t d = (int64_t)blockIdx.x * kConvDG + dl;
+  const int64_t rows = p.B * p.nblk;
   const CT *ws = (const CT *)p.ws;
-  CT s = 0;
-  for (int64_t r = 0; r < p.B * p.nblk; ++r) s += ws[(r * p.D + d) * (W + 1) + j];
-  if (j < W) vstore<CT>(p.dw, d * p.dw.s0 + j * p.dw.s1, s);
-  else if (p.has_dbias) vstore<CT>(p.dbias, d * p.dbias.s0, s);
+  CT acc[W + 1];
+#pragma unroll
+  for (int j = 0; j <= W; ++j) acc[j] = 0;
+  if (d < p.D) {
+#pragma unroll 4
+    for (int64_t r = g; r < rows; r += kConvFinGroups) {
+#pragma unroll
+      for (int j = 0; j <= W; ++j) acc[j] += ws[(r * p.D + d) * (W + 1) + j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j <= W; ++j) red[g][j][dl] = acc[j];
+  __syncthreads();
+  for (int e = threadIdx.x; e < (W + 1) * kConvDG; e += kConvDG * kConvFinGroups) {
+    const int j = e / kConvDG, l = e % kConvDG;
+    const int64_t dd = (int64_t)blockIdx.x * kConvDG + l;
+    if (dd >= p.D) continue;
+    CT s = 0;
+#pragma unroll
+    for (int q = 0; q < kConvFinGroups; ++q) s += red[q][j][l];
+    if (j < W) vstore<CT>(p.dw, dd * p.dw.s0 + j * p.dw.s1, s);
+    else if (p.has_dbias) vstore<CT>(p.dbias, dd * p.dbias.s0, s);
+  }
 }
 
 template <typename IT, int W>
 static hipError_t conv_t(const ConvParams &p, bool bwd, hipStream_t s) {
   typedef typename Conv<IT>::CT CT;
-  const int64_t n = p.B * p.D * p.nblk;
-  const dim3 grid((unsigned)((n + kThreads - 1) / kThreads));
+  const dim3 grid((unsigned)((p.D + kConvDG - 1) / kConvDG), (unsigned)p.nblk, (unsigned)p.B);
   if (!bwd) {
-    hipLaunchKernelGGL((k_conv_fwd<IT, W>), grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((k_conv_fwd<IT, W>), grid, dim3(kConvThreads), 0, s, p);
   } else {
-    hipLaunchKernelGGL((k_conv_bwd<IT, W>), grid, dim3(kThreads), 0, s, p);
-    const int64_t m = p.D * (W + 1);
-    hipLaunchKernelGGL((k_conv_fin<CT>), dim3((unsigned)((m + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((k_conv_bwd<IT, W>), grid, dim3(kConvThreads), 0, s, p);
+    hipLaunchKernelGGL((k_conv_fin<CT, W>), dim3(grid.x), dim3(kConvDG * kConvFinGroups), 0, s, p);
   }
   return hipGetLastError();
 }

@@ -77,7 +77,7 @@ k_fwd(const FwdParams p) {
     else if (p.has_h0) h = vload<CT>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
   }
 
-  const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = with_layout<UL>(p.z, p.x);
+  const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = p.z;  // z keeps its own strides
   const KView vout = with_layout<UL>(p.out, p.x), vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
   const bool xt = vx.s1 == 1, dtt = vdt.s1 == 1, bt = vB.s1 == 1, ctt = vC.s1 == 1;
   const bool ot = vout.s1 == 1;
@@ -100,9 +100,10 @@ k_fwd(const FwdParams p) {
   // read through raw buffers; otherwise through clamped global addresses.
   constexpr int ES = (int)sizeof(IT);
   constexpr int EX = WaveTile<IT, CT, CK, CW, UL>::E, EB = WaveTile<IT, CT, CK, NP, UL>::E;
-  uint32_t offX[EX], offB[EB];
+  uint32_t offX[EX], offB[EB], offZ[EX];
   tile_offsets<CK, CW>(offX, vx, dw, xt, lane, ES);
   tile_offsets<CK, NP>(offB, vB, 0, bt, lane, ES);
+  tile_offsets<CK, CW>(offZ, vzl, dw, ot, lane, ES);  // the gate (e.g. the in_proj split) may differ
   const __amdgpu_buffer_rsrc_t empty = __builtin_amdgcn_make_buffer_rsrc((void *)p.x.p, (short)0, 0, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES);
   const __amdgpu_buffer_rsrc_t rbdt = LR ? empty : row_buffer(vdt, b, L, D, ES);
@@ -126,7 +127,7 @@ k_fwd(const FwdParams p) {
       T.dt.load_buf(rbdt, offX, tx_);
       T.B.load_buf(rbB, offB, tb_);
       if (!SUM) T.C.load_buf(rbC, offB, tb_);
-      if (!SUM) T.z.load_buf(rbz, offX, tx_);
+      if (!SUM) T.z.load_buf(rbz, offZ, (uint32_t)(t0 * (int)vzl.s1 * ES));
     } else {
       T.x.load(vx, b, t0, L, dw, D, xt, lane);
       T.dt.load(vdt, b, t0, L, dw, D, dtt, lane);

@@ -148,12 +148,15 @@ struct DiscParams {
 };
 
 // Causal depthwise conv over (B, L, D) views; a lane owns (b, d, one block of TB steps).
+// Causal conv: a workgroup covers kConvDG channels x kConvTG lanes of kConvTT time steps
+// (kConvTT >= W - 1 for every width <= 8).
+constexpr int kConvTT = 8, kConvTG = 4, kConvDG = 64;
 struct ConvParams {
   int64_t B, L, D, W;
-  int nblk, TB;
+  int nblk, TB;  // time blocks of kConvTG * kConvTT steps (one workgroup row each), kConvTT
   int silu, has_bias, has_sin, has_sout, has_dbias;
   KView x, w, bias, sin, out, sout, dout, dx, dw, dbias;  // sin / sout: (B, D, W-1)
-  void *ws;  // backward: (B * nblk, D, W + 1) partial dweight / dbias
+  void *ws;  // backward: (B * nblk, D, W + 1) partial dweight / dbias, one row per workgroup
 };
 
 // Fused decode layer (float32, row-major); one workgroup per batch row.
