@@ -20,6 +20,7 @@ reference's CPU path (oracle/cpu_chunked.py), timed on a bounded sample of the s
 
 Other workloads (--workload): c0 (forward, B1 L512), c2 / c2bf16 (long-sequence forward),
 c3 (10-layer Mamba LM fwd+bwd), c4 (decode latency per layer at batch 64, HIP-graph replay),
+scans (the composed path's linear-scan algorithms and discretization, GB/s per kernel),
 copy (a plain device copy of known size, for PMC counter calibration).
 """
 
@@ -365,6 +366,56 @@ def bench_decode(args, dev):
             "tokens_per_s": B / (ms * 1e-3)}
 
 
+def bench_scans(args, dev):
+    """The composed path's kernels (models/scan.py's algorithms on the engine): each linear-scan
+    algorithm on (B, L, M) = (2, 4096, 16384) float32 (a, b read, h written: 3 x 4 x B L M
+    algorithmic bytes), and the materialized ZOH discretization on (B, L, D, N) =
+    (2, 4096, 1024, 16) (a, b written; delta, x, B read).  Device time per launch from HIP
+    events on the launch stream, against 8 TB/s."""
+    import ssm_scan
+    from ssm_scan import scan as S
+    B, L, M = 2, 4096, 16384
+    g = torch.Generator().manual_seed(0)
+    a = torch.rand(B, L, M, generator=g).to(dev) * 0.5 + 0.5
+    b = torch.randn(B, L, M, generator=g).to(dev)
+    lines = {}
+    for name in ("sequential", "hillis_steele", "blelloch", "chunked"):
+        fn = S.SCANS[name]
+        with torch.no_grad():
+            for _ in range(2):
+                fn(a, b)
+            with ssm_scan.KernelTimer() as tm:
+                for _ in range(args.steps):
+                    fn(a, b)
+        t = statistics.median(tm.times_ms()["ssm_lscan"])
+        nbytes = 3 * 4 * B * L * M
+        lines[name] = {"ms": t, "GB/s": nbytes / (t * 1e-3) / 1e9, "frac": nbytes / (t * 1e-3) / (HBM_PEAK_GBS * 1e9),
+                       "alg_bytes": nbytes}
+    del a, b
+    D, N = 1024, 16
+    delta = (torch.rand(B, L, D, generator=g) * 0.1).to(dev)
+    x = torch.randn(B, L, D, generator=g).to(dev)
+    Bm = torch.randn(B, L, N, generator=g).to(dev)
+    A = -torch.arange(1, N + 1, dtype=torch.float32).repeat(D, 1).to(dev)
+    with torch.no_grad():
+        for _ in range(2):
+            S.discretize(delta, A, Bm, x)
+        with ssm_scan.KernelTimer() as tm:
+            for _ in range(args.steps):
+                S.discretize(delta, A, Bm, x)
+    t = statistics.median(tm.times_ms()["ssm_disc_fwd"])
+    nbytes = 2 * 4 * B * L * D * N + 4 * (2 * B * L * D + B * L * N + D * N)
+    lines["discretize_zoh"] = {"ms": t, "GB/s": nbytes / (t * 1e-3) / 1e9,
+                               "frac": nbytes / (t * 1e-3) / (HBM_PEAK_GBS * 1e9), "alg_bytes": nbytes}
+    best = max(lines, key=lambda k: lines[k]["frac"])
+    return {"metric": "composed-path kernels, HBM GB/s (linear scans B2 L4096 M16384, discretize B2 L4096 D1024 N16)",
+            "value": lines[best]["GB/s"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 2,
+            "ms_per_step": lines[best]["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32", "data": "synthetic", "config": {"workload": "composed path (models/scan.py algorithms)",
+                                                             "best": best},
+            "kernels": lines}
+
+
 def bench_copy(args, dev):
     """A plain device copy of 256 MiB (reads 256 MiB, writes 256 MiB): PMC calibration."""
     src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
@@ -381,7 +432,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "c3", "c4", "copy"])
+    ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "c3", "c4", "scans", "copy"])
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--seqlen", type=int, default=131072)
     ap.add_argument("--segments", type=int, default=0, help="forward time segments (0 = automatic)")
@@ -407,6 +458,8 @@ def main():
         rec = bench_lm(args, dev)
     elif args.workload == "c4":
         rec = bench_decode(args, dev)
+    elif args.workload == "scans":
+        rec = bench_scans(args, dev)
     else:
         rec = bench_copy(args, dev)
     print(json.dumps(rec), flush=True)

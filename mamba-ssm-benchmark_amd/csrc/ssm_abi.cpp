@@ -557,7 +557,8 @@ int ssm_disc_check(const ssm_disc_args *a) {
   if (rc) return rc;
   if (a->dtype != SSM_F32 && a->dtype != SSM_F64)
     return fail(SSM_EINVAL, "materialized discretization takes float32 or float64");
-  if (a->batch * a->seqlen * a->dim * a->dstate >= (1LL << 39)) return fail(SSM_EINVAL, "problem too large");
+  if (a->batch * a->seqlen * a->dim * a->dstate >= (1LL << 39) || a->dim * a->dstate >= (1LL << 31))
+    return fail(SSM_EINVAL, "problem too large");
   REQUIRE(a->delta, "delta");
   REQUIRE(a->x, "x");
   REQUIRE(a->A, "A");

@@ -19,19 +19,25 @@ namespace ssm {
 
 template <typename CT, int METHOD>
 __global__ void __launch_bounds__(kThreads) k_disc_fwd(const DiscParams p) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  const int64_t total = p.B * p.L * p.D * p.N;
-  if (i >= total) return;
-  const int64_t n = i % p.N, d = (i / p.N) % p.D, row = i / (p.N * p.D);
-  const int64_t b = row / p.L, t = row % p.L;
-  const CT dt = vload<CT>(p.delta, b * p.delta.s0 + t * p.delta.s1 + d * p.delta.s2);
-  const CT xv = vload<CT>(p.x, b * p.x.s0 + t * p.x.s1 + d * p.x.s2);
-  const CT Bv = vload<CT>(p.Bm, b * p.Bm.s0 + t * p.Bm.s1 + n * p.Bm.s2);
+  // grid: x over the D*N elements of a (b, t) row (32-bit index, contiguous outputs), y over t
+  // (about 8 rows per lane), z over b (striding); the per-(d, n) constants are formed once
+  const int e = blockIdx.x * kThreads + threadIdx.x;
+  const int DN = (int)(p.D * p.N);
+  if (e >= DN) return;
+  const int n = e % (int)p.N, d = e / (int)p.N;
   const AConst<CT> ac = make_aconst(vload<CT>(p.A, d * p.A.s0 + n * p.A.s1));
-  CT a, coef;
-  disc<METHOD>(dt, ac, a, coef);
-  ((CT *)p.a)[i] = a;
-  ((CT *)p.b)[i] = bcoef<METHOD>(dt, coef) * (Bv * xv);
+  for (int64_t b = blockIdx.z; b < p.B; b += gridDim.z) {
+    for (int64_t t = blockIdx.y; t < p.L; t += gridDim.y) {
+      const CT dt = vload<CT>(p.delta, b * p.delta.s0 + t * p.delta.s1 + d * p.delta.s2);
+      const CT xv = vload<CT>(p.x, b * p.x.s0 + t * p.x.s1 + d * p.x.s2);
+      const CT Bv = vload<CT>(p.Bm, b * p.Bm.s0 + t * p.Bm.s1 + n * p.Bm.s2);
+      CT a, coef;
+      disc<METHOD>(dt, ac, a, coef);
+      const int64_t i = (b * p.L + t) * DN + e;
+      ((CT *)p.a)[i] = a;
+      ((CT *)p.b)[i] = bcoef<METHOD>(dt, coef) * (Bv * xv);
+    }
+  }
 }
 
 template <typename CT, int NP, int METHOD>
@@ -47,8 +53,8 @@ __global__ void __launch_bounds__(kThreads) k_disc_bwd(const DiscParams p) {
   AConst<CT> ac = make_aconst<CT>(-1);
   if (valid) ac = make_aconst(vload<CT>(p.A, d * p.A.s0 + n * p.A.s1));
   CT gA = 0;
-  for (int64_t r = r0; r < r1; ++r) {
-    const int64_t b = r / p.L, t = r % p.L;
+  int64_t b = r0 / p.L, t = r0 - (r0 / p.L) * p.L;  // (b, t) of row r, advanced incrementally
+  for (int64_t r = r0; r < r1; ++r, t = t + 1 < p.L ? t + 1 : 0, b += t == 0 ? 1 : 0) {
     CT gd = 0, gx = 0, gB = 0;
     if (valid) {
       const CT dt = vload<CT>(p.delta, b * p.delta.s0 + t * p.delta.s1 + d * p.delta.s2);
@@ -71,7 +77,6 @@ __global__ void __launch_bounds__(kThreads) k_disc_bwd(const DiscParams p) {
       gx += __shfl_xor(gx, off);
     }
     if (n == 0 && d < p.D) {
-      const int64_t b = r / p.L, t = r % p.L;
       vstore<CT>(p.ddelta, b * p.ddelta.s0 + t * p.ddelta.s1 + d * p.ddelta.s2, gd);
       vstore<CT>(p.dx, b * p.dx.s0 + t * p.dx.s1 + d * p.dx.s2, gx);
     }
@@ -109,9 +114,10 @@ __global__ void __launch_bounds__(kThreads) k_disc_fin(const DiscParams p) {
 
 template <typename CT, int M>
 static hipError_t disc_fwd_t(const DiscParams &p, hipStream_t s) {
-  const int64_t total = p.B * p.L * p.D * p.N;
-  hipLaunchKernelGGL((k_disc_fwd<CT, M>), dim3((unsigned)((total + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                     s, p);
+  const int64_t ty = (p.L + 7) / 8;  // about 8 time rows per lane
+  const dim3 grid((unsigned)((p.D * p.N + kThreads - 1) / kThreads), (unsigned)(ty < 65535 ? ty : 65535),
+                  (unsigned)(p.B < 65535 ? p.B : 65535));
+  hipLaunchKernelGGL((k_disc_fwd<CT, M>), grid, dim3(kThreads), 0, s, p);
   return hipGetLastError();
 }
 

@@ -3,14 +3,18 @@
 // Replaces the four torch scans of models/scan.py with kernels that keep each algorithm's
 // structure (so `scan=` still selects an algorithm, as in the reference's SCANS registry,
 // models/scan.py:168-173):
-//   sequential     models/scan.py:70-76    one lane per (b, m) walks the sequence.
-//   hillis_steele  models/scan.py:87-98    a 256-lane workgroup per (b, m) runs recursive
-//                                          doubling over tiles of 256 steps in LDS; the state
-//                                          entering a tile is folded into its first element
-//                                          (as _fold_h0 does with h0, :79-84).
-//   blelloch       models/scan.py:101-135  up-sweep / down-sweep over tiles of 512 steps in
-//                                          LDS, giving exclusive (A, S) prefixes; h = a (A h_in
-//                                          + S) + b, the tile's last h carried to the next.
+//   sequential     models/scan.py:70-76    one lane per (b, m) walks the sequence, reading 16
+//                                          steps ahead of the dependent updates.
+//   hillis_steele  models/scan.py:87-98    a workgroup owns 64 neighbouring recurrences (lanes
+//                                          along m, so every global access is coalesced) and
+//                                          runs recursive doubling along time over tiles of 32
+//                                          steps in LDS; the state entering a tile is folded
+//                                          into its first element (as _fold_h0 does with h0,
+//                                          :79-84).
+//   blelloch       models/scan.py:101-135  the same 64-recurrence workgroups; up-sweep /
+//                                          down-sweep along time over tiles of 64 steps in LDS,
+//                                          giving exclusive (A, S) prefixes; h = a (A h_in + S)
+//                                          + b, the tile's last h carried to the next.
 //   chunked        models/scan.py:142-165  three launches: per-chunk local scans from zero
 //                                          (chunk summaries P = prod a, E = local end), a scan
 //                                          over the chunk summaries per (b, m), then the
@@ -47,49 +51,96 @@ struct Chain {
 };
 
 // ------------------------------------------------------------------ sequential
+constexpr int kSeqAhead = 16;  // steps whose inputs are read before their dependent updates
+
 template <typename CT>
 __global__ void __launch_bounds__(256) k_lscan_seq(const LscanParams P) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= P.B * P.M) return;
   Chain<CT> ch{P, i / P.M, i % P.M};
+  const int L = (int)P.L;
   CT h = ch.h0();
-  for (int pos = 0; pos < (int)P.L; ++pos) {
-    const int t = ch.t_of(pos);
-    h = fma(ch.mult(pos), h, ch.b_at(t));
-    vstore<CT>(P.h, ch.h_off(t), h);
+  int pos = 0;
+  for (; pos + kSeqAhead <= L; pos += kSeqAhead) {
+    CT av[kSeqAhead], bv[kSeqAhead];
+#pragma unroll
+    for (int u = 0; u < kSeqAhead; ++u) {
+      av[u] = ch.mult(pos + u);
+      bv[u] = ch.b_at(ch.t_of(pos + u));
+    }
+#pragma unroll
+    for (int u = 0; u < kSeqAhead; ++u) {
+      h = fma(av[u], h, bv[u]);
+      vstore<CT>(P.h, ch.h_off(ch.t_of(pos + u)), h);
+    }
+  }
+  for (; pos < L; ++pos) {
+    h = fma(ch.mult(pos), h, ch.b_at(ch.t_of(pos)));
+    vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), h);
   }
 }
+
+// Tiled parallel scans: a workgroup of 256 lanes owns kScanMC recurrences m (lane % 64) of one
+// batch row; lane / 64 selects which time rows of a tile the lane loads, updates and stores.
+constexpr int kScanMC = 64, kScanRowLanes = 4;
 
 // ------------------------------------------------------------------ Hillis-Steele
 template <typename CT>
 __global__ void __launch_bounds__(256) k_lscan_hs(const LscanParams P) {
-  constexpr int T = 256;
-  __shared__ CT sA[2][T], sS[2][T];
-  Chain<CT> ch{P, (int64_t)blockIdx.y, (int64_t)blockIdx.x};
-  const int j = threadIdx.x;
+  constexpr int T = 32, RL = kScanRowLanes, R = T / RL;
+  __shared__ CT sA[2][T][kScanMC], sS[2][T][kScanMC];
+  const int mi = threadIdx.x % kScanMC, tr = threadIdx.x / kScanMC;
+  const int64_t m = (int64_t)blockIdx.x * kScanMC + mi;
+  const bool mval = m < P.M;
+  Chain<CT> ch{P, (int64_t)blockIdx.y, mval ? m : 0};
+  const int L = (int)P.L;
   CT carry = ch.h0();
-  for (int base = 0; base < (int)P.L; base += T) {
-    const int pos = base + j;
-    const bool valid = pos < (int)P.L;
-    CT A = valid ? ch.mult(pos) : (CT)1;
-    CT S = valid ? ch.b_at(ch.t_of(pos)) : (CT)0;
-    if (j == 0) S = fma(A, carry, S);  // fold the incoming state into the first element
-    int cur = 0;
-    sA[cur][j] = A;
-    sS[cur][j] = S;
+  // a tile's inputs are read while the previous tile is scanned
+  CT na[R], nb[R];
+  auto fetch = [&](int base) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int pos = base + tr + RL * r;
+      const bool valid = mval && pos < L;
+      na[r] = valid ? ch.mult(pos) : (CT)1;
+      nb[r] = valid ? ch.b_at(ch.t_of(pos)) : (CT)0;
+    }
+  };
+  fetch(0);
+  for (int base = 0; base < L; base += T) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = tr + RL * r;
+      const CT A = na[r];
+      CT S = nb[r];
+      if (k == 0) S = fma(A, carry, S);  // fold the incoming state into the first element
+      sA[0][k][mi] = A;
+      sS[0][k][mi] = S;
+    }
     __syncthreads();
-    for (int off = 1; off < T; off *= 2) {  // after this step: composition of 2*off elements
-      if (j >= off) {
-        S = fma(A, sS[cur][j - off], S);
-        A = A * sA[cur][j - off];
+    if (base + T < L) fetch(base + T);
+    int cur = 0;
+    for (int off = 1; off < T; off *= 2) {  // after this step: compositions of 2*off elements
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int k = tr + RL * r;
+        CT A = sA[cur][k][mi], S = sS[cur][k][mi];
+        if (k >= off) {
+          S = fma(A, sS[cur][k - off][mi], S);
+          A = A * sA[cur][k - off][mi];
+        }
+        sA[cur ^ 1][k][mi] = A;
+        sS[cur ^ 1][k][mi] = S;
       }
-      sA[cur ^ 1][j] = A;
-      sS[cur ^ 1][j] = S;
       cur ^= 1;
       __syncthreads();
     }
-    if (valid) vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), S);
-    carry = sS[cur][T - 1];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = tr + RL * r, pos = base + k;
+      if (mval && pos < L) vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), sS[cur][k][mi]);
+    }
+    carry = sS[cur][T - 1][mi];
     __syncthreads();
   }
 }
@@ -97,65 +148,74 @@ __global__ void __launch_bounds__(256) k_lscan_hs(const LscanParams P) {
 // ------------------------------------------------------------------ Blelloch
 template <typename CT>
 __global__ void __launch_bounds__(256) k_lscan_bl(const LscanParams P) {
-  constexpr int T = 512;  // elements per tile, two per lane
-  __shared__ CT sA[T], sS[T];
-  Chain<CT> ch{P, (int64_t)blockIdx.y, (int64_t)blockIdx.x};
-  const int j = threadIdx.x;
+  constexpr int T = 64, RL = kScanRowLanes, R = T / RL;
+  __shared__ CT sA[T][kScanMC], sS[T][kScanMC], sLast[kScanMC];
+  const int mi = threadIdx.x % kScanMC, tr = threadIdx.x / kScanMC;
+  const int64_t m = (int64_t)blockIdx.x * kScanMC + mi;
+  const bool mval = m < P.M;
+  Chain<CT> ch{P, (int64_t)blockIdx.y, mval ? m : 0};
+  const int L = (int)P.L;
   CT carry = ch.h0();
-  for (int base = 0; base < (int)P.L; base += T) {
-    CT a_own[2], b_own[2];
+  // a tile's inputs are read while the previous tile is scanned
+  CT na[R], nb[R];
+  auto fetch = [&](int base) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int k = 2 * j + q, pos = base + k;
-      const bool valid = pos < (int)P.L;
-      a_own[q] = valid ? ch.mult(pos) : (CT)1;  // padding with the identity (1, 0)
-      b_own[q] = valid ? ch.b_at(ch.t_of(pos)) : (CT)0;
-      sA[k] = a_own[q];
-      sS[k] = b_own[q];
+    for (int r = 0; r < R; ++r) {
+      const int pos = base + tr + RL * r;
+      const bool valid = mval && pos < L;
+      na[r] = valid ? ch.mult(pos) : (CT)1;  // padding with the identity (1, 0)
+      nb[r] = valid ? ch.b_at(ch.t_of(pos)) : (CT)0;
+    }
+  };
+  fetch(0);
+  for (int base = 0; base < L; base += T) {
+    CT a_own[R], b_own[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = tr + RL * r;
+      a_own[r] = na[r];
+      b_own[r] = nb[r];
+      sA[k][mi] = a_own[r];
+      sS[k][mi] = b_own[r];
     }
     __syncthreads();
-    // up-sweep: right <- right o left
+    if (base + T < L) fetch(base + T);
+    // up-sweep: right <- right o left, over nodes k = (j + 1) s - 1
     for (int s = 2; s <= T; s *= 2) {
-      const int k = (j + 1) * s - 1;
-      if (k < T) {
-        const int l = k - s / 2;
-        sS[k] = fma(sA[k], sS[l], sS[k]);
-        sA[k] = sA[k] * sA[l];
+      for (int j = tr; j < T / s; j += RL) {
+        const int k = (j + 1) * s - 1, l = k - s / 2;
+        sS[k][mi] = fma(sA[k][mi], sS[l][mi], sS[k][mi]);
+        sA[k][mi] = sA[k][mi] * sA[l][mi];
       }
       __syncthreads();
     }
-    if (j == 0) {
-      sA[T - 1] = 1;
-      sS[T - 1] = 0;
+    if (tr == 0) {
+      sA[T - 1][mi] = 1;
+      sS[T - 1][mi] = 0;
     }
     __syncthreads();
     // down-sweep: left <- right; right <- left_old o right
     for (int s = T; s >= 2; s /= 2) {
-      const int k = (j + 1) * s - 1;
-      if (k < T) {
-        const int l = k - s / 2;
-        const CT tA = sA[l], tS = sS[l];
-        sA[l] = sA[k];
-        sS[l] = sS[k];
-        sS[k] = fma(sS[k], tA, tS);
-        sA[k] = sA[k] * tA;
+      for (int j = tr; j < T / s; j += RL) {
+        const int k = (j + 1) * s - 1, l = k - s / 2;
+        const CT tA = sA[l][mi], tS = sS[l][mi];
+        sA[l][mi] = sA[k][mi];
+        sS[l][mi] = sS[k][mi];
+        sS[k][mi] = fma(sS[k][mi], tA, tS);
+        sA[k][mi] = sA[k][mi] * tA;
       }
       __syncthreads();
     }
     // exclusive prefixes: the state entering element k is A_k h_in + S_k
-    CT last = 0;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int k = 2 * j + q, pos = base + k;
-      const CT prev = fma(sA[k], carry, sS[k]);
-      const CT h = fma(a_own[q], prev, b_own[q]);
-      if (pos < (int)P.L) vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), h);
-      if (k == T - 1) last = h;
+    for (int r = 0; r < R; ++r) {
+      const int k = tr + RL * r, pos = base + k;
+      const CT h = fma(a_own[r], fma(sA[k][mi], carry, sS[k][mi]), b_own[r]);
+      if (mval && pos < L) vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), h);
+      if (k == T - 1) sLast[mi] = h;  // the tile's last state, for every lane of the column
     }
     __syncthreads();
-    if (j == blockDim.x - 1) sS[0] = last;  // broadcast the tile's last state
-    __syncthreads();
-    carry = sS[0];
+    carry = sLast[mi];
     __syncthreads();
   }
 }
@@ -169,7 +229,23 @@ __global__ void __launch_bounds__(256) k_lscan_chunk_local(const LscanParams P) 
   Chain<CT> ch{P, b, m};
   CT h = 0, prod = 1;
   const int p0 = (int)cj * P.chunk;
-  for (int pos = p0; pos < p0 + P.chunk && pos < (int)P.L; ++pos) {
+  const int p1 = p0 + P.chunk < (int)P.L ? p0 + P.chunk : (int)P.L;
+  int pos = p0;
+  for (; pos + kSeqAhead <= p1; pos += kSeqAhead) {  // inputs read ahead of the updates
+    CT av[kSeqAhead], bv[kSeqAhead];
+#pragma unroll
+    for (int u = 0; u < kSeqAhead; ++u) {
+      av[u] = ch.mult(pos + u);
+      bv[u] = ch.b_at(ch.t_of(pos + u));
+    }
+#pragma unroll
+    for (int u = 0; u < kSeqAhead; ++u) {
+      h = fma(av[u], h, bv[u]);
+      prod *= av[u];
+      vstore<CT>(P.h, ch.h_off(ch.t_of(pos + u)), h);
+    }
+  }
+  for (; pos < p1; ++pos) {
     const CT a = ch.mult(pos);
     h = fma(a, h, ch.b_at(ch.t_of(pos)));
     prod *= a;
@@ -206,7 +282,22 @@ __global__ void __launch_bounds__(256) k_lscan_chunk_fix(const LscanParams P) {
   const CT hin = ((const CT *)P.ws)[2 * P.B * P.nc * P.M + i];
   CT prod = 1;
   const int p0 = (int)cj * P.chunk;
-  for (int pos = p0; pos < p0 + P.chunk && pos < (int)P.L; ++pos) {
+  const int p1 = p0 + P.chunk < (int)P.L ? p0 + P.chunk : (int)P.L;
+  int pos = p0;
+  for (; pos + kSeqAhead <= p1; pos += kSeqAhead) {  // inputs read ahead of the updates
+    CT av[kSeqAhead], hv[kSeqAhead];
+#pragma unroll
+    for (int u = 0; u < kSeqAhead; ++u) {
+      av[u] = ch.mult(pos + u);
+      hv[u] = vload<CT>(P.h, ch.h_off(ch.t_of(pos + u)));
+    }
+#pragma unroll
+    for (int u = 0; u < kSeqAhead; ++u) {
+      prod *= av[u];
+      vstore<CT>(P.h, ch.h_off(ch.t_of(pos + u)), fma(prod, hin, hv[u]));
+    }
+  }
+  for (; pos < p1; ++pos) {
     prod *= ch.mult(pos);
     const int64_t o = ch.h_off(ch.t_of(pos));
     vstore<CT>(P.h, o, fma(prod, hin, vload<CT>(P.h, o)));
@@ -216,10 +307,7 @@ __global__ void __launch_bounds__(256) k_lscan_chunk_fix(const LscanParams P) {
 // ------------------------------------------------------------------ adjoint epilogue
 // da_t = lambda_t * h_prev(t), dh0 = a_first * lambda_first (first in the forward's order).
 template <typename CT>
-__global__ void __launch_bounds__(256) k_lscan_grad(const LscanGradParams P) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= P.B * P.L * P.M) return;
-  const int64_t m = i % P.M, t = (i / P.M) % P.L, b = i / (P.M * P.L);
+__device__ __forceinline__ void lscan_grad_at(const LscanGradParams &P, int64_t b, int64_t t, int64_t m) {
   const CT lam = vload<CT>(P.db, b * P.db.s0 + t * P.db.s1 + m * P.db.s2);
   const int64_t tp = P.reverse ? t + 1 : t - 1;  // previous step of the forward scan
   CT hp;
@@ -232,6 +320,16 @@ __global__ void __launch_bounds__(256) k_lscan_grad(const LscanGradParams P) {
                vload<CT>(P.a, b * P.a.s0 + t * P.a.s1 + m * P.a.s2) * lam);
 }
 
+// grid: x over m (256 lanes), y over t, z over b; each strides over t and b past 65535
+template <typename CT>
+__global__ void __launch_bounds__(256) k_lscan_grad(const LscanGradParams P) {
+  const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (m >= P.M) return;
+  for (int64_t b = blockIdx.z; b < P.B; b += gridDim.z)
+    for (int64_t t = blockIdx.y; t < P.L; t += gridDim.y) lscan_grad_at<CT>(P, b, t, m);
+}
+
+
 template <typename CT>
 static hipError_t launch_lscan_t(const LscanParams &P, int algo, hipStream_t s) {
   const int64_t chains = P.B * P.M;
@@ -240,10 +338,12 @@ static hipError_t launch_lscan_t(const LscanParams &P, int algo, hipStream_t s) 
       hipLaunchKernelGGL((k_lscan_seq<CT>), dim3((unsigned)((chains + 255) / 256)), dim3(256), 0, s, P);
       break;
     case 2:
-      hipLaunchKernelGGL((k_lscan_hs<CT>), dim3((unsigned)P.M, (unsigned)P.B), dim3(256), 0, s, P);
+      hipLaunchKernelGGL((k_lscan_hs<CT>), dim3((unsigned)((P.M + kScanMC - 1) / kScanMC), (unsigned)P.B), dim3(256),
+                         0, s, P);
       break;
     case 3:
-      hipLaunchKernelGGL((k_lscan_bl<CT>), dim3((unsigned)P.M, (unsigned)P.B), dim3(256), 0, s, P);
+      hipLaunchKernelGGL((k_lscan_bl<CT>), dim3((unsigned)((P.M + kScanMC - 1) / kScanMC), (unsigned)P.B), dim3(256),
+                         0, s, P);
       break;
     default: {
       const int64_t n = P.B * P.nc * P.M;
@@ -260,8 +360,7 @@ hipError_t launch_lscan(const LscanParams &P, int algo, int dtype, hipStream_t s
 }
 
 hipError_t launch_lscan_grad(const LscanGradParams &P, int dtype, hipStream_t s) {
-  const int64_t n = P.B * P.L * P.M;
-  dim3 grid((unsigned)((n + 255) / 256));
+  dim3 grid((unsigned)((P.M + 255) / 256), (unsigned)(P.L < 65535 ? P.L : 65535), (unsigned)(P.B < 65535 ? P.B : 65535));
   if (dtype == 3) hipLaunchKernelGGL((k_lscan_grad<double>), grid, dim3(256), 0, s, P);
   else hipLaunchKernelGGL((k_lscan_grad<float>), grid, dim3(256), 0, s, P);
   return hipGetLastError();

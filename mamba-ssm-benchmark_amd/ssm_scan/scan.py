@@ -26,6 +26,7 @@ import torch
 
 from . import _abi, plan
 from .hip_scan import METHODS, FusedSelectiveScanFn, _check_shapes, _require_gpu
+from .profiling import timed_launch
 
 DISCRETIZATIONS = ("zoh", "euler", "bilinear")      # models/scan.py:36
 SCAN_ELEMENT_BUDGET = plan.SCAN_ELEMENT_BUDGET       # models/scan.py:182
@@ -52,7 +53,8 @@ def _ct(*ts):
 
 def _launch(name, fn, args, dev):
     with torch.cuda.device(dev):
-        rc = fn(ctypes.byref(args), _abi.stream_handle(dev))
+        stream = _abi.stream_handle(dev)
+        rc = timed_launch(name, stream, lambda: fn(ctypes.byref(args), stream))
     _abi.check(rc, name)
 
 

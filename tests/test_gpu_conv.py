@@ -80,6 +80,22 @@ def test_forward_backward_matches_torch(dev, dtype, activation, with_bias):
         np.testing.assert_allclose(np64(bl.grad), rb.grad.numpy(), rtol=rt, atol=at * gs * 10)
 
 
+@pytest.mark.parametrize("W,L,D,B", [(1, 33, 37, 2), (3, 70, 100, 3), (8, 31, 64, 1), (5, 97, 130, 2)])
+def test_backward_widths_and_ragged_shapes(dev, W, L, D, B):
+    """float64 backward across widths, sequence lengths that end inside a 32-step workgroup
+    block and channel counts that end inside a 64-channel one (the per-workgroup weight
+    partial rows and their fixed-order sum)."""
+    x, w, bias = inputs(B, L, D, W, seed=W * 31 + L)
+    leaves = [t.to(dev).requires_grad_() for t in (x, w, bias)]
+    y = causal_conv1d(*leaves)
+    dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(W + L), dtype=torch.float64)
+    y.backward(dy.to(dev))
+    refs = [t.detach().clone().requires_grad_() for t in (x, w, bias)]
+    ref_conv(*refs).backward(dy)
+    for a, r, name in zip(leaves, refs, ("dx", "dw", "dbias")):
+        np.testing.assert_allclose(np64(a.grad), r.grad.numpy(), rtol=1e-12, atol=1e-12, err_msg=name)
+
+
 def test_nn_conv1d_weight_and_contiguous_input(dev):
     x, w, bias = inputs(2, 70, 32, 4, seed=3, split_view=False)
     conv = torch.nn.Conv1d(32, 32, 4, groups=32, bias=True).double()
