@@ -165,6 +165,12 @@ __device__ __forceinline__ void disc_zoh_m1(double dt, const AConst<double> &c, 
   am1 = expm1(dt * c.A);
   coef = am1 * c.invA;
 }
+// a - 1 alone (ZOH)
+__device__ __forceinline__ float zoh_am1(float dt, const AConst<float> &c) {
+  const float z2 = dt * c.A2;
+  return em1_from(z2, fast_exp2(z2));
+}
+__device__ __forceinline__ double zoh_am1(double dt, const AConst<double> &c) { return expm1(dt * c.A); }
 
 // b coefficient multiplying B*x (bilinear stores u in coef).
 template <int METHOD, typename CT>

@@ -171,19 +171,24 @@ k_fwd(const FwdParams p) {
         lds_row(&S.B[n][(q + 1) * RB], nB);
         if (!SUM) lds_row(&S.C[n][(q + 1) * RB], nC);
       }
-      // ZOH keeps a - 1 (accurate expm1) and updates h <- h + (a - 1) h + b, which keeps the
-      // decay's relative accuracy for slowly decaying states (a close to 1).
+      // ZOH keeps a - 1 (accurate expm1) and, with b = (a - 1) Bx / A, updates
+      // h <- h + (a - 1)(h + Bx / A): the decay keeps its relative accuracy for slowly
+      // decaying states (a close to 1), and b needs no separate coefficient.
       CT a[RB], bx[RB];
 #pragma unroll
       for (int tt = 0; tt < RB; ++tt) {
-        CT coef;
-        if constexpr (METHOD == 0) disc_zoh_m1(rdt[tt], ac, a[tt], coef);
-        else disc<METHOD>(rdt[tt], ac, a[tt], coef);
-        bx[tt] = bcoef<METHOD>(rdt[tt], coef) * (rB[tt] * rx[tt]);
+        if constexpr (METHOD == 0) {
+          a[tt] = zoh_am1(rdt[tt], ac);
+          bx[tt] = (rB[tt] * rx[tt]) * ac.invA;
+        } else {
+          CT coef;
+          disc<METHOD>(rdt[tt], ac, a[tt], coef);
+          bx[tt] = bcoef<METHOD>(rdt[tt], coef) * (rB[tt] * rx[tt]);
+        }
       }
 #pragma unroll
       for (int tt = 0; tt < RB; ++tt) {
-        if constexpr (METHOD == 0) h = fma(a[tt], h, h + bx[tt]);
+        if constexpr (METHOD == 0) h = fma(a[tt], h + bx[tt], h);
         else h = fma(a[tt], h, bx[tt]);
         if constexpr (SUM) {  // padded steps (t >= L) have delta 0, i.e. a = 1, b = 0
           if constexpr (METHOD == 0) prod = fma(a[tt], prod, prod);
