@@ -83,7 +83,7 @@ def cpu_baseline_c1(t, budget_s=12.0):
                       f"{reps} reps in {dt:.1f} s"}
 
 
-def cpu_baseline_c2(L, budget_s=20.0):
+def cpu_baseline_fwd(L, budget_s=20.0, label="config-2"):
     """Time the reference CPU path's forward (oracle/cpu_chunked.fwd: SelectiveScanFn over
     channel tiles of d_block = 2^24 // (L N), scan_chunked inside) at B1 D512 N16 on a bounded
     sample: whole channel tiles, as many as fit the budget; the full forward is that time x
@@ -106,7 +106,7 @@ def cpu_baseline_c2(L, budget_s=20.0):
     full_s = dt * len(tiles)
     return {"value": L / full_s / 1e6, "unit": "Mtok/s", "cores": torch.get_num_threads(), "kind": "port",
             "seconds_full_forward": full_s,
-            "sample": f"config-2 forward B1 L{L} D512 N16 fp32 on the torch-CPU restatement of the reference "
+            "sample": f"{label} forward B1 L{L} D512 N16 fp32 on the torch-CPU restatement of the reference "
                       f"CPU path (SelectiveScanFn + scan_chunked, d_block {j - i}): {reps} of its {len(tiles)} "
                       f"independent channel tiles timed ({dt:.2f} s each), scaled to all tiles"}
 
@@ -242,8 +242,8 @@ def bench_fwd(args, dev, B, L, dtype, workload):
            "segments": args.segments or "auto",
            "step_mode": "hip-graph replay" if ms != eager_ms else "eager launches", "eager_ms_per_step": eager_ms,
            "graph_ms_per_step": graph_ms, "graph_matches_eager": graph_ok, "kernel_ms": fwd_ms}
-    if L >= 4096 and not args.no_cpu_baseline:
-        cb = cpu_baseline_c2(L)
+    if not args.no_cpu_baseline and B == 1:
+        cb = cpu_baseline_fwd(L, label="config-0" if L == 512 else "config-2")
         rec["cpu_baseline"] = cb
         rec["gpu_time_frac_of_cpu"] = fwd_ms * 1e-3 / cb["seconds_full_forward"]
     return rec
