@@ -354,6 +354,7 @@ def bench_decode(args, dev):
     module_graph_ms = graph_time(module_step)
     fast_eager_ms = eager_time(fast_step)
     ms = graph_time(fast_step)
+    rec_cpu = None if args.no_cpu_baseline else cpu_baseline_decode(model, B)
     return {"metric": "Mamba LM decode latency per token per layer, batch 64 (10 layers)", "value": ms * 1e3 / 10,
             "unit": "us/layer", "n_gpus": 1, "steps": args.decode_steps, "warmup": 20, "ms_per_step": ms,
             "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
@@ -363,7 +364,30 @@ def bench_decode(args, dev):
                        "batch": B, "layers": 10, "d_model": 256, "d_inner": 512, "dstate": 16, "conv_width": 4},
             "ms_per_token_model": ms, "fused_eager_ms_per_token_model": fast_eager_ms,
             "module_path_ms_per_token_model": {"eager": eager_ms, "graph": module_graph_ms},
-            "tokens_per_s": B / (ms * 1e-3)}
+            "tokens_per_s": B / (ms * 1e-3), **({"cpu_baseline": rec_cpu} if rec_cpu else {})}
+
+
+def cpu_baseline_decode(model, B, budget_s=10.0):
+    """The reference's decode step on the host: the torch-CPU restatement of models/mamba.py's
+    recurrent step inside models/lm.py's LM (oracle/lm_ref, float32 here), one token for the
+    batch through all 10 layers with conv and SSM states, repeated within a time budget."""
+    from oracle import lm_ref
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    p = {k: v.detach().cpu().float() for k, v in model.state_dict().items()}
+    g = torch.Generator().manual_seed(3)
+    states = [{"conv": torch.randn(B, 512, 3, generator=g), "ssm": torch.randn(B, 512, 16, generator=g)}
+              for _ in range(10)]
+    tok = torch.randint(0, 256, (B, 1), generator=g)
+    with torch.no_grad():
+        lm_ref.lm_forward(p, tok, n_layers=10, states=states)
+        reps, t0 = 0, time.perf_counter()
+        while reps < 3 or (time.perf_counter() - t0 < budget_s and reps < 200):
+            lm_ref.lm_forward(p, tok, n_layers=10, states=states)
+            reps += 1
+    per_tok = (time.perf_counter() - t0) / reps
+    return {"value": per_tok * 1e6 / 10, "unit": "us/layer", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"batch {B}, one token through the 10-layer LM on the torch-CPU restatement of the "
+                      f"reference decode path (oracle/lm_ref, float32), {reps} tokens timed"}
 
 
 def bench_scans(args, dev):
