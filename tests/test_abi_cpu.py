@@ -205,3 +205,17 @@ def test_lowrank_delta_needs_small_dstate():
     a._keep2 = (W, low)
     with pytest.raises(ValueError):
         _abi.check(_abi.lib().ssm_fwd_check(ctypes.byref(a)), "ssm_fwd")
+
+
+@pytest.mark.parametrize("field,value", [("dstate", 65), ("width", 9), ("method", 3), ("batch", 0), ("dt_rank", 300)])
+def test_decode_layer_validation(field, value):
+    """ssm_decode_check rejects out-of-range layer shapes before any launch."""
+    a = _abi.DecodeArgs()
+    a.batch, a.dim, a.dstate, a.width, a.dt_rank, a.d_model, a.method = 2, 64, 16, 4, 4, 32, 0
+    for name in ("u", "xz", "conv_w", "conv_b", "conv_state", "x_proj_wt", "dt_proj_w", "dt_bias", "A_log",
+                 "Dskip", "ssm_state", "y"):
+        setattr(a, name, 16)   # non-null placeholders: the check never dereferences them
+    assert _abi.lib().ssm_decode_check(ctypes.byref(a)) == 0
+    setattr(a, field, value)
+    with pytest.raises(ValueError):
+        _abi.check(_abi.lib().ssm_decode_check(ctypes.byref(a)), "ssm_decode_step")

@@ -132,16 +132,26 @@ def test_lowrank_rank_above_capacity_uses_a_gemm(dev):
 
 
 def test_lowrank_mixed_layouts(dev):
-    """x channel-major with a time-major gate: not a uniform layout, so the kernels take the
-    strided-address path; the projection is staged the same way."""
+    """x a split view (row stride 2D, as in_proj's output) while the outputs it allocates are
+    contiguous: not a uniform layout, so forward and backward take the strided-address path;
+    the projection is staged the same way."""
     B, L, D, N, Rk = 2, 50, 48, 16, 16
-    x, proj, W, A, Dv, z, bias, dout = make(B, L, D, N, Rk, seed=13, channel_major=True)
-    ins = (x, proj, W, A, Dv, z.contiguous(), bias, dout)
-    out, last, grads = run(dev, *ins, Rk, N, "zoh")
-    rout, rlast, rg = oracle(*ins, Rk, N, "zoh")
+    x, proj, W, A, Dv, z, bias, dout = make(B, L, D, N, Rk, seed=13)
+    xz = torch.cat([x, z], -1).to(dev).requires_grad_()          # split on the device: views
+    leaves = [t.to(dev).requires_grad_() for t in (proj, W, A, Dv, bias)]
+    pg, Wg, Ag, Dg, bg = leaves
+    xg, zg = xz[..., :D], xz[..., D:]
+    assert xg.stride() == (L * 2 * D, 2 * D, 1)
+    dt, Bm, Cm = pg[..., :Rk], pg[..., Rk:Rk + N], pg[..., Rk + N:]
+    out = ssm_scan.selective_scan_fn(xg, dt, Ag, Bm, Cm, D=Dg, z=zg, delta_bias=bg, delta_softplus=True,
+                                     delta_proj=Wg)
+    (out * dout.to(dev)).sum().backward()
+    rout, _, rg = oracle(x, proj, W, A, Dv, z, bias, dout, Rk, N, "zoh")
     close(out, rout, name="out")
-    for k, v in grads.items():
-        close(v, rg[k], name=k)
+    close(xz.grad[..., :D], rg["dx"], name="dx")
+    close(xz.grad[..., D:], rg["dz"], name="dz")
+    for name, t in zip(("dproj", "dW", "dA", "dD", "dbias"), leaves):
+        close(t.grad, rg[name], name=name)
 
 
 def test_lowrank_bf16_inputs(dev):
@@ -154,3 +164,27 @@ def test_lowrank_bf16_inputs(dev):
     close(out, rout, 2e-2, 2e-2, "out")
     close(last, rlast, 2e-2, 2e-2, "last")
     close(grads["dW"], rg["dW"], 2e-2, 2e-2, "dW")
+
+
+def test_lowrank_with_initial_state_and_last_gradient(dev):
+    """h0 and a gradient on the final state through the projected-delta path equal the same
+    computation with the projection done by a torch GEMM first."""
+    B, L, D, N, Rk = 2, 45, 24, 16, 8
+    x, proj, W, A, Dv, z, bias, dout = make(B, L, D, N, Rk, seed=31)
+    g = torch.Generator().manual_seed(32)
+    h0 = torch.randn(B, D, N, generator=g)
+    dlast = torch.randn(B, D, N, generator=g)
+    res = []
+    for lowrank in (True, False):
+        leaves = [t.to(dev).requires_grad_() for t in (x, proj, W, A, Dv, z, bias, h0)]
+        xg, pg, Wg, Ag, Dg, zg, bg, hg = leaves
+        dt, Bm, Cm = pg[..., :Rk], pg[..., Rk:Rk + N], pg[..., Rk + N:]
+        kw = dict(D=Dg, z=zg, delta_bias=bg, delta_softplus=True, h0=hg, return_last_state=True)
+        if lowrank:
+            out, last = ssm_scan.selective_scan_fn(xg, dt, Ag, Bm, Cm, delta_proj=Wg, **kw)
+        else:
+            out, last = ssm_scan.selective_scan_fn(xg, torch.nn.functional.linear(dt, Wg), Ag, Bm, Cm, **kw)
+        ((out * dout.to(dev)).sum() + (last * dlast.to(dev)).sum()).backward()
+        res.append([out.detach(), last.detach()] + [t.grad for t in leaves])
+    for i, (a, b_) in enumerate(zip(*res)):
+        close(a, np64(b_), name=str(i))
