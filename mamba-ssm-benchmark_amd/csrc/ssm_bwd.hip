@@ -412,45 +412,94 @@ k_bwd(const BwdParams p) {
 }
 
 // Fixed-order final reductions: dB/dC over channel tiles, dA/dD/d_bias over the batch.
-template <typename OT, typename CT>
+// Each sum runs over its terms in index order; the reads of a group of kFinGroup terms are
+// issued together ahead of their adds (the sums are latency-bound chains of dependent
+// round trips otherwise).  With V4 a lane sums four consecutive states of dB or of dC with
+// 16-byte reads (float partials, 16-byte aligned, np a multiple of 4).
+constexpr int kFinGroup = 4;
+
+template <typename CT>
+__device__ inline CT fin_sum(const CT *src, int64_t stride, int64_t count) {
+  CT s = 0;
+  int64_t k = 0;
+  for (; k + kFinGroup <= count; k += kFinGroup) {
+    CT v[kFinGroup];
+#pragma unroll
+    for (int u = 0; u < kFinGroup; ++u) v[u] = src[(k + u) * stride];
+#pragma unroll
+    for (int u = 0; u < kFinGroup; ++u) s += v[u];
+  }
+  for (; k < count; ++k) s += src[k * stride];
+  return s;
+}
+
+__device__ inline float4 fin_sum4(const float4 *src, int64_t stride, int count) {
+  float4 s = {0.f, 0.f, 0.f, 0.f};
+  int k = 0;
+  for (; k + kFinGroup <= count; k += kFinGroup) {
+    float4 v[kFinGroup];
+#pragma unroll
+    for (int u = 0; u < kFinGroup; ++u) v[u] = src[(k + u) * stride];
+#pragma unroll
+    for (int u = 0; u < kFinGroup; ++u) {
+      s.x += v[u].x; s.y += v[u].y; s.z += v[u].z; s.w += v[u].w;
+    }
+  }
+  for (; k < count; ++k) {
+    const float4 v = src[k * stride];
+    s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+  }
+  return s;
+}
+
+// Lanes handling dB / dC with V4 (two quantities, np / 4 lanes per (b, t)) or without.
+__host__ __device__ inline int64_t fin_bc_lanes(const FinParams &p, bool v4) {
+  return v4 ? 2 * p.B * p.L * (p.np / 4) : p.B * p.L * p.N;
+}
+
+template <typename OT, typename CT, bool V4>
 __global__ void __launch_bounds__(256) k_bwd_finalize(const FinParams p) {
-  const int64_t nBLN = p.B * p.L * p.N;
+  const int64_t nBC = fin_bc_lanes(p, V4);
   const int64_t nDN = p.D * p.N;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < nBLN) {
-    const int64_t nn = i % p.N, t = (i / p.N) % p.L, b = i / (p.N * p.L);
-    const CT *wB = (const CT *)p.ws_dB, *wC = (const CT *)p.ws_dC;
-    CT sb = 0, sc = 0;
-    for (int tile = 0; tile < p.ntiles; ++tile) {
-      const int64_t off = ((b * p.ntiles + tile) * p.L + t) * p.np + nn;
-      sb += wB[off];
-      sc += wC[off];
+  if (i < nBC) {
+    const int64_t tstride = p.L * p.np;  // between the partials of consecutive tiles
+    if constexpr (V4) {
+      const int q4 = p.np / 4;
+      const int64_t half = nBC / 2;
+      const bool isC = i >= half;
+      const int64_t r = isC ? i - half : i;
+      const int64_t n4 = r % q4, t = (r / q4) % p.L, b = r / (q4 * p.L);
+      const float4 *src = (const float4 *)(isC ? p.ws_dC : p.ws_dB) + (b * p.ntiles * p.L + t) * q4 + n4;
+      const float4 s = fin_sum4(src, tstride / 4, p.ntiles);
+      const KView &o = isC ? p.dC : p.dB;
+      const float sv[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int64_t nn = n4 * 4 + k;
+        if (nn < p.N) Conv<OT>::store(vpw<OT>(o) + b * o.s0 + t * o.s1 + nn * o.s2, sv[k]);
+      }
+    } else {
+      const int64_t nn = i % p.N, t = (i / p.N) % p.L, b = i / (p.N * p.L);
+      const int64_t off0 = (b * p.ntiles * p.L + t) * p.np + nn;
+      const CT sb = fin_sum((const CT *)p.ws_dB + off0, tstride, p.ntiles);
+      const CT sc = fin_sum((const CT *)p.ws_dC + off0, tstride, p.ntiles);
+      Conv<OT>::store(vpw<OT>(p.dB) + b * p.dB.s0 + t * p.dB.s1 + nn * p.dB.s2, sb);
+      Conv<OT>::store(vpw<OT>(p.dC) + b * p.dC.s0 + t * p.dC.s1 + nn * p.dC.s2, sc);
     }
-    Conv<OT>::store(vpw<OT>(p.dB) + b * p.dB.s0 + t * p.dB.s1 + nn * p.dB.s2, sb);
-    Conv<OT>::store(vpw<OT>(p.dC) + b * p.dC.s0 + t * p.dC.s1 + nn * p.dC.s2, sc);
     return;
   }
-  const int64_t j = i - nBLN;
+  const int64_t j = i - nBC;
   if (j < nDN) {
     const int64_t d = j / p.N, nn = j % p.N;
-    const CT *wA = (const CT *)p.ws_dA;
-    CT s = 0;
-    for (int64_t b = 0; b < p.B; ++b) s += wA[(b * p.D + d) * p.np + nn];
+    const CT s = fin_sum((const CT *)p.ws_dA + d * p.np + nn, p.D * p.np, p.B);
     vstore<CT>(p.dA, d * p.dA.s0 + nn * p.dA.s1, s);
     return;
   }
   const int64_t k = j - nDN;
   if (k < p.D) {
-    if (p.has_D) {
-      CT s = 0;
-      for (int64_t b = 0; b < p.B; ++b) s += ((const CT *)p.ws_dD)[b * p.D + k];
-      vstore<CT>(p.dD, k * p.dD.s0, s);
-    }
-    if (p.has_bias) {
-      CT s = 0;
-      for (int64_t b = 0; b < p.B; ++b) s += ((const CT *)p.ws_db)[b * p.D + k];
-      vstore<CT>(p.dbias, k * p.dbias.s0, s);
-    }
+    if (p.has_D) vstore<CT>(p.dD, k * p.dD.s0, fin_sum((const CT *)p.ws_dD + k, p.D, p.B));
+    if (p.has_bias) vstore<CT>(p.dbias, k * p.dbias.s0, fin_sum((const CT *)p.ws_db + k, p.D, p.B));
   }
 }
 
@@ -503,14 +552,18 @@ hipError_t launch_bwd(const BwdParams &p, int dtype, int method, int np, hipStre
 }
 
 hipError_t launch_bwd_finalize(const FinParams &p, int dtype, hipStream_t s) {
-  const int64_t total = p.B * p.L * p.N + p.D * p.N + p.D;
+  // float partials read as float4 when both partial arrays are 16-byte aligned
+  const bool v4 = dtype != 3 && p.np % 4 == 0 && ((uintptr_t)p.ws_dB | (uintptr_t)p.ws_dC) % 16 == 0;
+  const int64_t total = fin_bc_lanes(p, v4) + p.D * p.N + p.D;
   dim3 grid((unsigned)((total + 255) / 256));
+#define SSM_FIN(OT, CT, V) hipLaunchKernelGGL((k_bwd_finalize<OT, CT, V>), grid, dim3(256), 0, s, p)
   switch (dtype) {
-    case 0: hipLaunchKernelGGL((k_bwd_finalize<float, float>), grid, dim3(256), 0, s, p); break;
-    case 1: hipLaunchKernelGGL((k_bwd_finalize<bf16_t, float>), grid, dim3(256), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((k_bwd_finalize<f16_t, float>), grid, dim3(256), 0, s, p); break;
-    default: hipLaunchKernelGGL((k_bwd_finalize<double, double>), grid, dim3(256), 0, s, p); break;
+    case 0: if (v4) SSM_FIN(float, float, true); else SSM_FIN(float, float, false); break;
+    case 1: if (v4) SSM_FIN(bf16_t, float, true); else SSM_FIN(bf16_t, float, false); break;
+    case 2: if (v4) SSM_FIN(f16_t, float, true); else SSM_FIN(f16_t, float, false); break;
+    default: SSM_FIN(double, double, false); break;
   }
+#undef SSM_FIN
   return hipGetLastError();
 }
 
