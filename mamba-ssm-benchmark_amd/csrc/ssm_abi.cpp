@@ -432,6 +432,9 @@ static int lscan_common(int64_t B, int64_t L, int64_t M, int algo, int dtype, in
   if (L >= (1LL << 30) || M >= (1LL << 31) || B * L * M >= (1LL << 39))
     return fail(SSM_EINVAL, "scan too large");
   if (chunk < 0 || chunk >= (1LL << 30)) return fail(SSM_EINVAL, "chunk=%lld out of range", (long long)chunk);
+  // one lane per recurrence (per chunk of one for the chunked algorithm): a 1-D grid below 2^31 lanes
+  const int64_t lanes = B * M * (algo == SSM_SCAN_CHUNKED ? cdiv(L, chunk ? chunk : ssm_default_chunk(L)) : 1);
+  if (lanes >= (1LL << 31)) return fail(SSM_EINVAL, "scan too large: %lld recurrences", (long long)lanes);
   return SSM_OK;
 }
 

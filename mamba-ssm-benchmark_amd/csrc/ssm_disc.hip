@@ -17,25 +17,40 @@
 
 namespace ssm {
 
+// Time rows per lane and pass: their reads are all issued before the first store (a wave's
+// read waits would otherwise also wait for its earlier stores).
+constexpr int kDiscRows = 8;
+
 template <typename CT, int METHOD>
 __global__ void __launch_bounds__(kThreads) k_disc_fwd(const DiscParams p) {
-  // grid: x over the D*N elements of a (b, t) row (32-bit index, contiguous outputs), y over t
-  // (about 8 rows per lane), z over b (striding); the per-(d, n) constants are formed once
+  // grid: x over the D*N elements of a (b, t) row (32-bit index, contiguous outputs), y over
+  // groups of kDiscRows time rows (striding), z over b (striding); the per-(d, n) constants
+  // are formed once
   const int e = blockIdx.x * kThreads + threadIdx.x;
   const int DN = (int)(p.D * p.N);
   if (e >= DN) return;
   const int n = e % (int)p.N, d = e / (int)p.N;
+  const int L = (int)p.L;
   const AConst<CT> ac = make_aconst(vload<CT>(p.A, d * p.A.s0 + n * p.A.s1));
   for (int64_t b = blockIdx.z; b < p.B; b += gridDim.z) {
-    for (int64_t t = blockIdx.y; t < p.L; t += gridDim.y) {
-      const CT dt = vload<CT>(p.delta, b * p.delta.s0 + t * p.delta.s1 + d * p.delta.s2);
-      const CT xv = vload<CT>(p.x, b * p.x.s0 + t * p.x.s1 + d * p.x.s2);
-      const CT Bv = vload<CT>(p.Bm, b * p.Bm.s0 + t * p.Bm.s1 + n * p.Bm.s2);
-      CT a, coef;
-      disc<METHOD>(dt, ac, a, coef);
-      const int64_t i = (b * p.L + t) * DN + e;
-      ((CT *)p.a)[i] = a;
-      ((CT *)p.b)[i] = bcoef<METHOD>(dt, coef) * (Bv * xv);
+    for (int t0 = blockIdx.y * kDiscRows; t0 < L; t0 += gridDim.y * kDiscRows) {
+      CT dt[kDiscRows], xv[kDiscRows], Bv[kDiscRows];
+#pragma unroll
+      for (int k = 0; k < kDiscRows; ++k) {  // clamped rows past the end are read, not stored
+        const int64_t t = min(t0 + k, L - 1);
+        dt[k] = vload<CT>(p.delta, b * p.delta.s0 + t * p.delta.s1 + d * p.delta.s2);
+        xv[k] = vload<CT>(p.x, b * p.x.s0 + t * p.x.s1 + d * p.x.s2);
+        Bv[k] = vload<CT>(p.Bm, b * p.Bm.s0 + t * p.Bm.s1 + n * p.Bm.s2);
+      }
+#pragma unroll
+      for (int k = 0; k < kDiscRows; ++k) {
+        if (t0 + k >= L) break;
+        CT a, coef;
+        disc<METHOD>(dt[k], ac, a, coef);
+        const int64_t i = (b * p.L + t0 + k) * DN + e;
+        ((CT *)p.a)[i] = a;
+        ((CT *)p.b)[i] = bcoef<METHOD>(dt[k], coef) * (Bv[k] * xv[k]);
+      }
     }
   }
 }
@@ -114,7 +129,7 @@ __global__ void __launch_bounds__(kThreads) k_disc_fin(const DiscParams p) {
 
 template <typename CT, int M>
 static hipError_t disc_fwd_t(const DiscParams &p, hipStream_t s) {
-  const int64_t ty = (p.L + 7) / 8;  // about 8 time rows per lane
+  const int64_t ty = (p.L + kDiscRows - 1) / kDiscRows;
   const dim3 grid((unsigned)((p.D * p.N + kThreads - 1) / kThreads), (unsigned)(ty < 65535 ? ty : 65535),
                   (unsigned)(p.B < 65535 ? p.B : 65535));
   hipLaunchKernelGGL((k_disc_fwd<CT, M>), grid, dim3(kThreads), 0, s, p);

@@ -51,32 +51,55 @@ struct Chain {
 };
 
 // ------------------------------------------------------------------ sequential
-constexpr int kSeqAhead = 16;  // steps whose inputs are read before their dependent updates
+// Steps per register set: a lane keeps two sets; while one set's updates run, the reads of the
+// other are in flight (512 wavefronts at the bench shape: bytes in flight per wavefront set
+// the bandwidth).
+template <typename CT> constexpr int seq_ahead() { return sizeof(CT) == 4 ? 32 : 16; }
+
+// One wavefront per workgroup: at (B, M) = (2, 16384) the 512 wavefronts spread over all 256
+// CUs (256-lane workgroups would occupy only 128 of them).
+constexpr int kSeqThreads = 64;
 
 template <typename CT>
-__global__ void __launch_bounds__(256) k_lscan_seq(const LscanParams P) {
+__global__ void __launch_bounds__(kSeqThreads) k_lscan_seq(const LscanParams P) {
+  constexpr int K = seq_ahead<CT>();
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= P.B * P.M) return;
   Chain<CT> ch{P, i / P.M, i % P.M};
   const int L = (int)P.L;
   CT h = ch.h0();
+  CT a0[K], b0[K], a1[K], b1[K];
+  // reads at clamped positions (past the end: re-reads of the last step, never used), so no
+  // read waits behind a branch
+  auto fetch = [&](CT (&av)[K], CT (&bv)[K], int pos0) {
+#pragma unroll
+    for (int u = 0; u < K; ++u) {
+      const int pos = min(pos0 + u, L - 1);
+      av[u] = ch.mult(pos);
+      bv[u] = ch.b_at(ch.t_of(pos));
+    }
+  };
+  auto run = [&](const CT (&av)[K], const CT (&bv)[K], int pos0, int n) {
+#pragma unroll
+    for (int u = 0; u < K; ++u) {
+      if (u < n) {
+        h = fma(av[u], h, bv[u]);
+        vstore<CT>(P.h, ch.h_off(ch.t_of(pos0 + u)), h);
+      }
+    }
+  };
+  fetch(a0, b0, 0);
   int pos = 0;
-  for (; pos + kSeqAhead <= L; pos += kSeqAhead) {
-    CT av[kSeqAhead], bv[kSeqAhead];
-#pragma unroll
-    for (int u = 0; u < kSeqAhead; ++u) {
-      av[u] = ch.mult(pos + u);
-      bv[u] = ch.b_at(ch.t_of(pos + u));
-    }
-#pragma unroll
-    for (int u = 0; u < kSeqAhead; ++u) {
-      h = fma(av[u], h, bv[u]);
-      vstore<CT>(P.h, ch.h_off(ch.t_of(pos + u)), h);
-    }
+  for (; pos + 2 * K <= L; pos += 2 * K) {
+    fetch(a1, b1, pos + K);
+    run(a0, b0, pos, K);
+    fetch(a0, b0, pos + 2 * K);
+    run(a1, b1, pos + K, K);
   }
-  for (; pos < L; ++pos) {
-    h = fma(ch.mult(pos), h, ch.b_at(ch.t_of(pos)));
-    vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), h);
+  if (pos < L) {  // fewer than 2K steps left; a0 holds the next K
+    fetch(a1, b1, pos + K);
+    run(a0, b0, pos, L - pos);
+    run(a1, b1, pos + K, L - pos - K);
   }
 }
 
@@ -221,6 +244,8 @@ __global__ void __launch_bounds__(256) k_lscan_bl(const LscanParams P) {
 }
 
 // ------------------------------------------------------------------ chunked (three phases)
+constexpr int kSeqAhead = 16;  // steps whose inputs are read before their dependent updates
+
 template <typename CT>
 __global__ void __launch_bounds__(256) k_lscan_chunk_local(const LscanParams P) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -335,7 +360,8 @@ static hipError_t launch_lscan_t(const LscanParams &P, int algo, hipStream_t s) 
   const int64_t chains = P.B * P.M;
   switch (algo) {
     case 1:
-      hipLaunchKernelGGL((k_lscan_seq<CT>), dim3((unsigned)((chains + 255) / 256)), dim3(256), 0, s, P);
+      hipLaunchKernelGGL((k_lscan_seq<CT>), dim3((unsigned)((chains + kSeqThreads - 1) / kSeqThreads)),
+                         dim3(kSeqThreads), 0, s, P);
       break;
     case 2:
       hipLaunchKernelGGL((k_lscan_hs<CT>), dim3((unsigned)((P.M + kScanMC - 1) / kScanMC), (unsigned)P.B), dim3(256),

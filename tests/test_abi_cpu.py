@@ -219,3 +219,23 @@ def test_decode_layer_validation(field, value):
     setattr(a, field, value)
     with pytest.raises(ValueError):
         _abi.check(_abi.lib().ssm_decode_check(ctypes.byref(a)), "ssm_decode_step")
+
+
+def test_linear_scan_grid_limit():
+    """One lane per recurrence (per chunk for the chunked algorithm) in a 1-D grid: 2^31 lanes
+    or more is rejected before any launch."""
+    t = torch.zeros(2, 8, 4)
+    a = _abi.LscanArgs()
+    a.batch, a.seqlen, a.width, a.algo, a.dtype = 2, 8, 4, 1, 0
+    for name in ("a", "b", "h"):
+        setattr(a, name, _abi.view(t))
+    lib = _abi.lib()
+    assert lib.ssm_lscan_check(ctypes.byref(a)) == 0
+    a.batch, a.width = 4, 1 << 29
+    with pytest.raises(ValueError, match="too large"):
+        _abi.check(lib.ssm_lscan_check(ctypes.byref(a)), "ssm_lscan")
+    a.batch, a.width, a.seqlen, a.chunk = 1, 1 << 20, 1 << 12, 1
+    assert lib.ssm_lscan_check(ctypes.byref(a)) == 0      # sequential: 2^20 lanes
+    a.algo = 4                                            # chunked, chunk 1: 2^32 lanes
+    with pytest.raises(ValueError, match="too large"):
+        _abi.check(lib.ssm_lscan_check(ctypes.byref(a)), "ssm_lscan")
