@@ -394,8 +394,9 @@ def bench_scans(args, dev):
     """The composed path's kernels (models/scan.py's algorithms on the engine): each linear-scan
     algorithm on (B, L, M) = (2, 4096, 16384) float32 (a, b read, h written: 3 x 4 x B L M
     algorithmic bytes), and the materialized ZOH discretization on (B, L, D, N) =
-    (2, 4096, 1024, 16) (a, b written; delta, x, B read).  Device time per launch from HIP
-    events on the launch stream, against 8 TB/s."""
+    (2, 4096, 1024, 16) (a, b written; delta, x, B read) and its backward (da, db read;
+    ddelta, dx, dBm, dA written).  Device time per launch from HIP events on the launch
+    stream, against 8 TB/s."""
     import ssm_scan
     from ssm_scan import scan as S
     B, L, M = 2, 4096, 16384
@@ -431,6 +432,21 @@ def bench_scans(args, dev):
     nbytes = 2 * 4 * B * L * D * N + 4 * (2 * B * L * D + B * L * N + D * N)
     lines["discretize_zoh"] = {"ms": t, "GB/s": nbytes / (t * 1e-3) / 1e9,
                                "frac": nbytes / (t * 1e-3) / (HBM_PEAK_GBS * 1e9), "alg_bytes": nbytes}
+    # its backward: da, db read; ddelta, dx, dBm, dA written (delta, x, Bm, A re-read)
+    leaves = [v.clone().requires_grad_() for v in (delta, A, Bm, x)]
+    with torch.enable_grad():
+        a_, b_ = S.discretize(*leaves)
+    ga, gb = torch.randn_like(a_), torch.randn_like(b_)
+    for _ in range(2):
+        torch.autograd.grad((a_, b_), leaves, (ga, gb), retain_graph=True)
+    with ssm_scan.KernelTimer() as tm:
+        for _ in range(args.steps):
+            torch.autograd.grad((a_, b_), leaves, (ga, gb), retain_graph=True)
+    t = statistics.median(tm.times_ms()["ssm_disc_bwd"])
+    nbytes = 2 * 4 * B * L * D * N + 4 * (4 * B * L * D + 2 * B * L * N + 2 * D * N)
+    lines["discretize_zoh_bwd"] = {"ms": t, "GB/s": nbytes / (t * 1e-3) / 1e9,
+                                   "frac": nbytes / (t * 1e-3) / (HBM_PEAK_GBS * 1e9), "alg_bytes": nbytes}
+    del a_, b_, ga, gb, leaves
     best = max(lines, key=lambda k: lines[k]["frac"])
     return {"metric": "composed-path kernels, HBM GB/s (linear scans B2 L4096 M16384, discretize B2 L4096 D1024 N16)",
             "value": lines[best]["GB/s"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 2,

@@ -68,6 +68,31 @@ constexpr float TAU_F = 0.3f;      // switch between Taylor f(z) and the closed 
 __device__ __forceinline__ float fast_exp2(float v) { return __builtin_amdgcn_exp2f(v); }
 __device__ __forceinline__ float fast_rcp(float v) { return __builtin_amdgcn_rcpf(v); }
 
+// Sum over aligned groups of NP lanes (NP a power of two, 8..64), every lane of a group
+// receiving the same bits.  Float: DPP row permutations inside each 16-lane row (lane i ^ 1,
+// i ^ 2, the mirrored quad of its half row, the mirrored half row), then cross-row shuffles.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int NP>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(NP >= 8 && NP <= 64 && (NP & (NP - 1)) == 0, "group size");
+  v += dpp_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  if constexpr (NP >= 16) v += dpp_f<0x140>(v);  // row_mirror
+  if constexpr (NP >= 32) v += __shfl_xor(v, 16);
+  if constexpr (NP >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+template <int NP>
+__device__ __forceinline__ double group_sum(double v) {
+#pragma unroll
+  for (int off = NP / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
 // expm1 for z <= ~0 given z2 = z*log2(e) and a = 2^z2; Taylor in z2 with coefficients ln2^k/k!.
 __device__ __forceinline__ float em1_from(float z2, float a) {
   const float c1 = 0.6931471805599453f, c2 = 0.2402265069591007f, c3 = 0.05550410866482158f,

@@ -4,8 +4,9 @@
 // (ddelta, dA, dBm, dx) through autograd (:249).
 //
 // Forward: one lane per output element; the (B, L, D, N) outputs are written contiguously.
-// Backward: a workgroup owns 256/NP channels x NP states and walks a group of (b, l) rows.
-//   ddelta, dx  (B, L, D)  sums over n: cross-lane butterfly inside each NP-lane group;
+// Backward: a workgroup owns 256/NP channels x NP states and walks a group of (b, l) rows,
+// issuing the next row's reads before the current row's arithmetic and stores.
+//   ddelta, dx  (B, L, D)  sums over n: DPP row permutations inside each NP-lane group;
 //   dBm (B, L, N)          sum over d: per-row LDS reduction over the tile's channels into a
 //                          (row, tile, n) partial, then a fixed-order sum over tiles;
 //   dA (D, N)              sum over (b, l): register accumulation over the group's rows into a
@@ -58,52 +59,67 @@ __global__ void __launch_bounds__(kThreads) k_disc_fwd(const DiscParams p) {
 template <typename CT, int NP, int METHOD>
 __global__ void __launch_bounds__(kThreads) k_disc_bwd(const DiscParams p) {
   constexpr int DT = kThreads / NP;
-  __shared__ CT red[DT][NP];
+  __shared__ CT red[2][DT][NP];  // double-buffered by row parity: one barrier per row
   const int tid = threadIdx.x, c = tid / NP, n = tid % NP;
   const int64_t tile = blockIdx.x, g = blockIdx.y;
   const int64_t d = tile * DT + c;
   const bool valid = d < p.D && n < p.N;
+  const int64_t dc = valid ? d : 0, nc = valid ? n : 0;  // clamped: every read stays in bounds
   const int64_t R = p.B * p.L;
   const int64_t r0 = g * p.rows_per_group, r1 = r0 + p.rows_per_group < R ? r0 + p.rows_per_group : R;
   AConst<CT> ac = make_aconst<CT>(-1);
   if (valid) ac = make_aconst(vload<CT>(p.A, d * p.A.s0 + n * p.A.s1));
+  // lane parts of the addresses (row parts are uniform)
+  const CT *pdel = (const CT *)p.delta.p + dc * p.delta.s2, *px = (const CT *)p.x.p + dc * p.x.s2;
+  const CT *pB = (const CT *)p.Bm.p + nc * p.Bm.s2;
+  const CT *pda = (const CT *)p.da + dc * p.N + nc, *pdb = (const CT *)p.db + dc * p.N + nc;
+  const int64_t DN = p.D * p.N;
   CT gA = 0;
-  int64_t b = r0 / p.L, t = r0 - (r0 / p.L) * p.L;  // (b, t) of row r, advanced incrementally
-  for (int64_t r = r0; r < r1; ++r, t = t + 1 < p.L ? t + 1 : 0, b += t == 0 ? 1 : 0) {
+  // the next row's reads are issued before this row's stores
+  int64_t b = r0 / p.L, t = r0 - (r0 / p.L) * p.L;
+  struct Row { CT dt, x, B, ga, gb; };
+  auto fetch = [&](int64_t bb, int64_t tt, int64_t r) {
+    Row v;
+    v.dt = pdel[bb * p.delta.s0 + tt * p.delta.s1];
+    v.x = px[bb * p.x.s0 + tt * p.x.s1];
+    v.B = pB[bb * p.Bm.s0 + tt * p.Bm.s1];
+    v.ga = pda[r * DN];
+    v.gb = pdb[r * DN];
+    return v;
+  };
+  Row cur = fetch(b, t, r0);
+  int buf = 0;
+  for (int64_t r = r0; r < r1; ++r, buf ^= 1) {
+    const int64_t bc = b, tc = t;
+    if (++t == p.L) { t = 0; ++b; }
+    const bool more = r + 1 < r1;
+    const Row nxt = fetch(more ? b : bc, more ? t : tc, more ? r + 1 : r);
     CT gd = 0, gx = 0, gB = 0;
     if (valid) {
-      const CT dt = vload<CT>(p.delta, b * p.delta.s0 + t * p.delta.s1 + d * p.delta.s2);
-      const CT xv = vload<CT>(p.x, b * p.x.s0 + t * p.x.s1 + d * p.x.s2);
-      const CT Bv = vload<CT>(p.Bm, b * p.Bm.s0 + t * p.Bm.s1 + n * p.Bm.s2);
-      const int64_t e = (r * p.D + d) * p.N + n;
-      const CT ga = ((const CT *)p.da)[e], gb = ((const CT *)p.db)[e];
       CT a, coef, dadz, dbdd, d2f;
-      disc<METHOD>(dt, ac, a, coef);
-      dfactors<METHOD>(dt, ac, a, coef, dadz, dbdd, d2f);
-      const CT bx = Bv * xv, gz = ga * dadz, gbc = gb * bcoef<METHOD>(dt, coef);
-      gd = fma(ac.A, gz, gb * dbdd * bx);
-      gA += fma(dt, gz, gb * d2f * bx);
-      gx = gbc * Bv;
-      gB = gbc * xv;
+      disc<METHOD>(cur.dt, ac, a, coef);
+      dfactors<METHOD>(cur.dt, ac, a, coef, dadz, dbdd, d2f);
+      const CT bx = cur.B * cur.x, gz = cur.ga * dadz, gbc = cur.gb * bcoef<METHOD>(cur.dt, coef);
+      gd = fma(ac.A, gz, cur.gb * dbdd * bx);
+      gA += fma(cur.dt, gz, cur.gb * d2f * bx);
+      gx = gbc * cur.B;
+      gB = gbc * cur.x;
     }
-#pragma unroll
-    for (int off = NP / 2; off > 0; off >>= 1) {
-      gd += __shfl_xor(gd, off);
-      gx += __shfl_xor(gx, off);
-    }
+    gd = group_sum<NP>(gd);
+    gx = group_sum<NP>(gx);
     if (n == 0 && d < p.D) {
-      vstore<CT>(p.ddelta, b * p.ddelta.s0 + t * p.ddelta.s1 + d * p.ddelta.s2, gd);
-      vstore<CT>(p.dx, b * p.dx.s0 + t * p.dx.s1 + d * p.dx.s2, gx);
+      vstore<CT>(p.ddelta, bc * p.ddelta.s0 + tc * p.ddelta.s1 + d * p.ddelta.s2, gd);
+      vstore<CT>(p.dx, bc * p.dx.s0 + tc * p.dx.s1 + d * p.dx.s2, gx);
     }
-    red[c][n] = gB;
+    red[buf][c][n] = gB;
     __syncthreads();
-    if (tid < NP) {
+    if (tid < NP) {  // dBm partial of (row, state): sum over the tile's DT channels in channel order
       CT s = 0;
 #pragma unroll
-      for (int k = 0; k < DT; ++k) s += red[k][tid];
+      for (int k = 0; k < DT; ++k) s += red[buf][k][tid];
       if (tid < p.N) ((CT *)p.ws_dB)[(r * p.dtiles + tile) * p.N + tid] = s;
     }
-    __syncthreads();
+    cur = nxt;
   }
   if (valid) ((CT *)p.ws_dA)[(g * p.D + d) * p.N + n] = gA;
 }
