@@ -191,6 +191,26 @@ def test_bf16_inputs(dev):
     close(last, rlast, RTOL_BF16, ATOL_BF16, "last")
 
 
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float16, 4e-3)])
+def test_half_precision_inputs_forward_and_backward(dev, dtype, tol):
+    """16-bit x, delta, B, C, z (A, D, bias, h0 and the state float32), forward and every
+    gradient, against the oracle on the rounded inputs.  The kernels compute in float32, so the
+    error is the 16-bit rounding of the outputs and gradients: 8 significand bits for bf16, 11
+    for float16 (tolerance ~8 and ~8 units of that rounding)."""
+    x, delta, A, Bm, Cm, h0 = triton_test_inputs(2, 70, 40, 16, True, seed=21)
+    g = torch.Generator().manual_seed(22)
+    Dv, bias = torch.randn(40, generator=g), torch.randn(40, generator=g) * 0.5 - 1.0
+    z = torch.randn(2, 70, 40, generator=g)
+    dout = torch.randn(2, 70, 40, generator=g).to(dtype)
+    lo = [t.to(dtype) for t in (x, delta, Bm, Cm, z)]
+    ins = (lo[0], lo[1], A, lo[2], lo[3], h0)
+    got = run_fused(ins, dev, "zoh", D=Dv, z=lo[4], bias=bias, softplus=True, dout=dout)
+    assert got[0].dtype == dtype and got[1].dtype == torch.float32
+    assert got[2]["dx"].dtype == dtype and got[2]["dA"].dtype == torch.float32
+    ref = oracle(ins, "zoh", D=Dv, z=lo[4], bias=bias, softplus=True, dout=dout)
+    check_all(got, ref, rtol=tol, atol=tol)
+
+
 def test_float64_inputs(dev):
     """float64 inputs compute in float64 (promote(dtype, float32)); tight agreement."""
     ins = [t.double() if t is not None else None for t in triton_test_inputs(2, 50, 24, 16, True, seed=8)]
