@@ -111,6 +111,22 @@ def cpu_baseline_fwd(L, budget_s=20.0, label="config-2"):
                       f"independent channel tiles timed ({dt:.2f} s each), scaled to all tiles"}
 
 
+def env_record(dev):
+    """The environment the line was measured in: torch/HIP versions, the GPU and the host."""
+    props = torch.cuda.get_device_properties(dev)
+    return {"torch": torch.__version__, "hip": torch.version.hip, "gpu": props.name,
+            "arch": getattr(props, "gcnArchName", None), "compute_units": props.multi_processor_count,
+            "host_cpus": os.cpu_count()}
+
+
+def time_stats(samples):
+    """Median, quartiles and count of a list of per-launch times (ms)."""
+    if len(samples) < 2:
+        return {"median": samples[0] if samples else None, "q1": None, "q3": None, "n": len(samples)}
+    q = statistics.quantiles(samples, n=4)
+    return {"median": statistics.median(samples), "q1": q[0], "q3": q[2], "n": len(samples)}
+
+
 def flush_buffer(dev):
     return torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
 
@@ -185,6 +201,8 @@ def bench_c1(args, dev):
     ct = cold.times_ms()
     del flush
     cold_f, cold_b = statistics.mean(ct["ssm_fwd"]), statistics.mean(ct["ssm_bwd"])
+    kstats = {"ssm_fwd": time_stats(times["ssm_fwd"]), "ssm_bwd": time_stats(times["ssm_bwd"]),
+              "ssm_fwd_cold": time_stats(ct["ssm_fwd"]), "ssm_bwd_cold": time_stats(ct["ssm_bwd"])}
 
     achieved = bb / (bwd_ms * 1e-3) / 1e9
     rec = {
@@ -202,6 +220,7 @@ def bench_c1(args, dev):
         "step_mode": "hip-graph replay of the fwd+bwd step" if ms_step != eager_ms else "eager launches",
         "eager_ms_per_step": eager_ms, "graph_ms_per_step": graph_ms, "graph_matches_eager": graph_ok,
         "kernels_ms": {"ssm_fwd": fwd_ms, "ssm_bwd": bwd_ms, "ssm_fwd_cold": cold_f, "ssm_bwd_cold": cold_b},
+        "kernels_ms_stats": kstats,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic("ssm_bwd_c1"),
                      "kernel": "ssm_bwd (k_bwd + k_bwd_finalize)", "alg_bytes_per_launch": bb,
@@ -502,6 +521,7 @@ def main():
         rec = bench_scans(args, dev)
     else:
         rec = bench_copy(args, dev)
+    rec["env"] = env_record(dev)
     print(json.dumps(rec), flush=True)
 
 
