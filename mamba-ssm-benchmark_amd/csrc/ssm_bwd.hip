@@ -224,7 +224,7 @@ k_bwd(const BwdParams p) {
         S.dy[cc][t] = g;
       }
     }
-    CT hh[CK + 1], aa[CK], cc_[CK];
+    CT hh[CK + 1], aa[CK], cc_[CK], bxs[CK];  // bxs: B x of each step, kept for the reverse walk
     hh[0] = k <= 0 ? h0v : T.ck;
     wave_lds_sync();
     load(T, k - 2);
@@ -243,7 +243,8 @@ k_bwd(const BwdParams p) {
           const int t = q * RB + tt;
           if constexpr (M1) disc_zoh_m1(rdt[tt], ac, aa[t], cc_[t]);
           else disc<METHOD>(rdt[tt], ac, aa[t], cc_[t]);
-          bx[tt] = bcoef<METHOD>(rdt[tt], cc_[t]) * (rB[tt] * rx[tt]);
+          bxs[t] = rB[tt] * rx[tt];
+          bx[tt] = bcoef<METHOD>(rdt[tt], cc_[t]) * bxs[t];
         }
         if (q + 1 < CK / RB) {
           lds_row(&S.dt[c][(q + 1) * RB], rdt);
@@ -280,15 +281,15 @@ k_bwd(const BwdParams p) {
           else dh64 = fma(dh64, (double)a_next, (double)(dyv * Cv));
           const CT lam = (CT)dh64;
           a_next = aa[t];
-          const CT hp = hh[t], Bx = Bv * xv;
+          const CT hp = hh[t], Bx = bxs[t];
           const CT pC = dyv * hh[t + 1];
           const CT dhc = lam * bcoef<METHOD>(dtv, cc_[t]);
           const CT px = dhc * Bv;
           const CT pB = dhc * xv;
           // ddelta_t per state = lambda (da/dz A h_{t-1} + db/ddelta / (B x) B x)
           CT pD;
-          if constexpr (METHOD == 0) {  // da/dz = db/ddelta-factor = a = 1 + am1
-            pD = fma(lam, aa[t], lam) * fma(ac.A, hp, Bx);
+          if constexpr (METHOD == 0) {  // da/dz = db/ddelta-factor = a; a (A h_{t-1} + B x) = A h_t + B x
+            pD = lam * fma(ac.A, hh[t + 1], Bx);
           } else if constexpr (METHOD == 1) {  // da/dz = a, db/ddelta-factor = 1
             pD = fma(lam * aa[t] * ac.A, hp, lam * Bx);
           } else {  // both factors u^2 with u = 1 / (1 - z/2), held in cc_
