@@ -254,6 +254,26 @@ typedef struct ssm_conv_args {
   int64_t workspace_bytes;
 } ssm_conv_args;
 
+/* ------------------------------------------------------------------ RMSNorm
+ * models/common.py:8-16 (the LM's pre-norms, models/lm.py:63,95):
+ *   y = (x * r) * weight,  r = 1 / sqrt(mean(x^2, last dim) + eps)  per row.
+ * Rows of `dim` <= 1024 elements with unit column stride; float32 or float64 throughout. */
+typedef struct ssm_norm_args {
+  int64_t rows, dim;
+  int32_t dtype;           /* SSM_F32 or SSM_F64: x, weight, out, rstd, dout, dx, dweight */
+  int32_t reserved0;
+  double eps;
+  ssm_tensor x;            /* (rows, dim): stride[0] = row stride, stride[1] = 1 */
+  ssm_tensor weight;       /* (dim,) contiguous */
+  ssm_tensor out;          /* forward: (rows, dim) */
+  void *rstd;              /* (rows,) r per row: written by the forward, read by the backward */
+  ssm_tensor dout;         /* backward: (rows, dim) */
+  ssm_tensor dx;           /* backward: (rows, dim) */
+  void *dweight;           /* backward: (dim,) */
+  void *workspace;         /* backward: ssm_norm_workspace_bytes() */
+  int64_t workspace_bytes;
+} ssm_norm_args;
+
 /* ------------------------------------------------------------------ entry points */
 int ssm_abi_version(void);
 const char *ssm_last_error(void);
@@ -267,6 +287,7 @@ int ssm_lscan_check(const ssm_lscan_args *args);
 int ssm_lscan_bwd_check(const ssm_lscan_bwd_args *args);
 int ssm_disc_check(const ssm_disc_args *args);
 int ssm_conv_check(const ssm_conv_args *args);
+int ssm_norm_check(const ssm_norm_args *args);
 
 /* Buffer sizes in bytes (host-only). */
 int64_t ssm_fwd_saved_bytes(const ssm_fwd_args *args);
@@ -276,6 +297,7 @@ int64_t ssm_lscan_workspace_bytes(const ssm_lscan_args *args);
 int64_t ssm_lscan_bwd_workspace_bytes(const ssm_lscan_bwd_args *args);
 int64_t ssm_disc_workspace_bytes(const ssm_disc_args *args);
 int64_t ssm_conv_workspace_bytes(const ssm_conv_args *args);
+int64_t ssm_norm_workspace_bytes(const ssm_norm_args *args);
 
 /* Launches (asynchronous on `stream`). */
 int ssm_fwd(const ssm_fwd_args *args, void *stream);
@@ -288,6 +310,8 @@ int ssm_disc_fwd(const ssm_disc_args *args, void *stream);
 int ssm_disc_bwd(const ssm_disc_args *args, void *stream);
 int ssm_conv_fwd(const ssm_conv_args *args, void *stream);
 int ssm_conv_bwd(const ssm_conv_args *args, void *stream);
+int ssm_norm_fwd(const ssm_norm_args *args, void *stream);   /* models/common.py:14-16 */
+int ssm_norm_bwd(const ssm_norm_args *args, void *stream);   /* autograd of :14-16 */
 
 /* ------------------------------------------------------------------ plans (host-only, exact integers)
  * The reference's integer planning functions, returned bit-exactly. */

@@ -715,4 +715,74 @@ int ssm_conv_bwd(const ssm_conv_args *a, void *stream) {
   return e == hipSuccess ? ok() : hip_fail(e, "ssm_conv_bwd");
 }
 
+// ------------------------------------------------------------------ RMSNorm
+static NormParams norm_params(const ssm_norm_args *a) {
+  NormParams p;
+  memset(&p, 0, sizeof(p));
+  p.R = a->rows;
+  p.C = a->dim;
+  p.eps = a->eps;
+  p.x = a->x.data; p.sx = a->x.stride[0];
+  p.w = a->weight.data;
+  p.y = a->out.data; p.sy = a->out.stride[0];
+  p.rstd = a->rstd;
+  p.dy = a->dout.data; p.sdy = a->dout.stride[0];
+  p.dx = a->dx.data; p.sdx = a->dx.stride[0];
+  p.dw = a->dweight;
+  p.rpw = norm_rows_per_wave(norm_kc_of(a->dim));
+  p.nblk = cdiv(a->rows, (int64_t)kNormWaves * p.rpw);
+  return p;
+}
+
+static int norm_row_view(const ssm_tensor &t, const char *name) {
+  if (!has(t)) return fail(SSM_EINVAL, "required tensor '%s' is missing", name);
+  if (t.stride[1] != 1) return fail(SSM_EINVAL, "%s must have unit column stride", name);
+  return SSM_OK;
+}
+
+int ssm_norm_check(const ssm_norm_args *a) {
+  if (!a) return fail(SSM_EINVAL, "null args");
+  if (a->dtype != SSM_F32 && a->dtype != SSM_F64) return fail(SSM_EINVAL, "RMSNorm takes float32 or float64");
+  if (a->rows < 1 || a->dim < 1) return fail(SSM_EINVAL, "empty RMSNorm: rows=%lld dim=%lld",
+                                             (long long)a->rows, (long long)a->dim);
+  if (a->dim > kNormMaxC) return fail(SSM_EINVAL, "RMSNorm dim=%lld > %d", (long long)a->dim, kNormMaxC);
+  if (a->rows >= (1LL << 31)) return fail(SSM_EINVAL, "RMSNorm rows=%lld too large", (long long)a->rows);
+  if (!(a->eps >= 0.0)) return fail(SSM_EINVAL, "RMSNorm eps must be >= 0");
+  int rc = norm_row_view(a->x, "x");
+  if (rc) return rc;
+  if (!has(a->weight) || (a->dim > 1 && a->weight.stride[0] != 1))
+    return fail(SSM_EINVAL, "weight must be a contiguous (dim,) tensor");
+  if (!a->rstd) return fail(SSM_EINVAL, "required buffer 'rstd' is missing");
+  return ok();
+}
+
+int64_t ssm_norm_workspace_bytes(const ssm_norm_args *a) {
+  if (ssm_norm_check(a)) return -1;
+  const NormParams p = norm_params(a);
+  return align256(p.nblk * a->dim * state_size(a->dtype));
+}
+
+int ssm_norm_fwd(const ssm_norm_args *a, void *stream) {
+  int rc = ssm_norm_check(a);
+  if (!rc) rc = norm_row_view(a->out, "out");
+  if (rc) return rc;
+  hipError_t e = launch_norm(norm_params(a), a->dtype, false, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "ssm_norm_fwd");
+}
+
+int ssm_norm_bwd(const ssm_norm_args *a, void *stream) {
+  int rc = ssm_norm_check(a);
+  if (!rc) rc = norm_row_view(a->dout, "dout");
+  if (!rc) rc = norm_row_view(a->dx, "dx");
+  if (rc) return rc;
+  if (!a->dweight) return fail(SSM_EINVAL, "required buffer 'dweight' is missing");
+  const int64_t need = ssm_norm_workspace_bytes(a);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(SSM_ESPACE, "workspace of %lld bytes required", (long long)need);
+  NormParams p = norm_params(a);
+  p.ws = a->workspace;
+  hipError_t e = launch_norm(p, a->dtype, true, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "ssm_norm_bwd");
+}
+
 }  // extern "C"

@@ -159,6 +159,25 @@ struct ConvParams {
   void *ws;  // backward: (B * nblk, D, W + 1) partial dweight / dbias, one row per workgroup
 };
 
+// RMSNorm over rows of C <= kNormMaxC elements (unit column stride): a wavefront per row,
+// kNormWaves wavefronts per workgroup; the backward's wavefronts take norm_rows_per_wave rows.
+constexpr int kNormWaves = 4, kNormThreads = kNormWaves * 64, kNormFinThreads = 1024, kNormMaxC = 1024;
+// columns per lane (power of two) for a row of C elements
+inline constexpr int norm_kc_of(int64_t C) {
+  return C <= 64 ? 1 : C <= 128 ? 2 : C <= 256 ? 4 : C <= 512 ? 8 : C <= 1024 ? 16 : 0;
+}
+inline constexpr int norm_rows_per_wave(int kc) { return kc <= 4 ? 8 : kc == 8 ? 4 : 2; }
+struct NormParams {
+  int64_t R, C;
+  double eps;
+  int64_t sx, sy, sdy, sdx;  // row strides (elements)
+  const void *x, *w, *dy;
+  void *y, *rstd, *dx, *dw;
+  void *ws;      // backward: (nblk, C) per-workgroup weight-gradient partials
+  int64_t nblk;  // backward workgroups
+  int rpw;       // backward rows per wavefront
+};
+
 // Fused decode layer (float32, row-major); one workgroup per batch row.
 struct DecodeParams {
   int64_t B, dim, N, W, R, dm, P;  // P = R + 2 N
@@ -177,6 +196,7 @@ hipError_t launch_lscan_grad(const LscanGradParams &p, int dtype, hipStream_t s)
 // Channels per workgroup of the discretize backward (its dB partial-sum tile).
 inline int disc_channels(int np) { return kThreads / np; }
 hipError_t launch_conv(const ConvParams &p, int dtype, bool bwd, hipStream_t s);
+hipError_t launch_norm(const NormParams &p, int dtype, bool bwd, hipStream_t s);
 size_t decode_shared_bytes(const DecodeParams &p);
 hipError_t launch_decode(const DecodeParams &p, int method, hipStream_t s);
 hipError_t launch_disc_fwd(const DiscParams &p, int dtype, int method, int np, hipStream_t s);

@@ -105,6 +105,14 @@ class ConvArgs(ctypes.Structure):
                 ("workspace", c_vp), ("workspace_bytes", c_i64)]
 
 
+class NormArgs(ctypes.Structure):
+    _fields_ = [("rows", c_i64), ("dim", c_i64), ("dtype", c_i32), ("reserved0", c_i32),
+                ("eps", ctypes.c_double),
+                ("x", Tensor), ("weight", Tensor), ("out", Tensor), ("rstd", c_vp),
+                ("dout", Tensor), ("dx", Tensor), ("dweight", c_vp),
+                ("workspace", c_vp), ("workspace_bytes", c_i64)]
+
+
 # name -> (restype, argtypes)
 _SIGS = {
     "ssm_abi_version": (c_i32, []),
@@ -117,6 +125,7 @@ _SIGS = {
     "ssm_lscan_bwd_check": (c_i32, [ctypes.POINTER(LscanBwdArgs)]),
     "ssm_disc_check": (c_i32, [ctypes.POINTER(DiscArgs)]),
     "ssm_conv_check": (c_i32, [ctypes.POINTER(ConvArgs)]),
+    "ssm_norm_check": (c_i32, [ctypes.POINTER(NormArgs)]),
     "ssm_fwd_saved_bytes": (c_i64, [ctypes.POINTER(FwdArgs)]),
     "ssm_fwd_workspace_bytes": (c_i64, [ctypes.POINTER(FwdArgs)]),
     "ssm_bwd_workspace_bytes": (c_i64, [ctypes.POINTER(BwdArgs)]),
@@ -124,6 +133,7 @@ _SIGS = {
     "ssm_lscan_bwd_workspace_bytes": (c_i64, [ctypes.POINTER(LscanBwdArgs)]),
     "ssm_disc_workspace_bytes": (c_i64, [ctypes.POINTER(DiscArgs)]),
     "ssm_conv_workspace_bytes": (c_i64, [ctypes.POINTER(ConvArgs)]),
+    "ssm_norm_workspace_bytes": (c_i64, [ctypes.POINTER(NormArgs)]),
     "ssm_fwd": (c_i32, [ctypes.POINTER(FwdArgs), c_vp]),
     "ssm_bwd": (c_i32, [ctypes.POINTER(BwdArgs), c_vp]),
     "ssm_step": (c_i32, [ctypes.POINTER(StepArgs), c_vp]),
@@ -134,6 +144,8 @@ _SIGS = {
     "ssm_disc_bwd": (c_i32, [ctypes.POINTER(DiscArgs), c_vp]),
     "ssm_conv_fwd": (c_i32, [ctypes.POINTER(ConvArgs), c_vp]),
     "ssm_conv_bwd": (c_i32, [ctypes.POINTER(ConvArgs), c_vp]),
+    "ssm_norm_fwd": (c_i32, [ctypes.POINTER(NormArgs), c_vp]),
+    "ssm_norm_bwd": (c_i32, [ctypes.POINTER(NormArgs), c_vp]),
     "ssm_default_chunk": (c_i64, [c_i64]),
     "ssm_scan_blocks": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.POINTER(c_i64), c_i64]),
     "ssm_block_d": (c_i64, [c_i64, c_i64]),

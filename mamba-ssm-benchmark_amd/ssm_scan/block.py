@@ -2,8 +2,9 @@
 models/lm.py restricted to Mamba layers -- the callers of the scan path.
 
 Same parameters (names, shapes, initialization) and the same forward / decode interface as
-the reference, so a state_dict moves between the two.  in_proj, x_proj and out_proj are torch GEMMs; the
-scan-path work runs in the engine's kernels:
+the reference, so a state_dict moves between the two.  in_proj, x_proj and out_proj are torch GEMMs
+(the weight gradients split over the tokens, ssm_scan.linear); the scan-path work runs in the
+engine's kernels:
   conv + SiLU                   ssm_scan.conv.causal_conv1d          (models/mamba.py:101-107)
   dt_proj (+ bias, softplus)    fused into the scan kernels' delta   (models/mamba.py:75-76)
                                 staging (the step kernel: bias + softplus)
@@ -26,6 +27,8 @@ import torch.nn.functional as F
 
 from .conv import causal_conv1d
 from .hip_scan import selective_scan_fn
+from .linear import linear
+from .norm import rms_norm
 from .scan import selective_scan
 from .step import ssm_step
 
@@ -82,7 +85,7 @@ class Mamba(nn.Module):
         Bsz, L, _ = x.shape
         ct = torch.promote_types(x.dtype, torch.float32)
         if self.selective:
-            dt, Bm, Cm = self.x_proj(x).split([self.dt_rank, self.d_state, self.d_state], dim=-1)
+            dt, Bm, Cm = linear(self.x_proj, x).split([self.dt_rank, self.d_state, self.d_state], dim=-1)
             # bias + softplus run in the kernel
             delta = (dt, self.dt_proj.weight) if lowrank else F.linear(dt, self.dt_proj.weight)
             bias = self.dt_proj.bias
@@ -127,7 +130,7 @@ class Mamba(nn.Module):
 
     def forward(self, u, state=None, pos=0, return_delta=False):
         Bsz, L, _ = u.shape
-        x, z = self.in_proj(u).chunk(2, dim=-1)
+        x, z = linear(self.in_proj, u).chunk(2, dim=-1)
         x = self._conv(x, state)
         decode = state is not None and L == 1
         fused = not decode and self.scan in ("auto", "triton")
@@ -153,12 +156,13 @@ class Mamba(nn.Module):
             y = (y + x * self.D.to(x.dtype)) * F.silu(z)
         if state is not None and L > 1:
             state.ssm.copy_(last)
-        out = self.out_proj(y)
+        out = linear(self.out_proj, y)
         return (out, full_delta) if return_delta else out
 
 
 class RMSNorm(nn.Module):
-    """models/common.py RMSNorm: x / rms(x) * weight."""
+    """models/common.py RMSNorm: x / rms(x) * weight (ssm_scan.norm: one kernel per pass for
+    float32 rows)."""
 
     def __init__(self, d, eps=1e-5):
         super().__init__()
@@ -166,8 +170,7 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(d))
 
     def forward(self, x):
-        xf = x.float()
-        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)).to(x.dtype) * self.weight
+        return rms_norm(x, self.weight, self.eps)
 
 
 class Block(nn.Module):
@@ -243,7 +246,7 @@ class MambaLM(nn.Module):
         x = self.embed(idx)
         for i, block in enumerate(self.blocks):
             x = block(x, None if states is None else states[i], pos)
-        return self.head(self.norm_f(x))
+        return linear(self.head, self.norm_f(x))
 
     @torch.no_grad()
     def generate(self, prompt, n_new, temperature=1.0, top_k=None, max_len=None):

@@ -1,0 +1,61 @@
+"""The LM's Linear layers (in_proj, x_proj, out_proj, the tied head) with a split-K weight
+gradient.
+
+A Linear layer's weight gradient is dW = dY^T X, contracted over the tokens (B * L of them).
+At config 3 (8,192 tokens) the library GEMM for the layers' (out, in) shapes (1024, 256),
+(256, 512), (48, 512) and (256, 256) tiles only the small output -- 32 to 256 workgroups on
+256 CUs -- and walks all 8,192 tokens inside each tile.  Splitting the tokens into S slices,
+S independent products in one batched GEMM followed by a fixed-order sum over the slices,
+fills the GPU: on one MI355X (float32) 45 / 26 / 26 / 25 us against 60 / 55 / 45 / 53 us.
+The forward and the input gradient stay the plain GEMMs of F.linear; the parameters are the
+nn.Linear modules' own (models/mamba.py, models/lm.py use nn.Linear).
+"""
+
+import torch
+import torch.nn.functional as F
+
+SPLITS = 8          # token slices of the weight gradient
+MIN_TOKENS = 2048   # below this the plain product already fills the GPU as well
+
+
+def weight_grad(dy, x, splits=SPLITS):
+    """dy (K, O), x (K, I) -> dy^T x (O, I).  Split over K when K is a multiple of `splits`
+    and at least MIN_TOKENS; the slices' products are summed in slice order."""
+    K = dy.shape[0]
+    if splits <= 1 or K % splits or K < MIN_TOKENS:
+        return dy.t() @ x
+    kc = K // splits
+    a = dy.reshape(splits, kc, dy.shape[1]).transpose(1, 2)   # (S, O, kc)
+    b = x.reshape(splits, kc, x.shape[1]).contiguous()         # (S, kc, I), right operand dense
+    return torch.bmm(a, b).sum(0)
+
+
+class _SplitKLinear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        ctx.save_for_backward(x, weight)
+        ctx.has_bias = bias is not None
+        return F.linear(x, weight, bias)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1])
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = (dy2 @ w).reshape(x.shape)
+        if ctx.needs_input_grad[1]:
+            dw = weight_grad(dy2, x.reshape(-1, x.shape[-1]))
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = dy2.sum(0)
+        return dx, dw, db
+
+
+def linear(layer, x):
+    """layer(x) for an nn.Linear; while its weight is trained on at least MIN_TOKENS tokens
+    (grad mode, no autocast, matching dtypes) the weight gradient is the split-K product."""
+    w = layer.weight
+    if (torch.is_grad_enabled() and w.requires_grad and not torch.is_autocast_enabled(x.device.type)
+            and x.dtype == w.dtype and x.numel() // max(x.shape[-1], 1) >= MIN_TOKENS):
+        return _SplitKLinear.apply(x, w, layer.bias)
+    return layer(x)

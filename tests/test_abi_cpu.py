@@ -46,7 +46,7 @@ def test_ctypes_layout_matches_c_header(tmp_path):
     structs = {"ssm_tensor": _abi.Tensor, "ssm_fwd_args": _abi.FwdArgs, "ssm_bwd_args": _abi.BwdArgs,
                "ssm_step_args": _abi.StepArgs, "ssm_decode_args": _abi.DecodeArgs, "ssm_lscan_args": _abi.LscanArgs,
                "ssm_lscan_bwd_args": _abi.LscanBwdArgs,
-               "ssm_disc_args": _abi.DiscArgs, "ssm_conv_args": _abi.ConvArgs}
+               "ssm_disc_args": _abi.DiscArgs, "ssm_conv_args": _abi.ConvArgs, "ssm_norm_args": _abi.NormArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -239,3 +239,45 @@ def test_linear_scan_grid_limit():
     a.algo = 4                                            # chunked, chunk 1: 2^32 lanes
     with pytest.raises(ValueError, match="too large"):
         _abi.check(lib.ssm_lscan_check(ctypes.byref(a)), "ssm_lscan")
+
+
+def _norm_args(rows=4, dim=256, dtype=0):
+    x = torch.zeros(rows, dim)
+    a = _abi.NormArgs()
+    a.rows, a.dim, a.dtype, a.eps = rows, dim, dtype, 1e-5
+    a.x, a.weight = _abi.view(x), _abi.view(torch.ones(dim))
+    a.rstd = x.data_ptr()
+    a._keep = x
+    return a
+
+
+@pytest.mark.parametrize("change,ok", [({}, True), ({"dim": 1024}, True), ({"dim": 1025}, False),
+                                       ({"dim": 0}, False), ({"rows": 0}, False), ({"dtype": 1}, False),
+                                       ({"dtype": 3}, True), ({"eps": -1.0}, False)])
+def test_norm_validation(change, ok):
+    """RMSNorm rows of 1..1024 float32/float64 elements; other shapes and dtypes are rejected on
+    the host."""
+    a = _norm_args(**{k: v for k, v in change.items() if k in ("rows", "dim", "dtype")})
+    if "eps" in change:
+        a.eps = change["eps"]
+    rc = _abi.lib().ssm_norm_check(ctypes.byref(a))
+    if ok:
+        assert rc == 0
+    else:
+        with pytest.raises(ValueError):
+            _abi.check(rc, "ssm_norm")
+
+
+def test_norm_needs_unit_column_stride_and_rstd():
+    lib = _abi.lib()
+    a = _norm_args()
+    a.x.stride[1] = 2
+    with pytest.raises(ValueError, match="unit column stride"):
+        _abi.check(lib.ssm_norm_check(ctypes.byref(a)), "ssm_norm")
+    a = _norm_args()
+    a.rstd = None
+    with pytest.raises(ValueError, match="rstd"):
+        _abi.check(lib.ssm_norm_check(ctypes.byref(a)), "ssm_norm")
+    a = _norm_args(rows=1000, dim=256)
+    # backward partials: one (dim,) row per workgroup of 4 wavefronts x 8 rows
+    assert lib.ssm_norm_workspace_bytes(ctypes.byref(a)) == ((1000 + 31) // 32) * 256 * 4

@@ -68,3 +68,32 @@ def test_state_size_is_constant_in_length():
     s1 = MambaLM.state_nbytes(m.init_state(1, 100, "cpu"))
     s2 = MambaLM.state_nbytes(m.init_state(1, 1000, "cpu"))
     assert s1 == s2 == 2 * (64 * 3 + 64 * 16) * 4
+
+
+@pytest.mark.parametrize("K,splits", [(4096, 8), (4100, 8), (1024, 8), (8192, 1)])
+def test_split_k_weight_gradient_equals_the_plain_product(K, splits):
+    """dW = dy^T x summed over token slices (ssm_scan.linear) against the plain product, in
+    float64: ragged K and small K fall back to the plain product."""
+    from ssm_scan.linear import weight_grad
+    g = torch.Generator().manual_seed(K)
+    dy = torch.randn(K, 48, generator=g, dtype=torch.float64)
+    x = torch.randn(K, 40, generator=g, dtype=torch.float64)
+    torch.testing.assert_close(weight_grad(dy, x, splits), dy.t() @ x, rtol=1e-12, atol=1e-12)
+
+
+def test_split_k_linear_gradients_match_nn_linear():
+    """The LM's Linear with the split-K weight gradient gives nn.Linear's output and gradients
+    (input, weight, bias) in float64."""
+    from ssm_scan.linear import linear
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(40, 48).double()
+    x = torch.randn(2, 2048, 40, dtype=torch.float64, requires_grad=True)
+    y = linear(lin, x)
+    gy = torch.randn_like(y)
+    y.backward(gy)
+    got = [y.detach(), x.grad.clone(), lin.weight.grad.clone(), lin.bias.grad.clone()]
+    x.grad = lin.weight.grad = lin.bias.grad = None
+    ref = lin(x)
+    ref.backward(gy)
+    for a, b in zip(got, [ref.detach(), x.grad, lin.weight.grad, lin.bias.grad]):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
