@@ -1,0 +1,178 @@
+"""Seeded random configurations of the fused scan (forward + every gradient) against the
+float64 oracle: shapes, methods, optional operands and storage layouts drawn together, so
+combinations that the targeted tests do not list are still covered.
+
+Each case prints its configuration before running (it names the case if it fails).
+Tolerances as the fused tests: rtol 1e-4 / atol 1e-5 x max(1, RMS), float32.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import ssm_scan
+from oracle import scan_ref as R
+from ssm_inputs import np64
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-4, 1e-5
+METHODS = ("zoh", "euler", "bilinear")
+
+
+def close(got, ref, name):
+    got = np64(got)
+    scale = max(1.0, float(np.sqrt(np.mean(np.square(ref))))) if np.size(ref) else 1.0
+    np.testing.assert_allclose(got, ref, rtol=RTOL, atol=ATOL * scale, err_msg=name)
+
+
+def draw(seed):
+    rng = np.random.default_rng(seed)
+    cfg = dict(B=int(rng.integers(1, 4)), L=int(rng.choice([1, 2, 15, 16, 17, 63, 200, 333])),
+               D=int(rng.integers(1, 71)), N=int(rng.choice([1, 2, 5, 8, 16, 24, 32, 64])),
+               method=METHODS[int(rng.integers(0, 3))], gate=bool(rng.integers(0, 2)),
+               skip=bool(rng.integers(0, 2)), softplus=bool(rng.integers(0, 2)), h0=bool(rng.integers(0, 2)),
+               dlast=bool(rng.integers(0, 2)), channel_major=bool(rng.integers(0, 2)),
+               bc_split=bool(rng.integers(0, 2)))
+    return cfg
+
+
+def build(cfg, seed):
+    g = torch.Generator().manual_seed(seed)
+    B, L, D, N = cfg["B"], cfg["L"], cfg["D"], cfg["N"]
+    x = torch.randn(B, L, D, generator=g)
+    if cfg["softplus"]:
+        delta = torch.randn(B, L, D, generator=g) * 0.5 - 1.0
+        bias = torch.randn(D, generator=g) * 0.5 - 2.0
+    else:
+        delta = torch.rand(B, L, D, generator=g) * 0.3 + 1e-3
+        bias = None
+    A = -(torch.rand(D, N, generator=g) * 4 + 0.05)
+    proj = torch.randn(B, L, 3 + 2 * N, generator=g)
+    Dv = torch.randn(D, generator=g) if cfg["skip"] else None
+    z = torch.randn(B, L, D, generator=g) if cfg["gate"] else None
+    h0 = torch.randn(B, D, N, generator=g) if cfg["h0"] else None
+    dout = torch.randn(B, L, D, generator=g)
+    dlast = torch.randn(B, D, N, generator=g) if cfg["dlast"] else None
+    return x, delta, A, proj, Dv, z, bias, h0, dout, dlast
+
+
+def oracle(x, delta, A, proj, Dv, z, bias, h0, dout, dlast, N, method, softplus):
+    x, delta, A, proj = np64(x), np64(delta), np64(A), np64(proj)
+    Bm, Cm = proj[..., 3:3 + N], proj[..., 3 + N:]
+    raw = delta + (np64(bias) if bias is not None else 0.0)
+    d_eff = np.log1p(np.exp(raw)) if softplus else raw
+    D_, z_, h0_ = (None if t is None else np64(t) for t in (Dv, z, h0))
+    out, _, last = R.selective_scan_fwd(x, d_eff, A, Bm, Cm, h0_, method, D_, z_)
+    gr = R.selective_scan_bwd(x, d_eff, A, Bm, Cm, np64(dout), h0_, method, D_, z_,
+                              None if dlast is None else np64(dlast))
+    if softplus:
+        gr["ddelta"] = gr["ddelta"] / (1.0 + np.exp(-raw))
+    if bias is not None:
+        gr["ddelta_bias"] = gr["ddelta"].sum(axis=(0, 1))
+    return out, last, gr
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_configuration_matches_oracle(dev, seed):
+    cfg = draw(seed)
+    print(f"case seed={seed} {cfg}", flush=True)
+    x, delta, A, proj, Dv, z, bias, h0, dout, dlast = build(cfg, 1000 + seed)
+    N = cfg["N"]
+
+    def to_dev(t):
+        if t is None:
+            return None
+        t = t.to(dev)
+        if cfg["channel_major"] and t.dim() == 3 and t.shape[-1] == cfg["D"]:
+            t = t.transpose(1, 2).contiguous().transpose(1, 2)   # (B, D, L) storage
+        return t.requires_grad_()
+
+    leaves = [to_dev(t) for t in (x, delta, A, proj, Dv, z, bias, h0)]
+    xg, dg, Ag, pg, Dg, zg, bg, hg = leaves
+    if cfg["bc_split"]:
+        Bm, Cm = pg[..., 3:3 + N], pg[..., 3 + N:]          # strided views of an x_proj-like output
+    else:
+        Bm, Cm = pg[..., 3:3 + N].contiguous(), pg[..., 3 + N:].contiguous()
+    out, last = ssm_scan.selective_scan_fn(xg, dg, Ag, Bm, Cm, D=Dg, z=zg, delta_bias=bg,
+                                           delta_softplus=cfg["softplus"], h0=hg, method=cfg["method"],
+                                           return_last_state=True)
+    loss = (out * dout.to(dev)).sum()
+    if dlast is not None:
+        loss = loss + (last * dlast.to(dev)).sum()
+    loss.backward()
+    rout, rlast, rg = oracle(x, delta, A, proj, Dv, z, bias, h0, dout, dlast, N, cfg["method"], cfg["softplus"])
+    close(out, rout, "out")
+    close(last, rlast, "last")
+    close(xg.grad, rg["dx"], "dx")
+    close(dg.grad, rg["ddelta"], "ddelta")
+    close(Ag.grad, rg["dA"], "dA")
+    close(pg.grad[..., 3:3 + N], rg["dB"], "dB")
+    close(pg.grad[..., 3 + N:], rg["dC"], "dC")
+    assert float(pg.grad[..., :3].abs().max()) == 0.0
+    if Dg is not None:
+        close(Dg.grad, rg["dD"], "dD")
+    if zg is not None:
+        close(zg.grad, rg["dz"], "dz")
+    if bg is not None:
+        close(bg.grad, rg["ddelta_bias"], "ddelta_bias")
+    if hg is not None:
+        close(hg.grad, rg["dh0"], "dh0")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_lowrank_configuration_matches_oracle(dev, seed):
+    """The dt_proj projection fused into delta staging (delta_proj, rank 1..16, dstate <= 16):
+    random shapes, methods, gate/skip/h0 and layouts; every gradient including d(dt) and dW."""
+    rng = np.random.default_rng(500 + seed)
+    B, L, D = int(rng.integers(1, 4)), int(rng.choice([1, 16, 17, 100, 257])), int(rng.integers(1, 70))
+    N, Rk = int(rng.choice([1, 4, 8, 13, 16])), int(rng.integers(1, 17))
+    method = METHODS[int(rng.integers(0, 3))]
+    gate, skip, h0f, cm = (bool(rng.integers(0, 2)) for _ in range(4))
+    print(f"case seed={seed} B={B} L={L} D={D} N={N} R={Rk} {method} gate={gate} skip={skip} "
+          f"h0={h0f} channel_major={cm}", flush=True)
+    g = torch.Generator().manual_seed(2000 + seed)
+    x = torch.randn(B, L, D, generator=g)
+    proj = torch.randn(B, L, Rk + 2 * N, generator=g)
+    W = torch.randn(D, Rk, generator=g) * (0.5 / Rk ** 0.5)
+    A = -(torch.rand(D, N, generator=g) * 4 + 0.05)
+    bias = torch.rand(D, generator=g) * 2.0 - 4.0
+    Dv = torch.randn(D, generator=g) if skip else None
+    z = torch.randn(B, L, D, generator=g) if gate else None
+    h0 = torch.randn(B, D, N, generator=g) if h0f else None
+    dout = torch.randn(B, L, D, generator=g)
+
+    def to_dev(t):
+        if t is None:
+            return None
+        t = t.to(dev)
+        if cm and t.dim() == 3 and t.shape[-1] == D:
+            t = t.transpose(1, 2).contiguous().transpose(1, 2)
+        return t.requires_grad_()
+
+    xg, pg, Wg, Ag, bg, Dg, zg, hg = (to_dev(t) for t in (x, proj, W, A, bias, Dv, z, h0))
+    dt, Bm, Cm = pg[..., :Rk], pg[..., Rk:Rk + N], pg[..., Rk + N:]
+    out = ssm_scan.selective_scan_fn(xg, dt, Ag, Bm, Cm, D=Dg, z=zg, delta_bias=bg, delta_softplus=True,
+                                     h0=hg, method=method, delta_proj=Wg)
+    (out * dout.to(dev)).sum().backward()
+
+    xd, pd, Wd = np64(x), np64(proj), np64(W)
+    dtd, Bd, Cd = pd[..., :Rk], pd[..., Rk:Rk + N], pd[..., Rk + N:]
+    raw = dtd @ Wd.T + np64(bias)
+    d_eff = np.log1p(np.exp(raw))
+    D_, z_, h0_ = (None if t is None else np64(t) for t in (Dv, z, h0))
+    rout, _, _ = R.selective_scan_fwd(xd, d_eff, np64(A), Bd, Cd, h0_, method, D_, z_)
+    gr = R.selective_scan_bwd(xd, d_eff, np64(A), Bd, Cd, np64(dout), h0_, method, D_, z_, None)
+    draw_ = gr["ddelta"] / (1.0 + np.exp(-raw))
+    close(out, rout, "out")
+    close(xg.grad, gr["dx"], "dx")
+    close(Ag.grad, gr["dA"], "dA")
+    close(pg.grad, np.concatenate([draw_ @ Wd, gr["dB"], gr["dC"]], -1), "dproj")
+    close(Wg.grad, draw_.reshape(-1, D).T @ dtd.reshape(-1, Rk), "dW")
+    close(bg.grad, draw_.sum(axis=(0, 1)), "dbias")
+    if Dg is not None:
+        close(Dg.grad, gr["dD"], "dD")
+    if zg is not None:
+        close(zg.grad, gr["dz"], "dz")
+    if hg is not None:
+        close(hg.grad, gr["dh0"], "dh0")
