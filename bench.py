@@ -467,12 +467,38 @@ def bench_scans(args, dev):
                                    "frac": nbytes / (t * 1e-3) / (HBM_PEAK_GBS * 1e9), "alg_bytes": nbytes}
     del a_, b_, ga, gb, leaves
     best = max(lines, key=lambda k: lines[k]["frac"])
-    return {"metric": "composed-path kernels, HBM GB/s (linear scans B2 L4096 M16384, discretize B2 L4096 D1024 N16)",
-            "value": lines[best]["GB/s"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 2,
-            "ms_per_step": lines[best]["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "f32", "data": "synthetic", "config": {"workload": "composed path (models/scan.py algorithms)",
-                                                             "best": best},
-            "kernels": lines}
+    rec = {"metric": "composed-path kernels, HBM GB/s (linear scans B2 L4096 M16384, discretize B2 L4096 D1024 N16)",
+           "value": lines[best]["GB/s"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 2,
+           "ms_per_step": lines[best]["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f32", "data": "synthetic", "config": {"workload": "composed path (models/scan.py algorithms)",
+                                                            "best": best},
+           "kernels": lines}
+    if not args.no_cpu_baseline:
+        rec["cpu_baseline"] = cpu_baseline_scans(B, L, M, lines["chunked"]["ms"])
+    return rec
+
+
+def cpu_baseline_scans(B, L, M, gpu_ms, budget_s=10.0, m_sample=2048):
+    """The reference's CPU scan (scan_chunked, models/scan.py:142-165, restated in torch in
+    oracle/cpu_chunked.py) on a column sample of the scans workload; the columns are
+    independent recurrences, so the full scan's time is the sample's x M / m_sample."""
+    from oracle import cpu_chunked
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    g = torch.Generator().manual_seed(0)
+    a = torch.rand(B, L, m_sample, generator=g) * 0.5 + 0.5
+    b = torch.randn(B, L, m_sample, generator=g)
+    cpu_chunked.scan_chunked(a, b)                  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while reps < 1 or (time.perf_counter() - t0 < budget_s and reps < 200):
+        cpu_chunked.scan_chunked(a, b)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    full_s = dt * M / m_sample
+    return {"value": 3 * 4 * B * L * M / full_s / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "seconds_full_scan": full_s, "gpu_chunked_fraction": gpu_ms * 1e-3 / full_s,
+            "sample": f"scan_chunked of the torch-CPU restatement of the reference (oracle/cpu_chunked.py) on "
+                      f"(B, L, M) = ({B}, {L}, {m_sample}) float32, {reps} reps of {dt * 1e3:.1f} ms, scaled to "
+                      f"M = {M}"}
 
 
 def bench_copy(args, dev):
