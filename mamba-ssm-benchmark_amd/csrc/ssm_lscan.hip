@@ -15,10 +15,12 @@
 //                                          down-sweep along time over tiles of 64 steps in LDS,
 //                                          giving exclusive (A, S) prefixes; h = a (A h_in + S)
 //                                          + b, the tile's last h carried to the next.
-//   chunked        models/scan.py:142-165  three launches: per-chunk local scans from zero
-//                                          (chunk summaries P = prod a, E = local end), a scan
-//                                          over the chunk summaries per (b, m), then the
-//                                          correction h += (prod of a inside the chunk) h_in.
+//   chunked        models/scan.py:142-165  three launches: per-chunk summaries from zero
+//                                          (P = prod a, E = local end; no states written), a
+//                                          scan over the summaries per (b, m) giving each
+//                                          chunk's entering state h_in, then each chunk
+//                                          scanned from h_in (scan_chunked's local scan plus
+//                                          its correction h += P_t h_in, in one pass).
 // Direction: with `reverse` the recurrence runs from t = L-1 down to 0.  With `shift` (used
 // by the adjoint) the multiplier at a step is the a of the previous step in processing order
 // and 1 for the first step: lambda_t = g_t + a_{t+1} lambda_{t+1} (models/scan.py:239-240).
@@ -244,17 +246,18 @@ __global__ void __launch_bounds__(256) k_lscan_bl(const LscanParams P) {
 }
 
 // ------------------------------------------------------------------ chunked (three phases)
+// Reduce, carry, scan: each chunk's summary (P = product of its multipliers, E = its end
+// state from zero) is formed without writing any state; a sequential scan over the summaries
+// gives every chunk's entering state h_in; each chunk is then scanned from h_in.  The chunks'
+// states equal scan_chunked's local states corrected by P_t h_in (models/scan.py:152-164),
+// to rounding, and the states are written once instead of written, re-read and rewritten.
 constexpr int kSeqAhead = 16;  // steps whose inputs are read before their dependent updates
 
-template <typename CT>
-__global__ void __launch_bounds__(256) k_lscan_chunk_local(const LscanParams P) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= P.B * P.nc * P.M) return;
-  const int64_t m = i % P.M, cj = (i / P.M) % P.nc, b = i / (P.M * P.nc);
-  Chain<CT> ch{P, b, m};
-  CT h = 0, prod = 1;
-  const int p0 = (int)cj * P.chunk;
-  const int p1 = p0 + P.chunk < (int)P.L ? p0 + P.chunk : (int)P.L;
+// Walks positions [p0, p1) of a chain from state h: h <- mult h + b at each step, with the
+// product of the multipliers in prod (REDUCE) or every state stored (otherwise).
+template <typename CT, bool REDUCE>
+__device__ __forceinline__ void chunk_walk(const LscanParams &P, const Chain<CT> &ch, int p0, int p1, CT &h,
+                                           CT &prod) {
   int pos = p0;
   for (; pos + kSeqAhead <= p1; pos += kSeqAhead) {  // inputs read ahead of the updates
     CT av[kSeqAhead], bv[kSeqAhead];
@@ -266,20 +269,32 @@ __global__ void __launch_bounds__(256) k_lscan_chunk_local(const LscanParams P) 
 #pragma unroll
     for (int u = 0; u < kSeqAhead; ++u) {
       h = fma(av[u], h, bv[u]);
-      prod *= av[u];
-      vstore<CT>(P.h, ch.h_off(ch.t_of(pos + u)), h);
+      if constexpr (REDUCE) prod *= av[u];
+      else vstore<CT>(P.h, ch.h_off(ch.t_of(pos + u)), h);
     }
   }
   for (; pos < p1; ++pos) {
     const CT a = ch.mult(pos);
     h = fma(a, h, ch.b_at(ch.t_of(pos)));
-    prod *= a;
-    vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), h);
+    if constexpr (REDUCE) prod *= a;
+    else vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), h);
   }
+}
+
+template <typename CT>
+__global__ void __launch_bounds__(256) k_lscan_chunk_reduce(const LscanParams P) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P.B * P.nc * P.M) return;
+  const int64_t m = i % P.M, cj = (i / P.M) % P.nc, b = i / (P.M * P.nc);
+  Chain<CT> ch{P, b, m};
+  const int p0 = (int)cj * P.chunk;
+  const int p1 = p0 + P.chunk < (int)P.L ? p0 + P.chunk : (int)P.L;
+  CT h = 0, prod = 1;
+  chunk_walk<CT, true>(P, ch, p0, p1, h, prod);
   CT *ws = (CT *)P.ws;
   const int64_t stride = P.B * P.nc * P.M;
-  ws[i] = prod;           // P: product of the chunk's multipliers
-  ws[stride + i] = h;     // E: local end state
+  ws[i] = prod;        // P: product of the chunk's multipliers
+  ws[stride + i] = h;  // E: end state from zero
 }
 
 template <typename CT>
@@ -299,34 +314,15 @@ __global__ void __launch_bounds__(256) k_lscan_chunk_carry(const LscanParams P) 
 }
 
 template <typename CT>
-__global__ void __launch_bounds__(256) k_lscan_chunk_fix(const LscanParams P) {
+__global__ void __launch_bounds__(256) k_lscan_chunk_scan(const LscanParams P) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= P.B * P.nc * P.M) return;
   const int64_t m = i % P.M, cj = (i / P.M) % P.nc, b = i / (P.M * P.nc);
   Chain<CT> ch{P, b, m};
-  const CT hin = ((const CT *)P.ws)[2 * P.B * P.nc * P.M + i];
-  CT prod = 1;
   const int p0 = (int)cj * P.chunk;
   const int p1 = p0 + P.chunk < (int)P.L ? p0 + P.chunk : (int)P.L;
-  int pos = p0;
-  for (; pos + kSeqAhead <= p1; pos += kSeqAhead) {  // inputs read ahead of the updates
-    CT av[kSeqAhead], hv[kSeqAhead];
-#pragma unroll
-    for (int u = 0; u < kSeqAhead; ++u) {
-      av[u] = ch.mult(pos + u);
-      hv[u] = vload<CT>(P.h, ch.h_off(ch.t_of(pos + u)));
-    }
-#pragma unroll
-    for (int u = 0; u < kSeqAhead; ++u) {
-      prod *= av[u];
-      vstore<CT>(P.h, ch.h_off(ch.t_of(pos + u)), fma(prod, hin, hv[u]));
-    }
-  }
-  for (; pos < p1; ++pos) {
-    prod *= ch.mult(pos);
-    const int64_t o = ch.h_off(ch.t_of(pos));
-    vstore<CT>(P.h, o, fma(prod, hin, vload<CT>(P.h, o)));
-  }
+  CT h = ((const CT *)P.ws)[2 * P.B * P.nc * P.M + i], prod = 1;
+  chunk_walk<CT, false>(P, ch, p0, p1, h, prod);
 }
 
 // ------------------------------------------------------------------ adjoint epilogue
@@ -373,9 +369,9 @@ static hipError_t launch_lscan_t(const LscanParams &P, int algo, hipStream_t s) 
       break;
     default: {
       const int64_t n = P.B * P.nc * P.M;
-      hipLaunchKernelGGL((k_lscan_chunk_local<CT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, P);
+      hipLaunchKernelGGL((k_lscan_chunk_reduce<CT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, P);
       hipLaunchKernelGGL((k_lscan_chunk_carry<CT>), dim3((unsigned)((chains + 255) / 256)), dim3(256), 0, s, P);
-      hipLaunchKernelGGL((k_lscan_chunk_fix<CT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, P);
+      hipLaunchKernelGGL((k_lscan_chunk_scan<CT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, P);
     }
   }
   return hipGetLastError();
