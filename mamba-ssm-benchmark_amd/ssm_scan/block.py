@@ -27,7 +27,7 @@ import torch.nn.functional as F
 
 from .conv import causal_conv1d
 from .hip_scan import selective_scan_fn
-from .linear import linear
+from .linear import embedding, linear
 from .norm import rms_norm
 from .scan import selective_scan
 from .step import ssm_step
@@ -243,7 +243,7 @@ class MambaLM(nn.Module):
         return sum(Mamba.state_nbytes(s) for s in states)
 
     def forward(self, idx, states=None, pos=0):
-        x = self.embed(idx)
+        x = embedding(self.embed, idx)
         for i, block in enumerate(self.blocks):
             x = block(x, None if states is None else states[i], pos)
         return linear(self.head, self.norm_f(x))

@@ -1,5 +1,5 @@
 """The LM's Linear layers (in_proj, x_proj, out_proj, the tied head) with a split-K weight
-gradient.
+gradient, and its token embedding with a dense weight gradient.
 
 A Linear layer's weight gradient is dW = dY^T X, contracted over the tokens (B * L of them).
 At config 3 (8,192 tokens) the library GEMM for the layers' (out, in) shapes (1024, 256),
@@ -59,3 +59,37 @@ def linear(layer, x):
             and x.dtype == w.dtype and x.numel() // max(x.shape[-1], 1) >= MIN_TOKENS):
         return _SplitKLinear.apply(x, w, layer.bias)
     return layer(x)
+
+
+MAX_DENSE_VOCAB = 4096  # vocabularies up to this size take the one-hot product
+
+
+class _DenseGradEmbedding(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, idx, weight):
+        ctx.save_for_backward(idx)
+        ctx.vocab = weight.shape[0]
+        return F.embedding(idx, weight)
+
+    @staticmethod
+    def backward(ctx, dy):
+        (idx,) = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1])
+        classes = torch.arange(ctx.vocab, device=idx.device)
+        onehot = (idx.reshape(-1, 1) == classes).to(dy2.dtype)   # (tokens, vocab)
+        return None, weight_grad(onehot, dy2)
+
+
+def embedding(layer, idx):
+    """layer(idx) for a plain nn.Embedding.  While it is trained (grad mode, float32, vocabulary
+    <= MAX_DENSE_VOCAB) the weight gradient is onehot(idx)^T dY, a dense product (split-K over
+    the tokens): the same sums as torch's embedding backward, which sorts the indices with
+    sizes it reads back on the host -- this one makes no host reads, so a training step that
+    contains it can be captured in a HIP graph, and it runs in a fixed order."""
+    w = layer.weight
+    plain = (layer.padding_idx is None and layer.max_norm is None and not layer.scale_grad_by_freq
+             and not layer.sparse)
+    if (plain and torch.is_grad_enabled() and w.requires_grad and w.dtype == torch.float32
+            and w.shape[0] <= MAX_DENSE_VOCAB and not torch.is_autocast_enabled(w.device.type)):
+        return _DenseGradEmbedding.apply(idx, w)
+    return layer(idx)

@@ -97,3 +97,21 @@ def test_split_k_linear_gradients_match_nn_linear():
     ref.backward(gy)
     for a, b in zip(got, [ref.detach(), x.grad, lin.weight.grad, lin.bias.grad]):
         torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+
+
+def test_dense_embedding_gradient_on_the_cpu():
+    """ssm_scan.linear.embedding: torch's embedding forward, the weight gradient as a one-hot
+    product (split over the tokens); equal to torch's gradient to float32 rounding."""
+    from ssm_scan.linear import embedding
+    torch.manual_seed(0)
+    emb = torch.nn.Embedding(300, 24)
+    idx = torch.randint(0, 300, (3, 1000))
+    gy = torch.randn(3, 1000, 24)
+    y = embedding(emb, idx)
+    y.backward(gy)
+    got = emb.weight.grad.clone()
+    emb.weight.grad = None
+    emb(idx).backward(gy)
+    torch.testing.assert_close(got, emb.weight.grad, rtol=1e-5, atol=1e-5)
+    with torch.no_grad():                         # not training: torch's own embedding
+        assert torch.equal(embedding(emb, idx), emb(idx))
