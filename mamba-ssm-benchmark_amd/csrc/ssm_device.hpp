@@ -29,7 +29,6 @@ typedef _Float16 f16_t;
 __device__ __forceinline__ float to_f32(float v) { return v; }
 __device__ __forceinline__ float to_f32(bf16_t v) { return __uint_as_float(((uint32_t)v.bits) << 16); }
 __device__ __forceinline__ float to_f32(f16_t v) { return (float)v; }
-__device__ __forceinline__ double to_f64(double v) { return v; }
 
 template <typename T> struct Conv;
 template <> struct Conv<float> {

@@ -140,14 +140,6 @@ struct WaveTile {
     for (int i = 0; i < E; ++i) v[i] = buf_load<IT>(r, off[i] + toff);
   }
 
-  // element i of this lane is inside the (L, C) range
-  __device__ __forceinline__ static bool in_range(int i, bool tfast, int lane, int t0, int L, int c0, int C) {
-    const int e = lane + i * kWave;
-    int t, c;
-    tc_of<ROWS, COLS>(e, tfast, t, c);
-    return e < ROWS * COLS && t0 + t < L && c0 + c < C;
-  }
-
   template <int RP>
   __device__ __forceinline__ void store(CT (*S)[RP], bool tfast, int lane, int t0, int L, int c0, int C) const {
 #pragma unroll
