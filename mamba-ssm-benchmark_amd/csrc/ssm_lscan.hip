@@ -3,18 +3,20 @@
 // Replaces the four torch scans of models/scan.py with kernels that keep each algorithm's
 // structure (so `scan=` still selects an algorithm, as in the reference's SCANS registry,
 // models/scan.py:168-173):
-//   sequential     models/scan.py:70-76    one lane per (b, m) walks the sequence, reading 16
-//                                          steps ahead of the dependent updates.
+//   sequential     models/scan.py:70-76    one lane per (b, m) walks the sequence, reading up
+//                                          to 32 steps ahead of the dependent updates.
 //   hillis_steele  models/scan.py:87-98    a workgroup owns 64 neighbouring recurrences (lanes
 //                                          along m, so every global access is coalesced) and
 //                                          runs recursive doubling along time over tiles of 32
-//                                          steps in LDS; the state entering a tile is folded
+//                                          steps (offsets 1, 2 through LDS, 4..16 in
+//                                          registers); the state entering a tile is folded
 //                                          into its first element (as _fold_h0 does with h0,
 //                                          :79-84).
 //   blelloch       models/scan.py:101-135  the same 64-recurrence workgroups; up-sweep /
-//                                          down-sweep along time over tiles of 64 steps in LDS,
-//                                          giving exclusive (A, S) prefixes; h = a (A h_in + S)
-//                                          + b, the tile's last h carried to the next.
+//                                          down-sweep along time over tiles of 64 steps (a
+//                                          lane's 16-step block in registers, the block roots
+//                                          through LDS), giving exclusive (A, S) prefixes;
+//                                          h = a (A h_in + S) + b, the tile's last h carried.
 //   chunked        models/scan.py:142-165  three launches: per-chunk summaries from zero
 //                                          (P = prod a, E = local end; no states written), a
 //                                          scan over the summaries per (b, m) giving each
@@ -110,10 +112,14 @@ __global__ void __launch_bounds__(kSeqThreads) k_lscan_seq(const LscanParams P) 
 constexpr int kScanMC = 64, kScanRowLanes = 4;
 
 // ------------------------------------------------------------------ Hillis-Steele
+// Recursive doubling over a tile of T = 32 steps: at offset o every step k >= o composes with
+// step k - o of the previous pass (models/scan.py:87-98).  Row lane tr holds steps tr, tr + 4,
+// ..., so the offsets 4, 8, 16 pair registers of one lane and only the offsets 1 and 2 pair
+// different lanes, through LDS.
 template <typename CT>
 __global__ void __launch_bounds__(256) k_lscan_hs(const LscanParams P) {
-  constexpr int T = 32, RL = kScanRowLanes, R = T / RL;
-  __shared__ CT sA[2][T][kScanMC], sS[2][T][kScanMC];
+  constexpr int RL = kScanRowLanes, R = 8, T = RL * R;
+  __shared__ CT sA[2][T][kScanMC], sS[2][T][kScanMC], sLast[kScanMC];
   const int mi = threadIdx.x % kScanMC, tr = threadIdx.x / kScanMC;
   const int64_t m = (int64_t)blockIdx.x * kScanMC + mi;
   const bool mval = m < P.M;
@@ -133,48 +139,65 @@ __global__ void __launch_bounds__(256) k_lscan_hs(const LscanParams P) {
   };
   fetch(0);
   for (int base = 0; base < L; base += T) {
+    CT A[R], S[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int k = tr + RL * r;
-      const CT A = na[r];
-      CT S = nb[r];
-      if (k == 0) S = fma(A, carry, S);  // fold the incoming state into the first element
-      sA[0][k][mi] = A;
-      sS[0][k][mi] = S;
+      A[r] = na[r];
+      S[r] = nb[r];
     }
-    __syncthreads();
+    if (tr == 0) S[0] = fma(A[0], carry, S[0]);  // fold the incoming state into the first element
     if (base + T < L) fetch(base + T);
-    int cur = 0;
-    for (int off = 1; off < T; off *= 2) {  // after this step: compositions of 2*off elements
+    // offsets 1 and 2 (pass q: o = 2^q) through LDS: step k - o is in row lane tr - o, or in
+    // row lane tr - o + 4 one register lower
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int o = 1 << q;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        sA[q][tr + RL * r][mi] = A[r];
+        sS[q][tr + RL * r][mi] = S[r];
+      }
+      __syncthreads();
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int k = tr + RL * r;
-        CT A = sA[cur][k][mi], S = sS[cur][k][mi];
-        if (k >= off) {
-          S = fma(A, sS[cur][k - off][mi], S);
-          A = A * sA[cur][k - off][mi];
+        if (k >= o) {
+          S[r] = fma(A[r], sS[q][k - o][mi], S[r]);
+          A[r] = A[r] * sA[q][k - o][mi];
         }
-        sA[cur ^ 1][k][mi] = A;
-        sS[cur ^ 1][k][mi] = S;
       }
-      cur ^= 1;
-      __syncthreads();
+    }
+    // offsets 4, 8, 16 (j = o / 4 registers apart): descending r reads the previous pass's r - j
+#pragma unroll
+    for (int j = 1; j < R; j *= 2) {
+#pragma unroll
+      for (int r = R - 1; r >= j; --r) {
+        S[r] = fma(A[r], S[r - j], S[r]);
+        A[r] = A[r] * A[r - j];
+      }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int k = tr + RL * r, pos = base + k;
-      if (mval && pos < L) vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), sS[cur][k][mi]);
+      const int pos = base + tr + RL * r;
+      if (mval && pos < L) vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), S[r]);
     }
-    carry = sS[cur][T - 1][mi];
+    if (tr == RL - 1) sLast[mi] = S[R - 1];  // step T - 1: the state entering the next tile
     __syncthreads();
+    carry = sLast[mi];
   }
 }
 
 // ------------------------------------------------------------------ Blelloch
+// Up-sweep / down-sweep over a tile of T = 64 steps (models/scan.py:101-135).  Row lane tr
+// holds the 16 consecutive steps 16 tr .. 16 tr + 15, so the tree levels of span 2..16 are
+// register operations of one lane; the two top levels (span 32, 64) combine the four block
+// roots, which every lane of a column reads from LDS and sweeps itself (the same combines in
+// every lane, so the same bits).  Each tree node goes through the same combines as in a
+// tile-wide sweep.
 template <typename CT>
 __global__ void __launch_bounds__(256) k_lscan_bl(const LscanParams P) {
-  constexpr int T = 64, RL = kScanRowLanes, R = T / RL;
-  __shared__ CT sA[T][kScanMC], sS[T][kScanMC], sLast[kScanMC];
+  constexpr int RL = kScanRowLanes, R = 16, T = RL * R;
+  __shared__ CT sRA[RL][kScanMC], sRS[RL][kScanMC], sLast[kScanMC];
   const int mi = threadIdx.x % kScanMC, tr = threadIdx.x / kScanMC;
   const int64_t m = (int64_t)blockIdx.x * kScanMC + mi;
   const bool mval = m < P.M;
@@ -186,7 +209,7 @@ __global__ void __launch_bounds__(256) k_lscan_bl(const LscanParams P) {
   auto fetch = [&](int base) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int pos = base + tr + RL * r;
+      const int pos = base + tr * R + r;
       const bool valid = mval && pos < L;
       na[r] = valid ? ch.mult(pos) : (CT)1;  // padding with the identity (1, 0)
       nb[r] = valid ? ch.b_at(ch.t_of(pos)) : (CT)0;
@@ -194,54 +217,86 @@ __global__ void __launch_bounds__(256) k_lscan_bl(const LscanParams P) {
   };
   fetch(0);
   for (int base = 0; base < L; base += T) {
-    CT a_own[R], b_own[R];
+    CT a_own[R], b_own[R], A[R], S[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int k = tr + RL * r;
       a_own[r] = na[r];
       b_own[r] = nb[r];
-      sA[k][mi] = a_own[r];
-      sS[k][mi] = b_own[r];
+      A[r] = na[r];
+      S[r] = nb[r];
     }
-    __syncthreads();
     if (base + T < L) fetch(base + T);
-    // up-sweep: right <- right o left, over nodes k = (j + 1) s - 1
-    for (int s = 2; s <= T; s *= 2) {
-      for (int j = tr; j < T / s; j += RL) {
-        const int k = (j + 1) * s - 1, l = k - s / 2;
-        sS[k][mi] = fma(sA[k][mi], sS[l][mi], sS[k][mi]);
-        sA[k][mi] = sA[k][mi] * sA[l][mi];
+    // up-sweep inside the lane's block: right <- right o left at nodes (j + 1) s - 1
+#pragma unroll
+    for (int sp = 2; sp <= R; sp *= 2) {
+#pragma unroll
+      for (int k = sp - 1; k < R; k += sp) {
+        const int l = k - sp / 2;
+        S[k] = fma(A[k], S[l], S[k]);
+        A[k] = A[k] * A[l];
       }
-      __syncthreads();
     }
-    if (tr == 0) {
-      sA[T - 1][mi] = 1;
-      sS[T - 1][mi] = 0;
-    }
+    sRA[tr][mi] = A[R - 1];
+    sRS[tr][mi] = S[R - 1];
     __syncthreads();
-    // down-sweep: left <- right; right <- left_old o right
-    for (int s = T; s >= 2; s /= 2) {
-      for (int j = tr; j < T / s; j += RL) {
-        const int k = (j + 1) * s - 1, l = k - s / 2;
-        const CT tA = sA[l][mi], tS = sS[l][mi];
-        sA[l][mi] = sA[k][mi];
-        sS[l][mi] = sS[k][mi];
-        sS[k][mi] = fma(sS[k][mi], tA, tS);
-        sA[k][mi] = sA[k][mi] * tA;
-      }
-      __syncthreads();
+    // the two top levels over the block roots (nodes 1, 3 at span 2; node 3 at span 4), the
+    // root set to the identity, then their down-sweep: each root becomes the composition of
+    // the blocks before it
+    CT rA[RL], rS[RL];
+#pragma unroll
+    for (int q = 0; q < RL; ++q) {
+      rA[q] = sRA[q][mi];
+      rS[q] = sRS[q][mi];
     }
-    // exclusive prefixes: the state entering element k is A_k h_in + S_k
+#pragma unroll
+    for (int sp = 2; sp <= RL; sp *= 2) {
+#pragma unroll
+      for (int k = sp - 1; k < RL; k += sp) {
+        const int l = k - sp / 2;
+        rS[k] = fma(rA[k], rS[l], rS[k]);
+        rA[k] = rA[k] * rA[l];
+      }
+    }
+    rA[RL - 1] = 1;
+    rS[RL - 1] = 0;
+#pragma unroll
+    for (int sp = RL; sp >= 2; sp /= 2) {
+#pragma unroll
+      for (int k = sp - 1; k < RL; k += sp) {
+        const int l = k - sp / 2;
+        const CT tA = rA[l], tS = rS[l];
+        rA[l] = rA[k];
+        rS[l] = rS[k];
+        rS[k] = fma(rS[k], tA, tS);
+        rA[k] = rA[k] * tA;
+      }
+    }
+    A[R - 1] = rA[tr];
+    S[R - 1] = rS[tr];
+    // down-sweep inside the block: left <- right; right <- left_old o right
+#pragma unroll
+    for (int sp = R; sp >= 2; sp /= 2) {
+#pragma unroll
+      for (int k = sp - 1; k < R; k += sp) {
+        const int l = k - sp / 2;
+        const CT tA = A[l], tS = S[l];
+        A[l] = A[k];
+        S[l] = S[k];
+        S[k] = fma(S[k], tA, tS);
+        A[k] = A[k] * tA;
+      }
+    }
+    // exclusive prefixes: the state entering step k is A_k h_in + S_k
+    CT h = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int k = tr + RL * r, pos = base + k;
-      const CT h = fma(a_own[r], fma(sA[k][mi], carry, sS[k][mi]), b_own[r]);
+      const int pos = base + tr * R + r;
+      h = fma(a_own[r], fma(A[r], carry, S[r]), b_own[r]);
       if (mval && pos < L) vstore<CT>(P.h, ch.h_off(ch.t_of(pos)), h);
-      if (k == T - 1) sLast[mi] = h;  // the tile's last state, for every lane of the column
     }
+    if (tr == RL - 1) sLast[mi] = h;  // step T - 1: the state entering the next tile
     __syncthreads();
     carry = sLast[mi];
-    __syncthreads();
   }
 }
 
