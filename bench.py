@@ -241,14 +241,8 @@ def bench_fwd(args, dev, B, L, dtype, workload):
         with torch.no_grad():
             return ssm_scan.selective_scan_fn(*ins, return_last_state=True, segments=args.segments)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    eager_ms, graph_ms, graph_ok = time_steps(step, args)
+    ms = min(eager_ms, graph_ms) if graph_ok else eager_ms
     with ssm_scan.KernelTimer() as timer:
         for _ in range(args.steps):
             step()

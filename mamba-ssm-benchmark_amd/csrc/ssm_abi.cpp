@@ -176,7 +176,7 @@ int64_t ssm_fwd_saved_bytes(const ssm_fwd_args *a) {
 // wavefronts leave the GPU short of work (fewer than kSegEnough); then enough segments for
 // about kSegTarget wavefronts, each segment at least kSegMinChunks chunks long.  A positive
 // `requested` overrides the choice (clamped to the valid range).
-constexpr int64_t kSegEnough = 2048, kSegTarget = 4096, kSegMinChunks = 16;
+constexpr int64_t kSegEnough = 2048, kSegTarget = 4096, kSegMinChunks = 4;
 
 struct SegPlan {
   int nseg, seg_chunks;
