@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 2
+#define SSM_ABI_VERSION 3
 
 enum { SSM_OK = 0, SSM_EINVAL = 1, SSM_EKEY = 2, SSM_ESPACE = 3, SSM_EHIP = 4 };
 
@@ -93,6 +93,10 @@ typedef struct ssm_fwd_args {
    * dstate <= 16 and a 16- or 32-bit dtype. */
   ssm_tensor delta_proj;
   int64_t delta_rank;
+  /* A_is_log = 1: `A` holds log(-A), the A_log parameter of models/mamba.py:61,81 (A =
+   * -exp(A_log), :81), and the kernels form A themselves; 0: `A` is A. */
+  int32_t A_is_log;
+  int32_t reserved1;
 } ssm_fwd_args;
 
 /* ------------------------------------------------------------------ fused backward
@@ -125,6 +129,8 @@ typedef struct ssm_bwd_args {
    * (B,L,R) input and of delta_proj. */
   ssm_tensor delta_proj;
   int64_t delta_rank;
+  int32_t A_is_log;        /* as in ssm_fwd_args; dA is then the gradient of A_log */
+  int32_t reserved1;
 } ssm_bwd_args;
 
 /* ------------------------------------------------------------------ decode step

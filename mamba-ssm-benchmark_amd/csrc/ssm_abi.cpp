@@ -214,6 +214,7 @@ static void fill_fwd(FwdParams &p, const ssm_fwd_args *a, const FwdLayout &f) {
   p.x = kv(a->x); p.dt = kv(a->delta); p.A = kv(a->A); p.Bm = kv(a->Bm); p.Cm = kv(a->Cm);
   p.Dsk = kv(a->Dskip); p.z = kv(a->z); p.bias = kv(a->delta_bias); p.h0 = kv(a->h0);
   p.out = kv(a->out); p.last = kv(a->last);
+  p.a_log = a->A_is_log != 0;
   if (a->delta_rank > 0) {  // the (B, L, D) delta view aliases x: its tiles are never used
     p.lowrank = (int)a->delta_rank;
     p.dtl = kv(a->delta); p.dtw = kv(a->delta_proj); p.dt = kv(a->x);
@@ -296,6 +297,7 @@ int ssm_bwd(const ssm_bwd_args *a, void *stream) {
     fa.Dskip = a->Dskip; fa.z = a->z; fa.delta_bias = a->delta_bias;
     fa.delta_softplus = a->delta_softplus; fa.h0 = a->h0;
     fa.delta_proj = a->delta_proj; fa.delta_rank = a->delta_rank;
+    fa.A_is_log = a->A_is_log;
     fa.out = a->x;  // placeholder with x's layout, never written (write_out = 0)
     FwdParams fp;
     fill_fwd(fp, &fa, w.f);
@@ -320,6 +322,7 @@ int ssm_bwd(const ssm_bwd_args *a, void *stream) {
   p.dout = kv(a->dout); p.dlast = kv(a->dlast); p.dx = kv(a->dx); p.ddt = kv(a->ddelta);
   p.dz = kv(a->dz); p.dh0 = kv(a->dh0);
   p.ckpt = ckpt; p.ypre = ypre;
+  p.a_log = a->A_is_log != 0;
   if (a->delta_rank > 0) {  // as in the forward: the (B, L, D) delta view aliases x
     p.lowrank = (int)a->delta_rank;
     p.dtl = kv(a->delta); p.dtw = kv(a->delta_proj); p.dt = kv(a->x);
@@ -334,6 +337,7 @@ int ssm_bwd(const ssm_bwd_args *a, void *stream) {
   fin.B = a->batch; fin.L = a->seqlen; fin.D = a->dim; fin.N = a->dstate;
   fin.ntiles = w.ntiles; fin.np = w.f.np;
   fin.has_D = has(a->Dskip); fin.has_bias = has(a->delta_bias);
+  fin.a_log = a->A_is_log != 0; fin.A = kv(a->A);
   fin.ws_dB = p.ws_dB; fin.ws_dC = p.ws_dC; fin.ws_dA = p.ws_dA; fin.ws_dD = p.ws_dD; fin.ws_db = p.ws_db;
   fin.dB = kv(a->dBm); fin.dC = kv(a->dCm); fin.dA = kv(a->dA); fin.dD = kv(a->dD); fin.dbias = kv(a->ddelta_bias);
   e = launch_bwd_finalize(fin, a->dtype, s);

@@ -74,7 +74,10 @@ k_bwd(const BwdParams p) {
   const int L = (int)p.L, D = (int)p.D, N = (int)p.N;
 
   CT Av = (CT)-1;
-  if (dval && nval) Av = vload<CT>(p.A, d * p.A.s0 + n * p.A.s1);
+  if (dval && nval) {
+    Av = vload<CT>(p.A, d * p.A.s0 + n * p.A.s1);
+    if (p.a_log) Av = -exp(Av);  // models/mamba.py:81
+  }
   const AConst<CT> ac = make_aconst(Av);
   // The adjoint state is carried in float64: dh_t = a_{t+1} dh_{t+1} + dy_t C_t is a long,
   // slowly decaying accumulation (a -> 1 for small delta) and its float32 rounding dominates the
@@ -493,7 +496,8 @@ __global__ void __launch_bounds__(256) k_bwd_finalize(const FinParams p) {
   const int64_t j = i - nBC;
   if (j < nDN) {
     const int64_t d = j / p.N, nn = j % p.N;
-    const CT s = fin_sum((const CT *)p.ws_dA + d * p.np + nn, p.D * p.np, p.B);
+    CT s = fin_sum((const CT *)p.ws_dA + d * p.np + nn, p.D * p.np, p.B);
+    if (p.a_log) s *= -exp(vload<CT>(p.A, d * p.A.s0 + nn * p.A.s1));  // dA_log = dA * A
     vstore<CT>(p.dA, d * p.dA.s0 + nn * p.dA.s1, s);
     return;
   }

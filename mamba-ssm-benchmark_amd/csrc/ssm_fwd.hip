@@ -68,7 +68,10 @@ k_fwd(const FwdParams p) {
   const int L = (int)p.L, D = (int)p.D, N = (int)p.N;
 
   CT Av = (CT)-1;
-  if (dval && nval) Av = vload<CT>(p.A, d * p.A.s0 + n * p.A.s1);
+  if (dval && nval) {
+    Av = vload<CT>(p.A, d * p.A.s0 + n * p.A.s1);
+    if (p.a_log) Av = -exp(Av);  // models/mamba.py:81
+  }
   const AConst<CT> ac = make_aconst(Av);
   CT h = 0, prod = 1;
   const int64_t sidx = ((b * p.nseg + seg) * p.D + d) * NP + n;  // (B, nseg, D, NP) summaries

@@ -75,6 +75,7 @@ struct FwdParams {
   // aliases x (never read in the uniform layout) so that every tile load stays in bounds.
   int lowrank;
   KView dtl, dtw;
+  int a_log;   // A holds A_log: the kernel uses -exp(A_log)
   void *ckpt;  // (B, nchunks, D, NP) state type: state at the end of each chunk
   void *ypre;  // y + D x before the gate (iff gate and saving), state type; laid out
                // (B, L, D) when x is D-contiguous, else (B, D, L) -- see ypre_index()
@@ -95,6 +96,7 @@ struct BwdParams {
   KView x, dt, A, Bm, Cm, Dsk, z, bias, h0, dout, dlast, dx, ddt, dz, dh0;
   int lowrank;  // as in FwdParams
   KView dtl, dtw;
+  int a_log;    // as in FwdParams
   const void *ckpt;
   const void *ypre;
   void *ws_dB, *ws_dC;  // (B, ntiles, L, NP) partial sums over the tile's channels
@@ -106,8 +108,9 @@ struct FinParams {
   int64_t B, L, D, N;
   int ntiles, np;
   int has_D, has_bias;
+  int a_log;  // A holds A_log: dA is written as the gradient of A_log, dA * A
   const void *ws_dB, *ws_dC, *ws_dA, *ws_dD, *ws_db;
-  KView dB, dC, dA, dD, dbias;
+  KView A, dB, dC, dA, dD, dbias;
 };
 
 struct StepParams {

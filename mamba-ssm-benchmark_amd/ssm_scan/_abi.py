@@ -11,7 +11,7 @@ import os
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssmscan.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK, EINVAL, EKEY, ESPACE, EHIP = 0, 1, 2, 3, 4
 ZOH, EULER, BILINEAR = 0, 1, 2
@@ -36,7 +36,8 @@ class FwdArgs(ctypes.Structure):
                 ("delta_softplus", c_i32), ("segments", c_i32),
                 ("h0", Tensor), ("out", Tensor), ("last", Tensor),
                 ("saved", c_vp), ("workspace", c_vp), ("workspace_bytes", c_i64),
-                ("delta_proj", Tensor), ("delta_rank", c_i64)]
+                ("delta_proj", Tensor), ("delta_rank", c_i64),
+                ("A_is_log", c_i32), ("reserved1", c_i32)]
 
 
 class BwdArgs(ctypes.Structure):
@@ -49,7 +50,8 @@ class BwdArgs(ctypes.Structure):
                 ("dx", Tensor), ("ddelta", Tensor), ("dA", Tensor), ("dBm", Tensor), ("dCm", Tensor),
                 ("dD", Tensor), ("dz", Tensor), ("ddelta_bias", Tensor), ("dh0", Tensor),
                 ("workspace", c_vp), ("workspace_bytes", c_i64),
-                ("delta_proj", Tensor), ("delta_rank", c_i64)]
+                ("delta_proj", Tensor), ("delta_rank", c_i64),
+                ("A_is_log", c_i32), ("reserved1", c_i32)]
 
 
 class StepArgs(ctypes.Structure):

@@ -78,10 +78,11 @@ class Mamba(nn.Module):
         self.out_proj = nn.Linear(d_inner, d_model, bias=False)
         self.out_proj._residual_out = True
 
-    def ssm_inputs(self, x, lowrank=False):
+    def ssm_inputs(self, x, lowrank=False, a_log=False):
         """x (B, L, d_inner) -> raw delta (pre bias/softplus), delta bias, A, B, C (views).
         With lowrank (selective only) the raw delta is the pair (dt (B, L, dt_rank), dt_proj
-        weight): the fused kernels apply the projection while they stage delta."""
+        weight): the fused kernels apply the projection while they stage delta.  With a_log
+        the A returned is A_log itself (the fused kernels form -exp(A_log))."""
         Bsz, L, _ = x.shape
         ct = torch.promote_types(x.dtype, torch.float32)
         if self.selective:
@@ -94,7 +95,7 @@ class Mamba(nn.Module):
             bias = self.dt_bias
             Bm = self.B.to(x.dtype).expand(Bsz, L, -1)
             Cm = self.C.to(x.dtype).expand(Bsz, L, -1)
-        A = -torch.exp(self.A_log.to(ct))
+        A = self.A_log.to(ct) if a_log else -torch.exp(self.A_log.to(ct))
         if self.a_mode == "scalar":
             A = A.expand(-1, self.d_state)
         return delta, bias.to(ct), A, Bm, Cm
@@ -134,7 +135,7 @@ class Mamba(nn.Module):
         x = self._conv(x, state)
         decode = state is not None and L == 1
         fused = not decode and self.scan in ("auto", "triton")
-        delta, bias, A, Bm, Cm = self.ssm_inputs(x, lowrank=fused and self.selective)
+        delta, bias, A, Bm, Cm = self.ssm_inputs(x, lowrank=fused and self.selective, a_log=fused)
         if return_delta or getattr(self, "record_delta", False):   # models/mamba.py:109-110
             raw = F.linear(*delta) if isinstance(delta, tuple) else delta
             full_delta = F.softplus(raw.to(bias.dtype) + bias)
@@ -148,7 +149,7 @@ class Mamba(nn.Module):
             dt, proj = delta if isinstance(delta, tuple) else (delta, None)
             y, last = selective_scan_fn(x, dt, A, Bm, Cm, D=self.D, z=z, delta_bias=bias, delta_softplus=True,
                                         h0=h0, method=self.discretization, return_last_state=True,
-                                        delta_proj=proj)
+                                        delta_proj=proj, A_is_log=True)
         else:
             y, last = selective_scan(x, F.softplus(delta.to(bias.dtype) + bias), A, Bm, Cm, h0=h0,
                                      method=self.discretization, scan=self.scan, d_block=self.d_block,

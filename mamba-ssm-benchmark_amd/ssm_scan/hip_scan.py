@@ -103,7 +103,7 @@ class FusedSelectiveScanFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, delta, A, Bm, Cm, D, z, delta_bias, h0, method, delta_softplus, segments=0,
-                delta_proj=None):
+                delta_proj=None, A_is_log=False):
         io, ct = _dtypes(x, (delta, Bm, Cm, z))
         xs, ds, Bs, Cs, zs = (_cast_keep(t, io) for t in (x, delta, Bm, Cm, z))
         As, Dv, bv, h0v, Wv = (_cast_keep(t, ct) for t in (A, D, delta_bias, h0, delta_proj))
@@ -118,6 +118,7 @@ class FusedSelectiveScanFn(torch.autograd.Function):
         args.segments = int(segments or 0)
         if Wv is not None:
             args.delta_proj, args.delta_rank = _abi.view(Wv), Wv.shape[1]
+        args.A_is_log = 1 if A_is_log else 0
         lib = _abi.lib()
         wbytes = lib.ssm_fwd_workspace_bytes(ctypes.byref(args))
         if wbytes < 0:
@@ -139,7 +140,7 @@ class FusedSelectiveScanFn(torch.autograd.Function):
         if need_bwd:
             ctx.save_for_backward(xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, Wv, saved)
         ctx.set_materialize_grads(False)   # an unused `last` passes dlast = None (no zero fill)
-        ctx.method, ctx.softplus, ctx.io, ctx.ct = method, delta_softplus, io, ct
+        ctx.method, ctx.softplus, ctx.io, ctx.ct, ctx.a_log = method, delta_softplus, io, ct, A_is_log
         ctx.in_dtypes = [None if t is None else t.dtype for t in (x, delta, A, Bm, Cm, D, z, delta_bias, h0)]
         ctx.proj_dtype = None if delta_proj is None else delta_proj.dtype
         if out.dtype != x.dtype:
@@ -175,6 +176,7 @@ class FusedSelectiveScanFn(torch.autograd.Function):
         args.dz, args.ddelta_bias, args.dh0 = _abi.view(dz), _abi.view(db), _abi.view(dh0)
         if Wv is not None:
             args.delta_proj, args.delta_rank = _abi.view(Wv), Wv.shape[1]
+        args.A_is_log = 1 if ctx.a_log else 0
         lib = _abi.lib()
         nbytes = lib.ssm_bwd_workspace_bytes(ctypes.byref(args))
         if nbytes < 0:
@@ -195,14 +197,15 @@ class FusedSelectiveScanFn(torch.autograd.Function):
         out = []
         for g, dt in zip(grads, ctx.in_dtypes):
             out.append(None if g is None or dt is None else _cast_keep(g, dt))
-        return (*out, None, None, None, None if dW is None else _cast_keep(dW, ctx.proj_dtype))
+        return (*out, None, None, None, None if dW is None else _cast_keep(dW, ctx.proj_dtype), None)
 
 
 LOWRANK_MAX = 16  # rank of a delta projection the kernels apply while staging delta
 
 
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                      h0=None, method="zoh", return_last_state=False, segments=None, delta_proj=None):
+                      h0=None, method="zoh", return_last_state=False, segments=None, delta_proj=None,
+                      A_is_log=False):
     """out = (scan(u, delta', A, B, C) + D u) * silu(z), delta' = softplus(delta + bias).
 
     Logical layouts as the reference: u, delta, z (B, L, D); A (D, N); B, C (B, L, N);
@@ -212,7 +215,9 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_
     ``delta_proj`` (D, R): ``delta`` is then the low-rank (B, L, R) input and the scan uses
     delta @ delta_proj^T -- the dt_proj GEMM of models/mamba.py:76, done by the kernels while
     they stage delta for R <= 16 and dstate <= 16 with 16/32-bit inputs (no (B, L, D) delta in
-    memory), by a torch GEMM otherwise.  Gradients flow to both."""
+    memory), by a torch GEMM otherwise.  Gradients flow to both.
+    ``A_is_log``: ``A`` holds A_log (the parameter of models/mamba.py:61,81) and the kernels
+    use A = -exp(A_log); its gradient is that of A_log."""
     if method not in METHODS:
         raise ValueError(f"unknown discretization {method!r}")
     _require_gpu(u, delta, A, B, C, D, z, delta_bias, h0, delta_proj)
@@ -221,7 +226,7 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_
                                    or torch.promote_types(u.dtype, torch.float32) == torch.float64):
         delta, delta_proj = torch.nn.functional.linear(delta, delta_proj), None
     out, last = FusedSelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, h0, METHODS[method],
-                                           bool(delta_softplus), segments or 0, delta_proj)
+                                           bool(delta_softplus), segments or 0, delta_proj, bool(A_is_log))
     return (out, last) if return_last_state else out
 
 

@@ -241,3 +241,33 @@ def test_cpu_tensors_are_rejected():
     x, delta, A, Bm, Cm, _ = triton_test_inputs(1, 4, 8, 16, False)
     with pytest.raises(RuntimeError, match="GPU"):
         ssm_scan.selective_scan_hip(x, delta, A, Bm, Cm)
+
+
+@pytest.mark.parametrize("lowrank,L,scalar", [(False, 77, False), (True, 600, False), (True, 64, True)])
+def test_A_log_input_equals_A_input(dev, lowrank, L, scalar):
+    """A_is_log: the kernels form A = -exp(A_log) (models/mamba.py:81) and return the gradient of
+    A_log; equal to passing -exp(A_log) with torch and chaining its gradient, to float32
+    rounding (one exp evaluated by the kernel, one by torch).  Covers the low-rank delta, time
+    segments (B 1, L 600) and a stride-0 expanded A_log (the scalar-decay mode)."""
+    B, D, N, Rk = (1, 64, 16, 8) if L == 600 else (2, 40, 16, 8)
+    g = torch.Generator().manual_seed(L)
+    x = torch.randn(B, L, D, generator=g).to(dev)
+    dt = (torch.randn(B, L, Rk if lowrank else D, generator=g) * 0.5).to(dev)
+    W = (torch.randn(D, Rk, generator=g) * 0.3).to(dev) if lowrank else None
+    A_log = torch.log(torch.rand(D, 1 if scalar else N, generator=g) * 4 + 0.5).to(dev)
+    Bm, Cm = torch.randn(B, L, N, generator=g).to(dev), torch.randn(B, L, N, generator=g).to(dev)
+    Dv, z = torch.randn(D, generator=g).to(dev), torch.randn(B, L, D, generator=g).to(dev)
+    bias = (torch.rand(D, generator=g) - 3.0).to(dev)
+    dout = torch.randn(B, L, D, generator=g).to(dev)
+    res = []
+    for as_log in (True, False):
+        leaf = A_log.clone().requires_grad_()
+        A = leaf if as_log else -torch.exp(leaf)
+        if scalar:
+            A = A.expand(-1, N)
+        out = ssm_scan.selective_scan_fn(x, dt, A, Bm, Cm, D=Dv, z=z, delta_bias=bias, delta_softplus=True,
+                                         delta_proj=W, A_is_log=as_log)
+        (out * dout).sum().backward()
+        res.append((out.detach(), leaf.grad))
+    torch.testing.assert_close(res[0][0], res[1][0], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(res[0][1], res[1][1], rtol=1e-4, atol=1e-5)
