@@ -237,9 +237,11 @@ def bench_fwd(args, dev, B, L, dtype, workload):
     D, N = 512, 16
     t = baseline_inputs(B, L, D, N, dtype=dtype)
     ins = [t[k].to(dev) for k in ("u", "delta", "A", "Bm", "Cm")]
+    Dv = t["D"].to(dev)                      # D_skip = ones(D), no gate (BASELINE configs 0 and 2)
+
     def step():
         with torch.no_grad():
-            return ssm_scan.selective_scan_fn(*ins, return_last_state=True, segments=args.segments)
+            return ssm_scan.selective_scan_fn(*ins, D=Dv, return_last_state=True, segments=args.segments)
 
     eager_ms, graph_ms, graph_ok = time_steps(step, args)
     ms = min(eager_ms, graph_ms) if graph_ok else eager_ms
@@ -248,7 +250,7 @@ def bench_fwd(args, dev, B, L, dtype, workload):
             step()
     fwd_ms = statistics.mean(timer.times_ms()["ssm_fwd"])
     s = torch.tensor([], dtype=dtype).element_size()
-    fb, _ = alg_bytes(B, L, D, N, s=s, gate=False, skip=False)
+    fb, _ = alg_bytes(B, L, D, N, s=s, gate=False)
     achieved = fb / (fwd_ms * 1e-3) / 1e9
     rec = {"metric": f"selective-scan fwd Mtok/s, {workload}", "value": B * L / (ms * 1e-3) / 1e6,
             "unit": "Mtok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
