@@ -327,8 +327,10 @@ int ssm_bwd(const ssm_bwd_args *a, void *stream) {
     p.lowrank = (int)a->delta_rank;
     p.dtl = kv(a->delta); p.dtw = kv(a->delta_proj); p.dt = kv(a->x);
   }
-  const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->dout, &a->dx, &a->ddelta, &a->dz};
-  p.uniform = uniform_layout(bld, 6, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype, a->z);
+  // dz keeps its own strides (like z): it only needs 32-bit row offsets
+  const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->dout, &a->dx, &a->ddelta};
+  p.uniform = uniform_layout(bld, 5, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype, a->z) &&
+              (!has(a->dz) || row_fits(a->dz, a->seqlen, a->dim, a->dtype == SSM_F64 ? 8 : a->dtype == SSM_F32 ? 4 : 2));
   p.ws_dB = ws + w.dB; p.ws_dC = ws + w.dC; p.ws_dA = ws + w.dA; p.ws_dD = ws + w.dD; p.ws_db = ws + w.db;
   hipError_t e = launch_bwd(p, a->dtype, a->method, w.f.np, s);
   if (e != hipSuccess) return hip_fail(e, "ssm_bwd launch");

@@ -100,7 +100,8 @@ k_bwd(const BwdParams p) {
   CT dD_acc = 0, db_acc = 0;  // lanes < CW: channel dw + lane
 
   const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = p.z;  // z keeps its own strides
-  const KView vg = with_layout<UL>(p.dout, p.x), vdz = with_layout<UL>(p.dz, p.x);
+  const KView vg = with_layout<UL>(p.dout, p.x);
+  const KView vdz = p.dz;  // its own strides (e.g. the gate half of an in_proj-output gradient)
   const KView vdx = with_layout<UL>(p.dx, p.x), vddt = with_layout<UL>(p.ddt, p.x);
   const KView vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
   const bool xt = vx.s1 == 1, dtt = vdt.s1 == 1, bt = vB.s1 == 1, ctt = vC.s1 == 1;

@@ -28,6 +28,7 @@ import torch.nn.functional as F
 from .conv import causal_conv1d
 from .hip_scan import selective_scan_fn
 from .linear import embedding, linear
+from .mixer import mixer, mixer_applies
 from .norm import rms_norm
 from .scan import selective_scan
 from .step import ssm_step
@@ -131,6 +132,8 @@ class Mamba(nn.Module):
 
     def forward(self, u, state=None, pos=0, return_delta=False):
         Bsz, L, _ = u.shape
+        if mixer_applies(self, u, state, return_delta):   # one autograd node in_proj -> out_proj
+            return linear(self.out_proj, mixer(self, linear(self.in_proj, u)))
         x, z = linear(self.in_proj, u).chunk(2, dim=-1)
         x = self._conv(x, state)
         decode = state is not None and L == 1

@@ -36,15 +36,42 @@ def _launch(name, fn, args, dev):
     _abi.check(rc, name)
 
 
+def conv_forward(x, w2, bias, activation):
+    """One ssm_conv_fwd launch: (B, L, D) out for x, weight (D, W) and bias in the state type."""
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    args = _args(x, w2, bias, activation)
+    args.out = _abi.view(out)
+    _launch("ssm_conv_fwd", _abi.lib().ssm_conv_fwd, args, x.device)
+    return out
+
+
+def conv_backward(x, w2, bias, dout, activation, dx=None):
+    """One ssm_conv_bwd launch: (dx, dweight, dbias).  dx may be given (a (B, L, D) view into a
+    caller's buffer); it is allocated otherwise."""
+    dev = x.device
+    dout = dout.to(x.dtype)
+    dx = torch.empty(x.shape, dtype=x.dtype, device=dev) if dx is None else dx
+    dw = torch.empty_like(w2)
+    db = None if bias is None else torch.empty_like(bias)
+    args = _args(x, w2, bias, activation)
+    args.dout, args.dx = _abi.view(dout), _abi.view(dx)
+    args.dweight, args.dbias = _abi.view(dw), _abi.view(db)
+    lib = _abi.lib()
+    nbytes = lib.ssm_conv_workspace_bytes(ctypes.byref(args))
+    if nbytes < 0:
+        _abi.check(lib.ssm_conv_check(ctypes.byref(args)), "ssm_conv_bwd")
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
+    _launch("ssm_conv_bwd", lib.ssm_conv_bwd, args, dev)
+    return dx, dw, db
+
+
 class CausalConv1dFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, bias, activation):
         ct = torch.promote_types(x.dtype, torch.float32)
         w2, bv = weight.to(ct), None if bias is None else bias.to(ct)
-        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-        args = _args(x, w2, bv, activation)
-        args.out = _abi.view(out)
-        _launch("ssm_conv_fwd", _abi.lib().ssm_conv_fwd, args, x.device)
+        out = conv_forward(x, w2, bv, activation)
         ctx.save_for_backward(x, w2, bv)
         ctx.activation = activation
         ctx.wdtype = weight.dtype
@@ -54,21 +81,7 @@ class CausalConv1dFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         x, w2, bv = ctx.saved_tensors
-        dev = x.device
-        dout = dout.to(x.dtype)
-        dx = torch.empty(x.shape, dtype=x.dtype, device=dev)
-        dw = torch.empty_like(w2)
-        db = None if bv is None else torch.empty_like(bv)
-        args = _args(x, w2, bv, ctx.activation)
-        args.dout, args.dx = _abi.view(dout), _abi.view(dx)
-        args.dweight, args.dbias = _abi.view(dw), _abi.view(db)
-        lib = _abi.lib()
-        nbytes = lib.ssm_conv_workspace_bytes(ctypes.byref(args))
-        if nbytes < 0:
-            _abi.check(lib.ssm_conv_check(ctypes.byref(args)), "ssm_conv_bwd")
-        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-        args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
-        _launch("ssm_conv_bwd", lib.ssm_conv_bwd, args, dev)
+        dx, dw, db = conv_backward(x, w2, bv, dout, ctx.activation)
         return dx, dw.to(ctx.wdtype), None if db is None else db.to(ctx.bdtype), None
 
 

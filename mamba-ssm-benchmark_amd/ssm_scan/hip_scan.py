@@ -19,6 +19,7 @@ import ctypes
 import torch
 
 from . import _abi
+from .linear import weight_grad
 from .profiling import timed_launch
 
 ZOH, EULER, BILINEAR = 0, 1, 2
@@ -98,49 +99,107 @@ def _check_shapes(x, delta, A, Bm, Cm, D, z, bias, h0, delta_proj=None):
             raise ValueError(f"{name} must have shape {shp}, got {tuple(t.shape)}")
 
 
+def scan_forward(x, delta, A, Bm, Cm, D, z, delta_bias, h0, method, delta_softplus, segments=0,
+                 delta_proj=None, A_is_log=False, need_saved=True):
+    """One ssm_fwd launch.  Returns (out in the io dtype, last, state) where `state` holds what
+    scan_backward needs: the tensors as the kernels read them, the saved chunk states and the
+    launch settings."""
+    io, ct = _dtypes(x, (delta, Bm, Cm, z))
+    xs, ds, Bs, Cs, zs = (_cast_keep(t, io) for t in (x, delta, Bm, Cm, z))
+    As, Dv, bv, h0v, Wv = (_cast_keep(t, ct) for t in (A, D, delta_bias, h0, delta_proj))
+    Bsz, L, Dm = x.shape
+    N = A.shape[1]
+    dev = x.device
+    out = empty_like_layout(xs, io)
+    last = torch.empty((Bsz, Dm, N), dtype=ct, device=dev)
+    args = _abi.FwdArgs()
+    _fill_common(args, xs, ds, As, Bs, Cs, Dv, zs, bv, delta_softplus, h0v, method, io)
+    args.out, args.last = _abi.view(out), _abi.view(last)
+    args.segments = int(segments or 0)
+    if Wv is not None:
+        args.delta_proj, args.delta_rank = _abi.view(Wv), Wv.shape[1]
+    args.A_is_log = 1 if A_is_log else 0
+    lib = _abi.lib()
+    wbytes = lib.ssm_fwd_workspace_bytes(ctypes.byref(args))
+    if wbytes < 0:
+        _abi.check(lib.ssm_fwd_check(ctypes.byref(args)), "ssm_fwd")
+    ws = torch.empty(wbytes, dtype=torch.uint8, device=dev) if wbytes else None
+    if ws is not None:
+        args.workspace, args.workspace_bytes = ws.data_ptr(), wbytes
+    saved = None
+    if need_saved:
+        nbytes = lib.ssm_fwd_saved_bytes(ctypes.byref(args))
+        _abi.check(0 if nbytes >= 0 else 1, "ssm_fwd_saved_bytes")
+        saved = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        args.saved = saved.data_ptr()
+    with torch.cuda.device(dev):
+        stream = _abi.stream_handle(dev)
+        rc = timed_launch("ssm_fwd", stream, lambda: lib.ssm_fwd(ctypes.byref(args), stream))
+    _abi.check(rc, "ssm_fwd")
+    state = ((xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, Wv, saved), (method, bool(delta_softplus), io, ct, bool(A_is_log)))
+    return out, last, state
+
+
+def scan_backward(tensors, settings, dout, dlast, dz=None, dB=None, dC=None):
+    """One ssm_bwd launch from scan_forward's state.  dz, dB, dC may be given (views into a
+    caller's buffer, e.g. the in_proj / x_proj output gradients); the others are allocated.
+    Returns (dx, ddelta, dA, dB, dC, dD, dz, ddelta_bias, dh0); with a delta projection,
+    ddelta is the gradient of the projected (B, L, D) delta."""
+    xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, Wv, saved = tensors
+    method, softplus, io, ct, a_log = settings
+    if dout is None:
+        dout = torch.zeros(xs.shape, dtype=io, device=xs.device)
+    dout = _cast_keep(dout, io)
+    dlast = _cast_keep(dlast, ct)
+    Bsz, L, Dm = xs.shape
+    N = As.shape[1]
+    dev = xs.device
+    like = empty_like_layout
+    dx, dd = like(xs, io), like(ds if Wv is None else xs, io)
+    dA = torch.empty((Dm, N), dtype=ct, device=dev)
+    dB = like(Bs, io) if dB is None else dB
+    dC = like(Cs, io) if dC is None else dC
+    dD = torch.empty((Dm,), dtype=ct, device=dev) if Dv is not None else None
+    if zs is not None and dz is None:
+        dz = like(zs, io)
+    db = torch.empty((Dm,), dtype=ct, device=dev) if bv is not None else None
+    dh0 = torch.empty((Bsz, Dm, N), dtype=ct, device=dev) if h0v is not None else None
+    args = _abi.BwdArgs()
+    _fill_common(args, xs, ds, As, Bs, Cs, Dv, zs, bv, softplus, h0v, method, io)
+    args.saved = saved.data_ptr()
+    args.dout, args.dlast = _abi.view(dout), _abi.view(dlast)
+    args.dx, args.ddelta, args.dA = _abi.view(dx), _abi.view(dd), _abi.view(dA)
+    args.dBm, args.dCm, args.dD = _abi.view(dB), _abi.view(dC), _abi.view(dD)
+    args.dz, args.ddelta_bias, args.dh0 = _abi.view(dz), _abi.view(db), _abi.view(dh0)
+    if Wv is not None:
+        args.delta_proj, args.delta_rank = _abi.view(Wv), Wv.shape[1]
+    args.A_is_log = 1 if a_log else 0
+    lib = _abi.lib()
+    nbytes = lib.ssm_bwd_workspace_bytes(ctypes.byref(args))
+    if nbytes < 0:
+        _abi.check(lib.ssm_bwd_check(ctypes.byref(args)), "ssm_bwd")
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
+    with torch.cuda.device(dev):
+        stream = _abi.stream_handle(dev)
+        rc = timed_launch("ssm_bwd", stream, lambda: lib.ssm_bwd(ctypes.byref(args), stream))
+    _abi.check(rc, "ssm_bwd")
+    return dx, dd, dA, dB, dC, dD, dz, db, dh0
+
+
 class FusedSelectiveScanFn(torch.autograd.Function):
     """out, last = fused scan; gradients for x, delta, A, Bm, Cm, D, z, delta_bias, h0."""
 
     @staticmethod
     def forward(ctx, x, delta, A, Bm, Cm, D, z, delta_bias, h0, method, delta_softplus, segments=0,
                 delta_proj=None, A_is_log=False):
-        io, ct = _dtypes(x, (delta, Bm, Cm, z))
-        xs, ds, Bs, Cs, zs = (_cast_keep(t, io) for t in (x, delta, Bm, Cm, z))
-        As, Dv, bv, h0v, Wv = (_cast_keep(t, ct) for t in (A, D, delta_bias, h0, delta_proj))
-        Bsz, L, Dm = x.shape
-        N = A.shape[1]
-        dev = x.device
-        out = empty_like_layout(xs, io)
-        last = torch.empty((Bsz, Dm, N), dtype=ct, device=dev)
-        args = _abi.FwdArgs()
-        _fill_common(args, xs, ds, As, Bs, Cs, Dv, zs, bv, delta_softplus, h0v, method, io)
-        args.out, args.last = _abi.view(out), _abi.view(last)
-        args.segments = int(segments or 0)
-        if Wv is not None:
-            args.delta_proj, args.delta_rank = _abi.view(Wv), Wv.shape[1]
-        args.A_is_log = 1 if A_is_log else 0
-        lib = _abi.lib()
-        wbytes = lib.ssm_fwd_workspace_bytes(ctypes.byref(args))
-        if wbytes < 0:
-            _abi.check(lib.ssm_fwd_check(ctypes.byref(args)), "ssm_fwd")
-        ws = torch.empty(wbytes, dtype=torch.uint8, device=dev) if wbytes else None
-        if ws is not None:
-            args.workspace, args.workspace_bytes = ws.data_ptr(), wbytes
-        need_bwd = any(ctx.needs_input_grad[:9]) or (Wv is not None and ctx.needs_input_grad[12])
-        saved = None
+        need_bwd = any(ctx.needs_input_grad[:9]) or (delta_proj is not None and ctx.needs_input_grad[12])
+        out, last, (tensors, settings) = scan_forward(x, delta, A, Bm, Cm, D, z, delta_bias, h0, method,
+                                                      delta_softplus, segments, delta_proj, A_is_log, need_bwd)
         if need_bwd:
-            nbytes = lib.ssm_fwd_saved_bytes(ctypes.byref(args))
-            _abi.check(0 if nbytes >= 0 else 1, "ssm_fwd_saved_bytes")
-            saved = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-            args.saved = saved.data_ptr()
-        with torch.cuda.device(dev):
-            stream = _abi.stream_handle(dev)
-            rc = timed_launch("ssm_fwd", stream, lambda: lib.ssm_fwd(ctypes.byref(args), stream))
-        _abi.check(rc, "ssm_fwd")
-        if need_bwd:
-            ctx.save_for_backward(xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, Wv, saved)
+            ctx.save_for_backward(*tensors)
         ctx.set_materialize_grads(False)   # an unused `last` passes dlast = None (no zero fill)
-        ctx.method, ctx.softplus, ctx.io, ctx.ct, ctx.a_log = method, delta_softplus, io, ct, A_is_log
+        ctx.settings = settings
         ctx.in_dtypes = [None if t is None else t.dtype for t in (x, delta, A, Bm, Cm, D, z, delta_bias, h0)]
         ctx.proj_dtype = None if delta_proj is None else delta_proj.dtype
         if out.dtype != x.dtype:
@@ -149,49 +208,15 @@ class FusedSelectiveScanFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, dlast):
-        xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, Wv, saved = ctx.saved_tensors
-        io, ct = ctx.io, ctx.ct
-        if dout is None:
-            dout = torch.zeros(xs.shape, dtype=io, device=xs.device)
-        dout = _cast_keep(dout, io)
-        dlast = _cast_keep(dlast, ct)
-        Bsz, L, Dm = xs.shape
-        N = As.shape[1]
-        dev = xs.device
-
-        like = empty_like_layout
-        dx, dd = like(xs, io), like(ds if Wv is None else xs, io)
-        dA = torch.empty((Dm, N), dtype=ct, device=dev)
-        dB, dC = like(Bs, io), like(Cs, io)
-        dD = torch.empty((Dm,), dtype=ct, device=dev) if Dv is not None else None
-        dz = like(zs, io) if zs is not None else None
-        db = torch.empty((Dm,), dtype=ct, device=dev) if bv is not None else None
-        dh0 = torch.empty((Bsz, Dm, N), dtype=ct, device=dev) if h0v is not None else None
-        args = _abi.BwdArgs()
-        _fill_common(args, xs, ds, As, Bs, Cs, Dv, zs, bv, ctx.softplus, h0v, ctx.method, io)
-        args.saved = saved.data_ptr()
-        args.dout, args.dlast = _abi.view(dout), _abi.view(dlast)
-        args.dx, args.ddelta, args.dA = _abi.view(dx), _abi.view(dd), _abi.view(dA)
-        args.dBm, args.dCm, args.dD = _abi.view(dB), _abi.view(dC), _abi.view(dD)
-        args.dz, args.ddelta_bias, args.dh0 = _abi.view(dz), _abi.view(db), _abi.view(dh0)
-        if Wv is not None:
-            args.delta_proj, args.delta_rank = _abi.view(Wv), Wv.shape[1]
-        args.A_is_log = 1 if ctx.a_log else 0
-        lib = _abi.lib()
-        nbytes = lib.ssm_bwd_workspace_bytes(ctypes.byref(args))
-        if nbytes < 0:
-            _abi.check(lib.ssm_bwd_check(ctypes.byref(args)), "ssm_bwd")
-        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-        args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
-        with torch.cuda.device(dev):
-            stream = _abi.stream_handle(dev)
-            rc = timed_launch("ssm_bwd", stream, lambda: lib.ssm_bwd(ctypes.byref(args), stream))
-        _abi.check(rc, "ssm_bwd")
+        tensors = ctx.saved_tensors
+        dx, dd, dA, dB, dC, dD, dz, db, dh0 = scan_backward(tensors, ctx.settings, dout, dlast)
+        ds, Wv = tensors[1], tensors[9]
         dW = None
         if Wv is not None:
             # the projection's gradients: the two small GEMMs of F.linear's backward, in torch
+            ct = ctx.settings[3]
             ddc = dd.to(ct)
-            dW = ddc.reshape(-1, Dm).t() @ ds.to(ct).reshape(-1, Wv.shape[1])
+            dW = weight_grad(ddc.reshape(-1, ddc.shape[-1]), ds.to(ct).reshape(-1, Wv.shape[1]))
             dd = torch.matmul(ddc, Wv)
         grads = [dx, dd, dA, dB, dC, dD, dz, db, dh0]
         out = []
