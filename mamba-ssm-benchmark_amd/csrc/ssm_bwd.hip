@@ -311,30 +311,50 @@ k_bwd(const BwdParams p) {
         }
       }
       wave_lds_sync();
-      // (dx, ddelta): sum over the NP states of a channel, one (step, channel, quantity) per lane
+      // Every partial this lane adds is read before the first sum is written: a write between
+      // them would order the later reads after it, one LDS round trip per sum.
+      constexpr int NPN = (RH * CW * 2 + kWave - 1) / kWave, NPD = (RH * NP + kWave - 1) / kWave;
+      CT part[NPN][NP], pdv[NPD][CW][2];
 #pragma unroll
-      for (int i = 0; i < (RH * CW * 2 + kWave - 1) / kWave; ++i) {
+      for (int i = 0; i < NPN; ++i) {
         const int e = lane + i * kWave;
         if (e >= RH * CW * 2) break;
         const int q = e % 2, cn = (e / 2) % CW, tt = e / (2 * CW);
-        CT part[NP];
-        lds_row(&S.pn[tt][cn][q][0], part);
+        lds_row(&S.pn[tt][cn][q][0], part[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < NPD; ++i) {
+        const int e = lane + i * kWave;
+        if (e >= RH * NP) break;
+        const int tt = e / NP, nn = e % NP;
+#pragma unroll
+        for (int j = 0; j < CW; ++j) {
+          pdv[i][j][0] = S.pd[tt][j][nn][0];
+          pdv[i][j][1] = S.pd[tt][j][nn][1];
+        }
+      }
+      // (dx, ddelta): sum over the NP states of a channel, one (step, channel, quantity) per lane
+#pragma unroll
+      for (int i = 0; i < NPN; ++i) {
+        const int e = lane + i * kWave;
+        if (e >= RH * CW * 2) break;
+        const int q = e % 2, cn = (e / 2) % CW, tt = e / (2 * CW);
         CT sum = 0;
 #pragma unroll
-        for (int j = 0; j < NP; ++j) sum += part[j];
+        for (int j = 0; j < NP; ++j) sum += part[i][j];
         (q == 0 ? S.gx : S.gd)[cn][half * RH + tt] = sum;
       }
       // (dB, dC): sum over the wavefront's CW channels
 #pragma unroll
-      for (int i = 0; i < (RH * NP + kWave - 1) / kWave; ++i) {
+      for (int i = 0; i < NPD; ++i) {
         const int e = lane + i * kWave;
         if (e >= RH * NP) break;
         const int tt = e / NP, nn = e % NP;
         CT sb = 0, sc = 0;
 #pragma unroll
         for (int j = 0; j < CW; ++j) {
-          sb += S.pd[tt][j][nn][0];
-          sc += S.pd[tt][j][nn][1];
+          sb += pdv[i][j][0];
+          sc += pdv[i][j][1];
         }
         const int t = half * RH + tt;
         if constexpr (WPB > 1) {
