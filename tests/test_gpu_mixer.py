@@ -1,9 +1,9 @@
 """One Mamba layer through the single-node mixer (conv -> x_proj -> fused scan as one autograd
 node, ssm_scan.mixer) against the float64 restatement of models/mamba.py:93-126
 (oracle/lm_ref.mamba_layer) on identical weights: the output, the input gradient and every
-parameter gradient, for each discretization and for shapes whose dt_rank, d_state and d_inner
-are not multiples of the kernels' tiles.  The module-by-module path (taken when the layer
-records its delta) gives the same gradients.
+parameter gradient, for each discretization and for shapes whose dt_rank, d_state, d_inner and
+conv width are not the defaults or multiples of the kernels' tiles.  The module-by-module path
+(taken when the layer records its delta) gives the same gradients.
 
 Tolerances: float32 -- output rtol 1e-4 / atol 1e-5 x max|y|, gradients rtol 1e-3 / atol 1e-4
 x max|grad| per parameter (a gradient sums over B x L tokens).
@@ -34,14 +34,15 @@ def run_layer(m, u, dy):
     return y, u.grad, {k: p.grad.clone() for k, p in m.named_parameters()}
 
 
-@pytest.mark.parametrize("d_model,d_state,dt_rank,method,B,L", [
-    (64, 16, None, "zoh", 2, 96),
-    (40, 8, 3, "bilinear", 3, 37),
-    (48, 16, 5, "euler", 1, 130),
+@pytest.mark.parametrize("d_model,d_state,dt_rank,method,B,L,d_conv", [
+    (64, 16, None, "zoh", 2, 96, 4),
+    (40, 8, 3, "bilinear", 3, 37, 4),
+    (48, 16, 5, "euler", 1, 130, 4),
+    (56, 12, 4, "zoh", 2, 50, 3),
 ])
-def test_mixer_layer_matches_reference(dev, d_model, d_state, dt_rank, method, B, L):
+def test_mixer_layer_matches_reference(dev, d_model, d_state, dt_rank, method, B, L, d_conv):
     torch.manual_seed(d_model + L)
-    m = Mamba(d_model, d_state=d_state, dt_rank=dt_rank, discretization=method).to(dev)
+    m = Mamba(d_model, d_state=d_state, dt_rank=dt_rank, discretization=method, d_conv=d_conv).to(dev)
     u = torch.randn(B, L, d_model, device=dev)
     dy = torch.randn(B, L, d_model, device=dev)
     assert mixer_applies(m, u, None, False)
