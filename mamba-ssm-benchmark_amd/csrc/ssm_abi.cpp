@@ -605,6 +605,14 @@ int ssm_disc_bwd(const ssm_disc_args *a, void *stream) {
   REQUIRE(a->dx, "dx");
   REQUIRE(a->dA, "dA");
   REQUIRE(a->dBm, "dBm");
+  // the kernel addresses a lane's channel (or state) within a row by a 31-bit element offset
+  const ssm_tensor *per_channel[] = {&a->delta, &a->x, &a->ddelta, &a->dx};
+  for (const ssm_tensor *t : per_channel)
+    if (t->stride[2] < 0 || t->stride[2] * (a->dim - 1) >= (1LL << 31))
+      return fail(SSM_EINVAL, "channel stride %lld too large for dim=%lld", (long long)t->stride[2],
+                  (long long)a->dim);
+  if (a->Bm.stride[2] < 0 || a->Bm.stride[2] * (a->dstate - 1) >= (1LL << 31))
+    return fail(SSM_EINVAL, "Bm state stride %lld too large", (long long)a->Bm.stride[2]);
   DiscParams p = disc_params(a);
   const int ss = state_size(a->dtype);
   const int64_t wsB = align256(p.B * p.L * p.dtiles * p.N * ss);

@@ -5,7 +5,7 @@
 //
 // Forward: one lane per output element; the (B, L, D, N) outputs are written contiguously.
 // Backward: a workgroup owns 256/NP channels x NP states and walks a group of (b, l) rows,
-// issuing the next row's reads before the current row's arithmetic and stores.
+// with the reads of the next kDiscAhead rows in flight during a row's arithmetic and stores.
 //   ddelta, dx  (B, L, D)  sums over n: DPP row permutations inside each NP-lane group;
 //   dBm (B, L, N)          sum over d: per-row LDS reduction over the tile's channels into a
 //                          (row, tile, n) partial, then a fixed-order sum over tiles;
@@ -21,6 +21,8 @@ namespace ssm {
 // Time rows per lane and pass: their reads are all issued before the first store (a wave's
 // read waits would otherwise also wait for its earlier stores).
 constexpr int kDiscRows = 8;
+// Backward rows in flight per lane ahead of the row being computed.
+constexpr int kDiscAhead = 4;
 
 template <typename CT, int METHOD>
 __global__ void __launch_bounds__(kThreads) k_disc_fwd(const DiscParams p) {
@@ -69,31 +71,54 @@ __global__ void __launch_bounds__(kThreads) k_disc_bwd(const DiscParams p) {
   const int64_t r0 = g * p.rows_per_group, r1 = r0 + p.rows_per_group < R ? r0 + p.rows_per_group : R;
   AConst<CT> ac = make_aconst<CT>(-1);
   if (valid) ac = make_aconst(vload<CT>(p.A, d * p.A.s0 + n * p.A.s1));
-  // lane parts of the addresses (row parts are uniform)
-  const CT *pdel = (const CT *)p.delta.p + dc * p.delta.s2, *px = (const CT *)p.x.p + dc * p.x.s2;
-  const CT *pB = (const CT *)p.Bm.p + nc * p.Bm.s2;
-  const CT *pda = (const CT *)p.da + dc * p.N + nc, *pdb = (const CT *)p.db + dc * p.N + nc;
+  // Addresses: a uniform row offset (advanced one row at a time) plus the lane's 32-bit
+  // element offset (the host checks that every lane offset fits in 31 bits).
+  const uint32_t ldel = (uint32_t)(dc * p.delta.s2), lx = (uint32_t)(dc * p.x.s2), lB = (uint32_t)(nc * p.Bm.s2);
+  const uint32_t lg = (uint32_t)(dc * p.N + nc);
+  const uint32_t ldd = (uint32_t)(dc * p.ddelta.s2), ldx = (uint32_t)(dc * p.dx.s2);
   const int64_t DN = p.D * p.N;
-  CT gA = 0;
-  // the next row's reads are issued before this row's stores
-  int64_t b = r0 / p.L, t = r0 - (r0 / p.L) * p.L;
   struct Row { CT dt, x, B, ga, gb; };
-  auto fetch = [&](int64_t bb, int64_t tt, int64_t r) {
+  // row offsets of the next row to fetch (delta, x, Bm, and the (row, d, n) gradients)
+  int64_t fr = r0, fb = r0 / p.L, ft = r0 - fb * p.L;
+  int64_t odel = fb * p.delta.s0 + ft * p.delta.s1, ox = fb * p.x.s0 + ft * p.x.s1,
+          oB = fb * p.Bm.s0 + ft * p.Bm.s1, og = r0 * DN;
+  const CT *const del = (const CT *)p.delta.p, *const xs = (const CT *)p.x.p, *const Bs = (const CT *)p.Bm.p;
+  const CT *const das = (const CT *)p.da, *const dbs = (const CT *)p.db;
+  // Rows are fetched kDiscAhead ahead of the one being computed (a ring of registers, the
+  // loop unrolled over it).  Past the group's last row the fetch repeats that row, so every
+  // read stays in bounds.
+  auto fetch_next = [&]() {
     Row v;
-    v.dt = pdel[bb * p.delta.s0 + tt * p.delta.s1];
-    v.x = px[bb * p.x.s0 + tt * p.x.s1];
-    v.B = pB[bb * p.Bm.s0 + tt * p.Bm.s1];
-    v.ga = pda[r * DN];
-    v.gb = pdb[r * DN];
+    v.dt = (del + odel)[ldel];
+    v.x = (xs + ox)[lx];
+    v.B = (Bs + oB)[lB];
+    v.ga = (das + og)[lg];
+    v.gb = (dbs + og)[lg];
+    if (fr + 1 < r1) {
+      ++fr;
+      og += DN;
+      if (++ft == p.L) {
+        ft = 0;
+        ++fb;
+        odel += p.delta.s0 - (p.L - 1) * p.delta.s1;
+        ox += p.x.s0 - (p.L - 1) * p.x.s1;
+        oB += p.Bm.s0 - (p.L - 1) * p.Bm.s1;
+      } else {
+        odel += p.delta.s1;
+        ox += p.x.s1;
+        oB += p.Bm.s1;
+      }
+    }
     return v;
   };
-  Row cur = fetch(b, t, r0);
-  int buf = 0;
-  for (int64_t r = r0; r < r1; ++r, buf ^= 1) {
-    const int64_t bc = b, tc = t;
-    if (++t == p.L) { t = 0; ++b; }
-    const bool more = r + 1 < r1;
-    const Row nxt = fetch(more ? b : bc, more ? t : tc, more ? r + 1 : r);
+  // row offsets of the row being stored
+  int64_t sb = r0 / p.L, st = r0 - sb * p.L;
+  int64_t odd = sb * p.ddelta.s0 + st * p.ddelta.s1, odx = sb * p.dx.s0 + st * p.dx.s1;
+  CT *const dds = (CT *)p.ddelta.p, *const dxs = (CT *)p.dx.p;
+  CT *wsB = (CT *)p.ws_dB + (r0 * p.dtiles + tile) * p.N;
+  const int64_t wstep = p.dtiles * p.N;
+  CT gA = 0;
+  auto row = [&](const Row &cur, int buf) {
     CT gd = 0, gx = 0, gB = 0;
     if (valid) {
       CT a, coef, dadz, dbdd, d2f;
@@ -108,18 +133,38 @@ __global__ void __launch_bounds__(kThreads) k_disc_bwd(const DiscParams p) {
     gd = group_sum<NP>(gd);
     gx = group_sum<NP>(gx);
     if (n == 0 && d < p.D) {
-      vstore<CT>(p.ddelta, bc * p.ddelta.s0 + tc * p.ddelta.s1 + d * p.ddelta.s2, gd);
-      vstore<CT>(p.dx, bc * p.dx.s0 + tc * p.dx.s1 + d * p.dx.s2, gx);
+      (dds + odd)[ldd] = gd;
+      (dxs + odx)[ldx] = gx;
     }
     red[buf][c][n] = gB;
     __syncthreads();
     if (tid < NP) {  // dBm partial of (row, state): sum over the tile's DT channels in channel order
-      CT s = 0;
+      CT sum = 0;
 #pragma unroll
-      for (int k = 0; k < DT; ++k) s += red[buf][k][tid];
-      if (tid < p.N) ((CT *)p.ws_dB)[(r * p.dtiles + tile) * p.N + tid] = s;
+      for (int k = 0; k < DT; ++k) sum += red[buf][k][tid];
+      if (tid < p.N) wsB[tid] = sum;
     }
-    cur = nxt;
+    wsB += wstep;
+    if (++st == p.L) {
+      st = 0;
+      odd += p.ddelta.s0 - (p.L - 1) * p.ddelta.s1;
+      odx += p.dx.s0 - (p.L - 1) * p.dx.s1;
+    } else {
+      odd += p.ddelta.s1;
+      odx += p.dx.s1;
+    }
+  };
+  Row q[kDiscAhead];
+#pragma unroll
+  for (int k = 0; k < kDiscAhead; ++k) q[k] = fetch_next();
+  for (int64_t r = r0; r < r1; r += kDiscAhead) {
+#pragma unroll
+    for (int k = 0; k < kDiscAhead; ++k) {
+      if (r + k >= r1) break;  // uniform over the workgroup
+      const Row cur = q[k];
+      q[k] = fetch_next();
+      row(cur, k & 1);
+    }
   }
   if (valid) ((CT *)p.ws_dA)[(g * p.D + d) * p.N + n] = gA;
 }
