@@ -560,6 +560,15 @@ static DiscParams disc_params(const ssm_disc_args *a) {
   return p;
 }
 
+// The discretization kernels address a lane's channel (or state) within a row by a 31-bit
+// element offset.
+static int disc_lane_offsets(const ssm_tensor *t, int64_t extent) {
+  if (t->stride[2] < 0 || t->stride[2] * (extent - 1) >= (1LL << 31))
+    return fail(SSM_EINVAL, "inner stride %lld too large for extent %lld", (long long)t->stride[2],
+                (long long)extent);
+  return 0;
+}
+
 int ssm_disc_check(const ssm_disc_args *a) {
   if (!a) return fail(SSM_EINVAL, "null args");
   int rc = check_common(a->batch, a->seqlen, a->dim, a->dstate, a->method, a->dtype);
@@ -572,6 +581,9 @@ int ssm_disc_check(const ssm_disc_args *a) {
   REQUIRE(a->x, "x");
   REQUIRE(a->A, "A");
   REQUIRE(a->Bm, "Bm");
+  if ((rc = disc_lane_offsets(&a->delta, a->dim)) || (rc = disc_lane_offsets(&a->x, a->dim)) ||
+      (rc = disc_lane_offsets(&a->Bm, a->dstate)))
+    return rc;
   return ok();
 }
 
@@ -605,14 +617,9 @@ int ssm_disc_bwd(const ssm_disc_args *a, void *stream) {
   REQUIRE(a->dx, "dx");
   REQUIRE(a->dA, "dA");
   REQUIRE(a->dBm, "dBm");
-  // the kernel addresses a lane's channel (or state) within a row by a 31-bit element offset
-  const ssm_tensor *per_channel[] = {&a->delta, &a->x, &a->ddelta, &a->dx};
-  for (const ssm_tensor *t : per_channel)
-    if (t->stride[2] < 0 || t->stride[2] * (a->dim - 1) >= (1LL << 31))
-      return fail(SSM_EINVAL, "channel stride %lld too large for dim=%lld", (long long)t->stride[2],
-                  (long long)a->dim);
-  if (a->Bm.stride[2] < 0 || a->Bm.stride[2] * (a->dstate - 1) >= (1LL << 31))
-    return fail(SSM_EINVAL, "Bm state stride %lld too large", (long long)a->Bm.stride[2]);
+  rc = disc_lane_offsets(&a->ddelta, a->dim);
+  if (!rc) rc = disc_lane_offsets(&a->dx, a->dim);
+  if (rc) return rc;
   DiscParams p = disc_params(a);
   const int ss = state_size(a->dtype);
   const int64_t wsB = align256(p.B * p.L * p.dtiles * p.N * ss);

@@ -281,3 +281,23 @@ def test_norm_needs_unit_column_stride_and_rstd():
     a = _norm_args(rows=1000, dim=256)
     # backward partials: one (dim,) row per workgroup of 4 wavefronts x 8 rows
     assert lib.ssm_norm_workspace_bytes(ctypes.byref(a)) == ((1000 + 31) // 32) * 256 * 4
+
+
+def test_disc_lane_offsets_validated():
+    """The discretization kernels address a lane's channel (state) inside a row with a 31-bit
+    element offset: an inner stride whose span over the channels (states) reaches 2^31 is
+    rejected on the host; channel-major and time-major layouts of ordinary sizes pass."""
+    t = torch.zeros(2, 8, 4)
+    a = _abi.DiscArgs()
+    a.batch, a.seqlen, a.dim, a.dstate, a.method, a.dtype = 2, 8, 4, 4, 0, 0
+    a.delta, a.x, a.Bm, a.A = _abi.view(t), _abi.view(t.transpose(1, 2).contiguous().transpose(1, 2)), \
+        _abi.view(t), _abi.view(torch.zeros(4, 4))
+    lib = _abi.lib()
+    assert lib.ssm_disc_check(ctypes.byref(a)) == 0
+    a.x.stride[2] = (1 << 31) // 3 + 1                     # span 3 * stride >= 2^31
+    with pytest.raises(ValueError, match="inner stride"):
+        _abi.check(lib.ssm_disc_check(ctypes.byref(a)), "ssm_disc")
+    a.x.stride[2] = 1
+    a.Bm.stride[2] = -1
+    with pytest.raises(ValueError, match="inner stride"):
+        _abi.check(lib.ssm_disc_check(ctypes.byref(a)), "ssm_disc")
