@@ -45,9 +45,8 @@ class MixerFn(torch.autograd.Function):
         Dm = xz.shape[-1] // 2
         Wdt = tensors[9]
         R = Wdt.shape[1]
-        N = proj.shape[-1] - R
-        N //= 2
         P = proj.shape[-1]
+        N = (P - R) // 2
         dxz = torch.empty_like(xz)
         dproj = torch.empty_like(proj)
         dxc, dd, dA, _, _, dD, _, db, _ = scan_backward(tensors, ctx.settings, dy, None, dz=dxz[..., Dm:],
