@@ -119,7 +119,8 @@ typedef struct ssm_bwd_args {
   ssm_tensor dA;           /* (D,N) state type */
   ssm_tensor dBm, dCm;     /* (B,L,N) dtype */
   ssm_tensor dD;           /* (D,) state type, required iff Dskip */
-  ssm_tensor dz;           /* (B,L,D) dtype, required iff z */
+  ssm_tensor dz;           /* (B,L,D) dtype, required iff z; any strides (e.g. the gate half
+                              of an in_proj-output gradient, as z may be) */
   ssm_tensor ddelta_bias;  /* (D,) state type, required iff delta_bias */
   ssm_tensor dh0;          /* (B,D,N) state type, optional (gradient of h0) */
   void *workspace;         /* ssm_bwd_workspace_bytes() */
