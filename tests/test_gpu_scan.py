@@ -83,6 +83,28 @@ def test_discretize_strided_views_and_errors(dev):
         S.discretize(delta.to(dev), A.to(dev), Bm.to(dev), x.to(dev), "rk4")
 
 
+def test_discretize_backward_long_groups_and_strided_views(dev):
+    """The discretization backward walks groups of (b, t) rows per workgroup with reads four
+    rows ahead: at B3 L7001 D8 N4 a group holds 6 rows, groups cross batch rows and the last
+    one is partial; delta and x are read from (B, D, L) storage and B from a strided split
+    view.  Gradients against the float64 vector-Jacobian product of models/scan.py:39-55."""
+    x, delta, A, Bm, _, _ = sel_inputs(B=3, L=7001, D=8, N=4, seed=5, h0=False)
+    g = torch.Generator().manual_seed(6)
+    ga = torch.randn(3, 7001, 8, 4, generator=g, dtype=torch.float64)
+    gb = torch.randn(3, 7001, 8, 4, generator=g, dtype=torch.float64)
+    cm = lambda t: t.transpose(1, 2).contiguous().transpose(1, 2).to(dev, torch.float32)
+    big = torch.zeros(3, 7001, 11, dtype=torch.float64)
+    big[..., 3:7] = Bm
+    leaves = [cm(delta), A.to(dev, torch.float32), big.to(dev, torch.float32)[..., 3:7], cm(x)]
+    for t in leaves:
+        t.requires_grad_()
+    a, b = S.discretize(*leaves, method="zoh")
+    torch.autograd.backward((a, b), (ga.to(dev, torch.float32), gb.to(dev, torch.float32)))
+    ref = R.discretize_vjp(*(np64(t) for t in (delta, A, Bm, x)), np64(ga), np64(gb), "zoh")
+    for name, t, r in zip(("ddelta", "dA", "dBm", "dx"), leaves, ref):
+        close(t.grad, r, torch.float32, name)
+
+
 def test_zoh_matrix_matches_diagonal_discretize(dev):
     A = -torch.tensor([0.5, 1.5, 3.0], dtype=torch.float64, device=dev)
     Ad, Bd = S.zoh_matrix(torch.diag(A), torch.ones(3, 1, dtype=torch.float64, device=dev), 0.3)
