@@ -228,11 +228,12 @@ k_fwd(const FwdParams p) {
       const int tg = t0 + t, dd = dw + cc;
       CT part[NP];
       lds_row(&S.y[t][cc][0], part);
+      const CT xv = S.x[cc][t];  // read with the partials: one LDS round trip
       CT y = 0;
 #pragma unroll
       for (int j = 0; j < NP; ++j) y += part[j];
       if (tg >= Lc || dd >= D) continue;
-      const CT skip = p.has_D ? dskv[i] * S.x[cc][t] : (CT)0;
+      const CT skip = p.has_D ? dskv[i] * xv : (CT)0;
       if (p.ypre) ((CT *)p.ypre)[ypre_index(!xt, b, tg, dd, p.L, p.D)] = y + skip;
       if (!p.write_out) continue;
       CT o = y + skip;
