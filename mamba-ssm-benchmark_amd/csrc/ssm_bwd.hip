@@ -381,7 +381,8 @@ k_bwd(const BwdParams p) {
       const int tg = t0 + t, dd = dw + cc;
       if (tg >= Lc || dd >= D) continue;
       CT gx = S.gx[cc][t];
-      if (p.has_D) gx += S.dy[cc][t] * dskv[i];
+      const CT dyv = S.dy[cc][t];  // read with gx: one LDS round trip
+      if (p.has_D) gx += dyv * dskv[i];
       Conv<IT>::store(vpw<IT>(vdx) + b * vdx.s0 + row_off<UL>(tg, dd, vdx.s1, vdx.s2), gx);
     }
 #pragma unroll
