@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 3
+#define SSM_ABI_VERSION 4
 
 enum { SSM_OK = 0, SSM_EINVAL = 1, SSM_EKEY = 2, SSM_ESPACE = 3, SSM_EHIP = 4 };
 
@@ -109,7 +109,11 @@ typedef struct ssm_bwd_args {
   int32_t method, dtype;
   ssm_tensor x, delta, A, Bm, Cm, Dskip, z, delta_bias; /* as in ssm_fwd_args */
   int32_t delta_softplus;
-  int32_t reserved0;
+  int32_t segments;        /* time segments walked back in parallel: 0 = chosen by the library
+                              (more than 1 only when B x D alone cannot fill the GPU); each
+                              segment starts from the adjoint carried in from the later ones,
+                              combined as the forward combines its segments, in reverse.
+                              Float64 inputs always use one segment. */
   ssm_tensor h0;
   const void *saved;       /* the `saved` buffer of the matching ssm_fwd call, or NULL
                               (then the states are recomputed into the workspace) */

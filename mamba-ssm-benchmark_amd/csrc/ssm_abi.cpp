@@ -94,7 +94,7 @@ struct FwdLayout {
 
 FwdLayout fwd_layout(int64_t B, int64_t L, int64_t D, int64_t N, int dtype, bool gate) {
   FwdLayout f;
-  f.np = padded_n(N);
+  f.np = fused_np(N, dtype);
   f.ck = chunk_steps(dtype);
   f.nchunks = (int)cdiv(L, f.ck);
   f.ckpt_bytes = align256(B * f.nchunks * D * f.np * state_size(dtype));
@@ -102,16 +102,49 @@ FwdLayout fwd_layout(int64_t B, int64_t L, int64_t D, int64_t N, int dtype, bool
   return f;
 }
 
+// The uniform-layout kernels also address the saved chunk states and pre-gate output through
+// buffers over one batch row, with 32-bit byte offsets.
+bool saved_rows_fit(const FwdLayout &f, int64_t L, int64_t D, int dtype) {
+  const int64_t lim = (int64_t)1 << 31;
+  return (int64_t)f.nchunks * D * f.np * state_size(dtype) < lim && L * D * state_size(dtype) < lim;
+}
+
+// Time segments, shared by the forward and the backward: one unless the B x ceil(D /
+// channels-per-wavefront) wavefronts leave the GPU short of work (fewer than kSegEnough); then
+// enough segments for about kSegTarget wavefronts, each at least kSegMinChunks chunks long.  A
+// positive `requested` overrides the choice (clamped to the valid range).
+constexpr int64_t kSegEnough = 2048, kSegTarget = 4096, kSegMinChunks = 4;
+
+struct SegPlan {
+  int nseg, seg_chunks;
+};
+
+SegPlan seg_plan(int64_t B, int64_t D, const FwdLayout &f, int requested) {
+  SegPlan s;
+  const int64_t waves = B * cdiv(D, 64 / f.np);
+  int64_t n = 1;
+  if (requested > 0) n = requested;
+  else if (waves < kSegEnough) n = std::min(cdiv(kSegTarget, waves), (int64_t)f.nchunks / kSegMinChunks);
+  n = std::max((int64_t)1, std::min(n, std::min((int64_t)f.nchunks, 65535 / B)));
+  s.seg_chunks = (int)cdiv(f.nchunks, n);
+  s.nseg = (int)cdiv(f.nchunks, s.seg_chunks);
+  return s;
+}
+
 struct BwdLayout {
   FwdLayout f;
+  SegPlan sp;
   int ntiles;
-  int64_t saved, dB, dC, dA, dD, db, total;  // byte offsets
+  int64_t saved, dB, dC, dA, dD, db, mu, E, P, total;  // byte offsets
 };
 
 BwdLayout bwd_layout(const ssm_bwd_args *a) {
   BwdLayout w;
   w.f = fwd_layout(a->batch, a->seqlen, a->dim, a->dstate, a->dtype, has(a->z));
+  // float64 runs the register-staged kernel, which has no time segments
+  w.sp = a->dtype == SSM_F64 ? SegPlan{1, w.f.nchunks} : seg_plan(a->batch, a->dim, w.f, a->segments);
   const int ss = state_size(a->dtype);
+  const int64_t rows = a->batch * w.sp.nseg;
   w.ntiles = (int)cdiv(a->dim, bwd_channels_per_block(a->dtype, w.f.np));
   int64_t off = 0;
   w.saved = off;
@@ -119,9 +152,13 @@ BwdLayout bwd_layout(const ssm_bwd_args *a) {
   const int64_t part = align256(a->batch * w.ntiles * a->seqlen * w.f.np * ss);
   w.dB = off; off += part;
   w.dC = off; off += part;
-  w.dA = off; off += align256(a->batch * a->dim * w.f.np * ss);
-  w.dD = off; off += align256(a->batch * a->dim * ss);
-  w.db = off; off += align256(a->batch * a->dim * ss);
+  w.dA = off; off += align256(rows * a->dim * w.f.np * ss);
+  w.dD = off; off += align256(rows * a->dim * ss);
+  w.db = off; off += align256(rows * a->dim * ss);
+  const int64_t segs = w.sp.nseg > 1 ? rows * a->dim * w.f.np : 0;
+  w.mu = off; off += align256(segs * 8);
+  w.E = off; off += align256(segs * 8);
+  w.P = off; off += align256(segs * 4);
   w.total = off;
   return w;
 }
@@ -172,34 +209,15 @@ int64_t ssm_fwd_saved_bytes(const ssm_fwd_args *a) {
   return f.ckpt_bytes + f.ypre_bytes;
 }
 
-// Time segments of the forward.  One unless the B x ceil(D / channels-per-wavefront)
-// wavefronts leave the GPU short of work (fewer than kSegEnough); then enough segments for
-// about kSegTarget wavefronts, each segment at least kSegMinChunks chunks long.  A positive
-// `requested` overrides the choice (clamped to the valid range).
-constexpr int64_t kSegEnough = 2048, kSegTarget = 4096, kSegMinChunks = 4;
-
-struct SegPlan {
-  int nseg, seg_chunks;
-  int64_t buf_bytes;  // one (B, nseg, D, NP) state-type buffer
-};
-
-static SegPlan seg_plan(const ssm_fwd_args *a, const FwdLayout &f) {
-  SegPlan s;
-  const int64_t waves = a->batch * cdiv(a->dim, 64 / f.np);
-  int64_t n = 1;
-  if (a->segments > 0) n = a->segments;
-  else if (waves < kSegEnough) n = std::min(cdiv(kSegTarget, waves), (int64_t)f.nchunks / kSegMinChunks);
-  n = std::max((int64_t)1, std::min(n, std::min((int64_t)f.nchunks, 65535 / a->batch)));
-  s.seg_chunks = (int)cdiv(f.nchunks, n);
-  s.nseg = (int)cdiv(f.nchunks, s.seg_chunks);
-  s.buf_bytes = s.nseg > 1 ? align256(a->batch * s.nseg * a->dim * f.np * state_size(a->dtype)) : 0;
-  return s;
+// One (B, nseg, D, NP) state-type buffer of the forward's segment summaries (0 without segments).
+static int64_t seg_buf_bytes(const ssm_fwd_args *a, const FwdLayout &f, const SegPlan &sp) {
+  return sp.nseg > 1 ? align256(a->batch * sp.nseg * a->dim * f.np * state_size(a->dtype)) : 0;
 }
 
 int64_t ssm_fwd_workspace_bytes(const ssm_fwd_args *a) {
   if (ssm_fwd_check(a)) return -1;
   FwdLayout f = fwd_layout(a->batch, a->seqlen, a->dim, a->dstate, a->dtype, has(a->z));
-  return 3 * seg_plan(a, f).buf_bytes;
+  return 3 * seg_buf_bytes(a, f, seg_plan(a->batch, a->dim, f, a->segments));
 }
 
 static void fill_fwd(FwdParams &p, const ssm_fwd_args *a, const FwdLayout &f) {
@@ -220,7 +238,8 @@ static void fill_fwd(FwdParams &p, const ssm_fwd_args *a, const FwdLayout &f) {
     p.dtl = kv(a->delta); p.dtw = kv(a->delta_proj); p.dt = kv(a->x);
   }
   const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->out};
-  p.uniform = uniform_layout(bld, 3, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype, a->z);
+  p.uniform = uniform_layout(bld, 3, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype, a->z) &&
+              saved_rows_fit(f, a->seqlen, a->dim, a->dtype);
 }
 
 int ssm_fwd(const ssm_fwd_args *a, void *stream) {
@@ -233,16 +252,17 @@ int ssm_fwd(const ssm_fwd_args *a, void *stream) {
     p.ckpt = a->saved;
     p.ypre = has(a->z) ? (char *)a->saved + f.ckpt_bytes : nullptr;
   }
-  const SegPlan sp = seg_plan(a, f);
+  const SegPlan sp = seg_plan(a->batch, a->dim, f, a->segments);
+  const int64_t bb = seg_buf_bytes(a, f, sp);
   if (sp.nseg > 1) {
-    if (!a->workspace || a->workspace_bytes < 3 * sp.buf_bytes)
+    if (!a->workspace || a->workspace_bytes < 3 * bb)
       return fail(SSM_ESPACE, "workspace of %lld bytes is smaller than the %lld required",
-                  (long long)a->workspace_bytes, (long long)(3 * sp.buf_bytes));
+                  (long long)a->workspace_bytes, (long long)(3 * bb));
     p.nseg = sp.nseg;
     p.seg_chunks = sp.seg_chunks;
     p.seg_P = a->workspace;
-    p.seg_E = (char *)a->workspace + sp.buf_bytes;
-    p.seg_hin = (char *)a->workspace + 2 * sp.buf_bytes;
+    p.seg_E = (char *)a->workspace + bb;
+    p.seg_hin = (char *)a->workspace + 2 * bb;
   }
   hipError_t e = launch_fwd(p, a->dtype, a->method, f.np, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "ssm_fwd launch");
@@ -269,6 +289,7 @@ int ssm_bwd_check(const ssm_bwd_args *a) {
   if (has(a->z)) REQUIRE(a->dz, "dz");
   if (has(a->delta_bias)) REQUIRE(a->ddelta_bias, "ddelta_bias");
   if (has(a->dh0) && !has(a->h0)) return fail(SSM_EINVAL, "dh0 given without h0");
+  if (a->segments < 0) return fail(SSM_EINVAL, "segments=%d must be >= 0", a->segments);
   return check_lowrank(a->delta_rank, a->delta_proj, a->delta, a->seqlen, a->dstate, a->dtype);
 }
 
@@ -330,14 +351,17 @@ int ssm_bwd(const ssm_bwd_args *a, void *stream) {
   // dz keeps its own strides (like z): it only needs 32-bit row offsets
   const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->dout, &a->dx, &a->ddelta};
   p.uniform = uniform_layout(bld, 5, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype, a->z) &&
+              saved_rows_fit(w.f, a->seqlen, a->dim, a->dtype) &&
               (!has(a->dz) || row_fits(a->dz, a->seqlen, a->dim, a->dtype == SSM_F64 ? 8 : a->dtype == SSM_F32 ? 4 : 2));
   p.ws_dB = ws + w.dB; p.ws_dC = ws + w.dC; p.ws_dA = ws + w.dA; p.ws_dD = ws + w.dD; p.ws_db = ws + w.db;
+  p.nseg = w.sp.nseg; p.seg_chunks = w.sp.seg_chunks;
+  if (w.sp.nseg > 1) { p.seg_mu = ws + w.mu; p.seg_E = ws + w.E; p.seg_P = ws + w.P; }
   hipError_t e = launch_bwd(p, a->dtype, a->method, w.f.np, s);
   if (e != hipSuccess) return hip_fail(e, "ssm_bwd launch");
   FinParams fin;
   memset(&fin, 0, sizeof(fin));
   fin.B = a->batch; fin.L = a->seqlen; fin.D = a->dim; fin.N = a->dstate;
-  fin.ntiles = w.ntiles; fin.np = w.f.np;
+  fin.ntiles = w.ntiles; fin.np = w.f.np; fin.rows = a->batch * w.sp.nseg;
   fin.has_D = has(a->Dskip); fin.has_bias = has(a->delta_bias);
   fin.a_log = a->A_is_log != 0; fin.A = kv(a->A);
   fin.ws_dB = p.ws_dB; fin.ws_dC = p.ws_dC; fin.ws_dA = p.ws_dA; fin.ws_dD = p.ws_dD; fin.ws_db = p.ws_db;

@@ -18,6 +18,7 @@
 // The finalize kernel sums the dB / dC partials over channel tiles and dA / dD / d_bias over
 // the batch, in a fixed order (bitwise reproducible; no float atomics).
 #include "ssm_device.hpp"
+#include "ssm_dpp.hpp"
 #include "ssm_internal.hpp"
 #include "ssm_tiles.hpp"
 #include "ssm_wave.hpp"
@@ -531,36 +532,434 @@ __global__ void __launch_bounds__(256) k_bwd_finalize(const FinParams p) {
   const int64_t j = i - nBC;
   if (j < nDN) {
     const int64_t d = j / p.N, nn = j % p.N;
-    CT s = fin_sum((const CT *)p.ws_dA + d * p.np + nn, p.D * p.np, p.B);
+    CT s = fin_sum((const CT *)p.ws_dA + d * p.np + nn, p.D * p.np, p.rows);
     if (p.a_log) s *= -exp(vload<CT>(p.A, d * p.A.s0 + nn * p.A.s1));  // dA_log = dA * A
     vstore<CT>(p.dA, d * p.dA.s0 + nn * p.dA.s1, s);
     return;
   }
   const int64_t k = j - nDN;
   if (k < p.D) {
-    if (p.has_D) vstore<CT>(p.dD, k * p.dD.s0, fin_sum((const CT *)p.ws_dD + k, p.D, p.B));
-    if (p.has_bias) vstore<CT>(p.dbias, k * p.dbias.s0, fin_sum((const CT *)p.ws_db + k, p.D, p.B));
+    if (p.has_D) vstore<CT>(p.dD, k * p.dD.s0, fin_sum((const CT *)p.ws_dD + k, p.D, p.rows));
+    if (p.has_bias) vstore<CT>(p.dbias, k * p.dbias.s0, fin_sum((const CT *)p.ws_db + k, p.D, p.rows));
   }
+}
+
+// ------------------------------------------------------------------ float kernels (row tiles)
+// The float-compute backward (float32 / bf16 / fp16 inputs, float32 state), NP >= 16.  Same
+// per-chunk structure as k_bwd, with the changes of the forward's row-tile kernel:
+//   * x, delta (bias / softplus applied), dy = dout silu(z) and the softplus derivative stay in
+//     one register per lane (row tiles) and reach each step's lanes by DPP row broadcast; B is
+//     read from LDS once per chunk and kept in registers from the recompute to the walk back;
+//   * the sums over the states of the dx / ddelta terms land directly in the row-tile lanes
+//     that store them (no LDS round trip for the stores);
+//   * the adjoint keeps float64 accuracy with one float64 add per step: the step's increment
+//     (a - 1) lambda + dy C is formed in float32 (it is small against lambda, and dy C carries
+//     its own float32 rounding in any case) and accumulated into a float64 lambda;
+//   * buffer addresses take the chunk offset as a scalar operand.
+// Time segments (few batch rows x channels, long L): each segment walks its own chunks from the
+// adjoint carried into it.  A summary pass (SUM) gives each segment's zero-start adjoint at its
+// first step times that step's decay (E) and the product of its decays (P); k_bwd_carry turns
+// them into the adjoint entering every segment, the reverse of the forward's segment carry.
+template <int NP, bool LR>
+struct BwdwLds {
+  static constexpr int CW = kWave / NP, CKP = ck_pad(4), NPP = np_pad(4, NP), RH = 8;
+  float B[NP][CKP];
+  float C[NP][CKP];
+  float pn[RH][CW][2][NPP];  // (dx, ddelta) terms of half a chunk, per state
+  float pd[RH][CW][NP][2];   // (dB, dC) terms of half a chunk, per channel
+  float lr[LR ? kCK : 1][lr_pad(4)];
+  float wr[LR ? CW : 1][lr_pad(4)];
+};
+
+template <typename IT, int NP, int METHOD, bool UL, bool SUM, bool LR>
+__global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams p) {
+  typedef BwdwLds<NP, LR> WL;
+  typedef RowGeo<NP> G;
+  typedef RowTile<IT, NP, UL> RT;
+  constexpr int CW = G::CW, CK = kCK, RH = WL::RH, WPB = bwdw_waves(NP), NT = WPB * kWave;
+  constexpr bool M1 = METHOD == 0;
+  __shared__ __align__(16) WL lds_all[WPB];
+  __shared__ __align__(16) float dbc[2][WPB][RH][NP][2];  // per-wavefront (dB, dC) sums, by half parity
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave, wv = tid / kWave;
+  WL &S = lds_all[wv];
+  const int c = lane / NP, n = lane % NP;
+  const int tj = G::step(lane), tc = G::chan(lane);
+  const int64_t b = blockIdx.y / p.nseg;
+  const int seg = (int)(blockIdx.y % p.nseg);
+  if (SUM && seg == 0) return;  // the first segment's summary is never used
+  const int k0 = seg * p.seg_chunks;
+  const int k1 = k0 + p.seg_chunks < p.nchunks ? k0 + p.seg_chunks : p.nchunks;
+  const int tile = blockIdx.x;
+  const int dw = (tile * WPB + wv) * CW;
+  const int d = dw + c;
+  const bool dval = d < p.D, nval = n < p.N;
+  const bool tval = dw + tc < p.D;
+  const int L = (int)p.L, D = (int)p.D, N = (int)p.N;
+  const int64_t sidx = ((b * p.nseg + seg) * p.D + d) * NP + n;  // (B, nseg, D, NP)
+
+  float Av = -1.0f;
+  if (dval && nval) {
+    Av = vload<float>(p.A, d * p.A.s0 + n * p.A.s1);
+    if (p.a_log) Av = -__expf(Av);  // models/mamba.py:81
+  }
+  const AConst<float> ac = make_aconst(Av);
+  // the adjoint entering the segment's last step: dlast, or the carry of the later segments
+  double lam = 0.0;
+  if (!SUM && dval && nval) {
+    if (p.nseg > 1) lam = ((const double *)p.seg_mu)[sidx];
+    else if (p.has_dlast) lam = (double)vload<float>(p.dlast, b * p.dlast.s0 + d * p.dlast.s1 + n * p.dlast.s2);
+  }
+  float lamf = (float)lam;
+  float m_next = M1 ? 0.0f : 1.0f;  // a - 1 (ZOH) or a of the step after the current one
+  float prod = 1.0f;                // summary: product of the segment's decays
+  float h0v = 0.0f;
+  if (!SUM && p.has_h0 && dval && nval) h0v = vload<float>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
+  float dA_acc = 0.0f, dDp = 0.0f, dbp = 0.0f;
+  const float biasv = p.has_bias && tval ? vload<float>(p.bias, (int64_t)(dw + tc) * p.bias.s0) : 0.0f;
+  const float dskv = p.has_D && tval ? vload<float>(p.Dsk, (int64_t)(dw + tc) * p.Dsk.s0) : 0.0f;
+
+  const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = p.z;
+  const KView vg = with_layout<UL>(p.dout, p.x), vdz = p.dz;
+  const KView vdx = with_layout<UL>(p.dx, p.x), vddt = with_layout<UL>(p.ddt, p.x);
+  const KView vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
+  const bool xt = vx.s1 == 1, bt = vB.s1 == 1, ctt = vC.s1 == 1;
+  const KView vzl = p.has_z ? vz : vx;
+  const float *ypre = (const float *)p.ypre;
+  struct Tiles {
+    RT x, dt, g, z, yp;
+    WaveTile<IT, float, CK, NP, UL> B, C;
+    LowRankTile<IT, float, CK> lr;
+    float ck;
+  };
+  constexpr int ES = (int)sizeof(IT), EB = WaveTile<IT, float, CK, NP, UL>::E;
+  const uint32_t offX = RT::offset(vx, dw, lane), offZ = RT::offset(vzl, dw, lane);
+  const uint32_t offDZ = p.has_z ? RT::offset(vdz, dw, lane) : 0u;
+  uint32_t offB[EB];
+  tile_offsets<CK, NP>(offB, vB, 0, bt, lane, ES);
+  const __amdgpu_buffer_rsrc_t empty = flat_buffer(p.x.p, 0);
+  const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbdt = LR ? empty : row_buffer(vdt, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbg = row_buffer(vg, b, L, D, ES), rbz = row_buffer(vzl, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbB = row_buffer(vB, b, L, N, ES), rbC = row_buffer(vC, b, L, N, ES);
+  const int64_t ckrow = (int64_t)p.nchunks * p.D * NP;
+  const __amdgpu_buffer_rsrc_t rbk = flat_buffer((const float *)p.ckpt + b * ckrow, ckrow * 4);
+  const __amdgpu_buffer_rsrc_t rby = flat_buffer(ypre ? ypre + b * p.L * p.D : p.x.p, ypre ? p.L * p.D * 4 : 0);
+  const uint32_t offK = (uint32_t)((dval ? d : 0) * NP + n) * 4u;
+  const uint32_t offY = (uint32_t)(ypre_index(!xt, 0, tj, dw + tc, p.L, p.D) * 4);
+  const uint32_t tstepY = (uint32_t)((xt ? 1 : (int)p.D) * CK * 4);
+  __amdgpu_buffer_rsrc_t rblr = empty;
+  uint32_t offLR = 0, tstepLR = 0;
+  bool rvLR = false;
+  if constexpr (LR) {
+    rblr = row_buffer(p.dtl, b, L, p.lowrank, ES);
+    lowrank_offsets(p.dtl, p.lowrank, lane, ES, offLR, tstepLR, rvLR);
+    lowrank_weights<float, CW>(S.wr, p.dtw, p.lowrank, dw, D, lane);
+  }
+
+  // Loads run one chunk ahead of the walk (chunks go from the last to the first): a chunk's
+  // tiles are requested as soon as the previous chunk is staged.  Every load is unconditional,
+  // and a chunk k < k0 re-reads chunk k0 and is inert.
+  auto load = [&](Tiles &T, int k) {
+    const int kc = k < k0 ? k0 : k;
+    const int t0 = kc * CK;
+    if constexpr (LR) T.lr.load(rblr, offLR + (uint32_t)(t0 * (int)p.dtl.s1 * ES), tstepLR, rvLR);
+    if constexpr (UL) {
+      const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES), tb_ = (uint32_t)(t0 * (int)vB.s1 * ES);
+      if constexpr (!SUM) T.x.v = buf_load_s<IT>(rbx, offX, tx_);
+      if constexpr (!LR) T.dt.v = buf_load_s<IT>(rbdt, offX, tx_);
+      T.g.v = buf_load_s<IT>(rbg, offX, tx_);
+      T.z.v = buf_load_s<IT>(rbz, offZ, (uint32_t)(t0 * (int)vzl.s1 * ES));
+      if constexpr (!SUM) {
+#pragma unroll
+        for (int i = 0; i < EB; ++i) T.B.v[i] = buf_load_s<IT>(rbB, offB[i], tb_);
+      }
+#pragma unroll
+      for (int i = 0; i < EB; ++i) T.C.v[i] = buf_load_s<IT>(rbC, offB[i], tb_);
+      if constexpr (!SUM) {
+        T.yp.v = buf_load_s<float>(rby, offY, (uint32_t)kc * tstepY);
+        T.ck = buf_load_s<float>(rbk, offK, (uint32_t)((kc > 0 ? kc - 1 : 0) * (int)p.D * NP * 4));
+      }
+    } else {
+      if constexpr (!SUM) T.x.load(vx, b, t0, L, dw, D, lane);
+      if constexpr (!LR) T.dt.load(vdt, b, t0, L, dw, D, lane);
+      T.g.load(vg, b, t0, L, dw, D, lane);
+      T.z.load(vzl, b, t0, L, dw, D, lane);
+      if constexpr (!SUM) T.B.load(vB, b, t0, L, 0, N, bt, lane);
+      T.C.load(vC, b, t0, L, 0, N, ctt, lane);
+      if constexpr (!SUM) {
+        T.yp.v = ypre ? ypre[ypre_index(!xt, b, min(t0 + tj, L - 1), min(dw + tc, D - 1), p.L, p.D)] : 0.0f;
+        T.ck = ((const float *)p.ckpt)[((b * p.nchunks + (kc > 0 ? kc - 1 : 0)) * p.D + (dval ? d : 0)) * NP + n];
+      }
+    }
+  };
+
+  float Rh[2];  // the half chunks' state sums: lane (r, j) holds step 8 h + j % 8, quantity j / 8
+  auto chunk = [&](Tiles &T, int k) {
+    const bool live = k >= k0;
+    const int t0 = (live ? k : k0) * CK;
+    const int Lc = live ? L : 0;
+    const bool ev = t0 + tj < Lc && tval;
+    const int par = k & 1;
+    // ------------------------------------------------------------ stage
+    if constexpr (!SUM) T.B.store(S.B, bt, lane, t0, Lc, 0, N);
+    T.C.store(S.C, ctt, lane, t0, Lc, 0, N);
+    const float xv = ev ? T.x.v : 0.0f;
+    float dv;
+    if constexpr (LR) {
+      T.lr.store(S.lr, lane);
+      wave_lds_sync();
+      float a_[kLR], w_[kLR];
+      lds_row(&S.lr[tj][0], a_);
+      lds_row(&S.wr[tc][0], w_);
+      dv = 0.0f;
+#pragma unroll
+      for (int r = 0; r < kLR; ++r) dv = fmaf(a_[r], w_[r], dv);
+    } else {
+      dv = T.dt.v;
+    }
+    dv += biasv;
+    float sgv = 1.0f;
+    if (p.softplus) {
+      sgv = sigmoidf(dv);
+      dv = softplusf(dv);
+    }
+    dv = ev ? dv : 0.0f;
+    // dy = dout silu(z); dz = dout (y + D x) silu'(z) from the saved pre-gate output
+    const float g0 = ev ? T.g.v : 0.0f;
+    float dyv = g0;
+    if (p.has_z) {
+      const float zv = T.z.v, sz = sigmoidf(zv);
+      dyv = g0 * (zv * sz);
+      if constexpr (!SUM) {
+        const float dzv = g0 * T.yp.v * sz * (1.0f + zv * (1.0f - sz));
+        if constexpr (UL) {
+          buf_store_s<IT>(row_buffer(vdz, b, L, D, ES), offDZ, (uint32_t)(t0 * (int)vdz.s1 * ES), ev && G::lead(lane),
+                          dzv);
+        } else if (ev && G::lead(lane)) {
+          Conv<IT>::store(vpw<IT>(vdz) + b * vdz.s0 + (int64_t)(t0 + tj) * vdz.s1 + (int64_t)(dw + tc) * vdz.s2, dzv);
+        }
+      }
+    }
+    const float hstart = k <= 0 ? h0v : T.ck;
+    wave_lds_sync();
+    load(T, k - 1);
+
+    // ------------------------------------------------------------ recompute the chunk's states
+    float am[CK], bx[CK], hh[CK + 1];
+    if constexpr (!SUM) hh[0] = hstart;
+    static_for<0, CK>([&](auto tcst) {
+      constexpr int t = decltype(tcst)::value;
+      const float dtb = row_bcast<t>(dv);
+      float cf;
+      if constexpr (M1) {
+        am[t] = zoh_am1(dtb, ac);
+      } else {
+        disc<METHOD>(dtb, ac, am[t], cf);
+      }
+      if constexpr (!SUM) {
+        bx[t] = S.B[n][t] * row_bcast<t>(xv);
+        if constexpr (M1) hh[t + 1] = fmaf(am[t], fmaf(bx[t], ac.invA, hh[t]), hh[t]);
+        else hh[t + 1] = fmaf(am[t], hh[t], bcoef<METHOD>(dtb, cf) * bx[t]);
+      }
+    });
+
+    // ------------------------------------------------------------ walk back, half a chunk at a time
+    // The walk broadcasts delta and x again rather than keeping the recompute's 2 x 16 values
+    // live (tied to the adjoint: the compiler cannot reuse them).
+    float dvw = dv, xvw = xv;
+    order_after(dvw, lamf);
+    order_after(xvw, lamf);
+    static_for_down<0, CK / RH>([&](auto hcst) {
+      constexpr int half = decltype(hcst)::value;
+      float rC[RH], rB[RH];
+      lds_row(&S.C[n][half * RH], rC);
+      if constexpr (!SUM) lds_row(&S.B[n][half * RH], rB);
+      static_for_down<0, RH>([&](auto tcst) {
+        constexpr int tt = decltype(tcst)::value;
+        constexpr int t = half * RH + tt;
+        const float dyb = row_bcast<t>(dyv);
+        const float gC = dyb * rC[tt];
+        // lambda_t = dy_t C_t + a_{t+1} lambda_{t+1}
+        if constexpr (M1) {
+          lam += (double)fmaf(m_next, lamf, gC);
+        } else {
+          lam = fma((double)m_next, lam, (double)gC);
+        }
+        lamf = (float)lam;
+        m_next = am[t];
+        if constexpr (SUM) {
+          if constexpr (M1) prod = fmaf(am[t], prod, prod);
+          else prod *= am[t];
+        } else {
+          const float dtb = row_bcast<t>(dvw);
+          float cf, pD;
+          if constexpr (M1) {
+            cf = am[t] * ac.invA;
+            pD = lamf * fmaf(ac.A, hh[t + 1], bx[t]);  // a (A h_{t-1} + B x) = A h_t + B x
+          } else {
+            float a_, u_;
+            disc<METHOD>(dtb, ac, a_, u_);
+            cf = bcoef<METHOD>(dtb, u_);
+            if constexpr (METHOD == 1) pD = fmaf(lamf * a_ * ac.A, hh[t], lamf * bx[t]);
+            else pD = lamf * (u_ * u_) * fmaf(ac.A, hh[t], bx[t]);
+          }
+          const float dhc = lamf * cf;
+          // A dA = sum_t (dt pD - lambda b): a and b depend on A only through dt A (see k_bwd)
+          dA_acc = fmaf(dtb, pD, fmaf(-dhc, bx[t], dA_acc));
+          S.pn[tt][c][0][n] = dhc * rB[tt];
+          S.pn[tt][c][1][n] = pD;
+          S.pd[tt][c][n][0] = dhc * row_bcast<t>(xvw);
+          S.pd[tt][c][n][1] = dyb * hh[t + 1];
+        }
+      });
+      if constexpr (!SUM) {
+        wave_lds_sync();
+        // (dx, ddelta) of step 8 half + j % 8: lane (r, j) sums quantity j / 8 over the states
+        {
+          float part[NP];
+          lds_row(&S.pn[tj % RH][tc][tj / RH][0], part);
+          float sum = 0.0f;
+#pragma unroll
+          for (int j = 0; j < NP; ++j) sum += part[j];
+          Rh[half] = sum;
+        }
+        // (dB, dC): sum over the wavefront's channels, then over the workgroup's wavefronts
+        constexpr int NI = (RH * NP * 2 + kWave - 1) / kWave;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int e = lane + i * kWave;
+          if (e < RH * NP * 2) {
+            const int q = e % 2, nn = (e / 2) % NP, st = e / (2 * NP);
+            float v = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CW; ++j) v += S.pd[st][j][nn][q];
+            dbc[half][wv][st][nn][q] = v;
+          }
+        }
+        lds_barrier();
+        for (int e = tid; e < RH * NP * 2; e += NT) {
+          const int q = e % 2, nn = (e / 2) % NP, st = e / (2 * NP);
+          const int tg = t0 + half * RH + st;
+          float v = 0.0f;
+#pragma unroll
+          for (int w = 0; w < WPB; ++w) v += dbc[half][w][st][nn][q];
+          if (tg < Lc) ((float *)(q == 0 ? p.ws_dB : p.ws_dC))[((b * p.ntiles + tile) * p.L + tg) * NP + nn] = v;
+        }
+      }
+    });
+    (void)par;
+    if constexpr (SUM) {
+      wave_lds_sync();
+      return;
+    }
+    // ------------------------------------------------------------ stores (row-tile lanes)
+    // both shifts run with every lane active (a select around a DPP move could otherwise become
+    // a masked branch, whose shift would read disabled lanes)
+    float sh = row_shr8(Rh[1]), sl = row_shl8(Rh[0]);
+    asm volatile("" : "+v"(sh), "+v"(sl));
+    const float dxs = tj < RH ? Rh[0] : sh;
+    const float dds = tj < RH ? sl : Rh[1];
+    const float dxo = fmaf(dyv, dskv, dxs);
+    const float ddo = dds * sgv;
+    dDp = fmaf(dyv, xv, dDp);
+    dbp += ev ? ddo : 0.0f;  // padded / inert steps carry state terms but no gradient
+    const bool st = ev && G::lead(lane);
+    if constexpr (UL) {
+      const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES);
+      buf_store_s<IT>(row_buffer(vdx, b, L, D, ES), offX, tx_, st, dxo);
+      buf_store_s<IT>(row_buffer(vddt, b, L, D, ES), offX, tx_, st, ddo);
+    } else if (st) {
+      const int tg = t0 + tj, dd = dw + tc;
+      Conv<IT>::store(vpw<IT>(vdx) + b * vdx.s0 + (int64_t)tg * vdx.s1 + (int64_t)dd * vdx.s2, dxo);
+      Conv<IT>::store(vpw<IT>(vddt) + b * vddt.s0 + (int64_t)tg * vddt.s1 + (int64_t)dd * vddt.s2, ddo);
+    }
+    wave_lds_sync();
+  };
+
+  Tiles T0;
+  load(T0, k1 - 1);
+  chunk(T0, k1 - 1);
+  for (int k = k1 - 2; k >= k0 - 1; --k) chunk(T0, k);  // ends on an inert chunk
+
+  // lambda a of the segment's first step (an inert chunk after it already applied it: m_next = 0)
+  const double lam_a = M1 ? lam + (double)m_next * lam : lam * (double)m_next;
+  if constexpr (SUM) {
+    if (dval && nval) {
+      ((double *)p.seg_E)[sidx] = lam_a;
+      ((float *)p.seg_P)[sidx] = prod;
+    }
+    return;
+  } else {
+    if (dval) ((float *)p.ws_dA)[sidx] = dA_acc * ac.invA;
+    if (p.has_dh0 && dval && nval && seg == 0)
+      vstore<float>(p.dh0, b * p.dh0.s0 + d * p.dh0.s1 + n * p.dh0.s2, (float)lam_a);
+    // dD and d_bias: the lead row's lanes hold one step slot each; sum them (fixed order)
+    const float sD = row_sum(dDp), sb = row_sum(dbp);
+    if (G::lead(lane) && tj == 0 && tval) {
+      ((float *)p.ws_dD)[(b * p.nseg + seg) * p.D + dw + tc] = sD;
+      ((float *)p.ws_db)[(b * p.nseg + seg) * p.D + dw + tc] = sb;
+    }
+  }
+}
+
+// The adjoint entering each time segment's last step, from the last segment to the first:
+// mu[nseg - 1] = dlast (or 0), mu[s - 1] = E[s] + P[s] mu[s]  (float64), one lane per (b, d, n).
+template <int NP>
+__global__ void __launch_bounds__(kThreads) k_bwd_carry(const BwdParams p) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= p.B * p.D * NP) return;
+  const int n = (int)(i % NP);
+  const int64_t d = (i / NP) % p.D, b = i / (NP * p.D);
+  if (n >= p.N) return;
+  double mu = p.has_dlast ? (double)vload<float>(p.dlast, b * p.dlast.s0 + d * p.dlast.s1 + n * p.dlast.s2) : 0.0;
+  for (int s = p.nseg - 1; s >= 0; --s) {
+    const int64_t k = ((b * p.nseg + s) * p.D + d) * NP + n;
+    ((double *)p.seg_mu)[k] = mu;
+    if (s > 0) mu = ((const double *)p.seg_E)[k] + (double)((const float *)p.seg_P)[k] * mu;
+  }
+}
+
+template <typename IT, int NP, int M, bool SUM, bool LR>
+static void bwdw_pass(const BwdParams &p, dim3 grid, hipStream_t s) {
+  if (p.uniform) hipLaunchKernelGGL((k_bwdw<IT, NP, M, true, SUM, LR>), grid, dim3(kWave * bwdw_waves(NP)), 0, s, p);
+  else hipLaunchKernelGGL((k_bwdw<IT, NP, M, false, SUM, LR>), grid, dim3(kWave * bwdw_waves(NP)), 0, s, p);
+}
+
+template <typename IT, int NP, int M, bool LR>
+static hipError_t launch_bwdw_lr(const BwdParams &p, hipStream_t s) {
+  dim3 grid((unsigned)p.ntiles, (unsigned)(p.B * p.nseg));
+  if (p.nseg > 1) {
+    bwdw_pass<IT, NP, M, true, LR>(p, grid, s);
+    const int64_t lanes = p.B * p.D * NP;
+    hipLaunchKernelGGL((k_bwd_carry<NP>), dim3((unsigned)((lanes + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
+                       p);
+  }
+  bwdw_pass<IT, NP, M, false, LR>(p, grid, s);
+  return hipGetLastError();
 }
 
 template <typename IT, int NP, int M>
 static hipError_t launch_bwd_t(const BwdParams &p, hipStream_t s) {
   typedef typename Conv<IT>::CT CT;
-  constexpr int WPB = bwd_waves(sizeof(CT), NP);
-  constexpr int DT = WPB * (kWave / NP);
-  if (p.ntiles != (int)((p.D + DT - 1) / DT)) return hipErrorInvalidValue;
-  dim3 grid((unsigned)p.ntiles, (unsigned)p.B);
-  if constexpr (NP <= 16 && sizeof(IT) <= 4) {  // the low-rank delta kernels (see launch_fwd)
-    if (p.lowrank) {
-      if (p.uniform) hipLaunchKernelGGL((k_bwd<IT, NP, M, true, true>), grid, dim3(WPB * kWave), 0, s, p);
-      else hipLaunchKernelGGL((k_bwd<IT, NP, M, false, true>), grid, dim3(WPB * kWave), 0, s, p);
-      return hipGetLastError();
+  if constexpr (sizeof(IT) == 8) {  // float64: the register-staged kernel
+    constexpr int WPB = bwd_waves(sizeof(CT), NP);
+    constexpr int DT = WPB * (kWave / NP);
+    if (p.ntiles != (int)((p.D + DT - 1) / DT) || p.nseg != 1 || p.lowrank) return hipErrorInvalidValue;
+    dim3 grid((unsigned)p.ntiles, (unsigned)p.B);
+    if (p.uniform) hipLaunchKernelGGL((k_bwd<IT, NP, M, true, false>), grid, dim3(WPB * kWave), 0, s, p);
+    else hipLaunchKernelGGL((k_bwd<IT, NP, M, false, false>), grid, dim3(WPB * kWave), 0, s, p);
+    return hipGetLastError();
+  } else {
+    constexpr int DT = bwdw_waves(NP) * (kWave / NP);
+    if (p.ntiles != (int)((p.D + DT - 1) / DT)) return hipErrorInvalidValue;
+    if constexpr (NP <= 16) {  // the low-rank delta kernels (see launch_fwd)
+      if (p.lowrank) return launch_bwdw_lr<IT, NP, M, true>(p, s);
     }
+    if (p.lowrank) return hipErrorInvalidValue;
+    return launch_bwdw_lr<IT, NP, M, false>(p, s);
   }
-  if (p.lowrank) return hipErrorInvalidValue;
-  if (p.uniform) hipLaunchKernelGGL((k_bwd<IT, NP, M, true, false>), grid, dim3(WPB * kWave), 0, s, p);
-  else hipLaunchKernelGGL((k_bwd<IT, NP, M, false, false>), grid, dim3(WPB * kWave), 0, s, p);
-  return hipGetLastError();
 }
 
 template <typename IT, int NP>
@@ -574,8 +973,11 @@ static hipError_t launch_bwd_m(const BwdParams &p, int method, hipStream_t s) {
 
 template <typename IT>
 static hipError_t launch_bwd_n(const BwdParams &p, int method, int np, hipStream_t s) {
+  if (np != fused_np(p.N, sizeof(IT) == 8 ? 3 : 0)) return hipErrorInvalidValue;
   switch (np) {
-    case 8: return launch_bwd_m<IT, 8>(p, method, s);
+    case 8:
+      if constexpr (sizeof(IT) == 8) return launch_bwd_m<IT, 8>(p, method, s);
+      return hipErrorInvalidValue;
     case 16: return launch_bwd_m<IT, 16>(p, method, s);
     case 32: return launch_bwd_m<IT, 32>(p, method, s);
     default: return launch_bwd_m<IT, 64>(p, method, s);

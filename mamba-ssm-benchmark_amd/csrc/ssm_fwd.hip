@@ -26,6 +26,7 @@
 // its decays; a carry kernel scans the (product, end state) pairs per (b, d, n); the main pass
 // then restarts every segment from the state that enters it.
 #include "ssm_device.hpp"
+#include "ssm_dpp.hpp"
 #include "ssm_internal.hpp"
 #include "ssm_tiles.hpp"
 #include "ssm_wave.hpp"
@@ -280,16 +281,278 @@ __global__ void __launch_bounds__(kThreads) k_fwd_carry(const FwdParams p) {
   }
 }
 
+// ------------------------------------------------------------------ float kernels (row tiles)
+// The float-compute forward (float32 / bf16 / fp16 inputs, float32 state).  Same mapping and
+// chunk walk as k_fwd, with two changes for gfx950's issue model (a wavefront issues at most one
+// VALU instruction every few cycles, a dependent one later still, and at B16 D512 N16 only two
+// wavefronts share a SIMD):
+//   * the per-(step, channel) inputs x, delta and the gate stay in one register per lane (a
+//     row tile, ssm_dpp.hpp) and reach each step's lanes by DPP row broadcast, so only B, C
+//     and the C h partials pass through LDS;
+//   * the chunk loop is software-pipelined: iteration k runs the serial state updates of chunk
+//     k - 1 interleaved step by step with the independent per-step work of chunk k (exp,
+//     expm1, B x), so most instructions have their operands ready when they issue.
+// NP >= 16 (a smaller dstate is padded to 16).
+template <int NP>
+struct FwdwLds {
+  static constexpr int CW = kWave / NP, CKP = ck_pad(4), NPP = np_pad(4, NP);
+  float B[NP][CKP];
+  float C[NP][CKP];
+  float y[kCK][CW][NPP];
+  float lr[kCK][lr_pad(4)];  // low-rank delta input rows of the chunk
+  float wr[CW][lr_pad(4)];   // low-rank weight rows of the wavefront's channels
+};
+constexpr int kFwdwWaves = 4;
+
+// Per-chunk values between the independent phase (iteration k) and the serial phase (k + 1).
+template <bool SUM>
+struct FwdwStage {
+  float m[kCK];  // ZOH: a - 1 (expm1); other methods: a
+  float u[kCK];  // ZOH: B x / A; other methods: b
+  float C[SUM ? 1 : kCK];
+  float x, z;    // the lane's row-tile element of x and the gate
+};
+
+template <typename IT, int NP, int METHOD, bool UL, bool SUM, bool LR>
+__global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) {
+  typedef FwdwLds<NP> WL;
+  typedef RowGeo<NP> G;
+  typedef RowTile<IT, NP, UL> RT;
+  typedef FwdwStage<SUM> ST;
+  constexpr int CW = G::CW, CK = kCK, WPB = kFwdwWaves;
+  __shared__ __align__(16) WL lds_all[WPB];
+
+  const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  WL &S = lds_all[wv];
+  const int c = lane / NP, n = lane % NP;              // the lane's state h[c][n]
+  const int tj = G::step(lane), tc = G::chan(lane);    // the lane's row-tile element (step tj, channel tc)
+  const int64_t b = blockIdx.y / p.nseg;
+  const int seg = (int)(blockIdx.y % p.nseg);
+  if (SUM && seg == p.nseg - 1) return;  // the last segment's summary is never used
+  const int k0 = seg * p.seg_chunks;
+  const int k1 = k0 + p.seg_chunks < p.nchunks ? k0 + p.seg_chunks : p.nchunks;
+  const int dw = (blockIdx.x * WPB + wv) * CW;  // first channel of this wavefront
+  const int d = dw + c;
+  const bool dval = d < p.D, nval = n < p.N;
+  const int L = (int)p.L, D = (int)p.D, N = (int)p.N;
+  const bool tval = dw + tc < D;  // the row-tile element's channel exists
+
+  float Av = -1.0f;
+  if (dval && nval) {
+    Av = vload<float>(p.A, d * p.A.s0 + n * p.A.s1);
+    if (p.a_log) Av = -__expf(Av);  // models/mamba.py:81
+  }
+  const AConst<float> ac = make_aconst(Av);
+  float h = 0.0f, prod = 1.0f;
+  const int64_t sidx = ((b * p.nseg + seg) * p.D + d) * NP + n;  // (B, nseg, D, NP) summaries
+  if (!SUM && dval && nval) {
+    if (p.nseg > 1) h = ((const float *)p.seg_hin)[sidx];
+    else if (p.has_h0) h = vload<float>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
+  }
+  const float biasv = p.has_bias && tval ? vload<float>(p.bias, (int64_t)(dw + tc) * p.bias.s0) : 0.0f;
+  const float dskv = p.has_D && tval ? vload<float>(p.Dsk, (int64_t)(dw + tc) * p.Dsk.s0) : 0.0f;
+
+  const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = p.z;  // z keeps its own strides
+  const KView vout = with_layout<UL>(p.out, p.x), vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
+  const bool xt = vx.s1 == 1, bt = vB.s1 == 1, ctt = vC.s1 == 1;
+  const bool zt = p.has_z && p.write_out && !SUM;
+  const KView vzl = zt ? vz : vx;  // without a gate the z tile re-reads x (never used)
+  struct Tiles {
+    RT x, dt, z;
+    WaveTile<IT, float, CK, NP, UL> B, C;
+    LowRankTile<IT, float, CK> lr;
+  };
+  constexpr int ES = (int)sizeof(IT), EB = WaveTile<IT, float, CK, NP, UL>::E;
+  const uint32_t offX = RT::offset(vx, dw, lane), offZ = RT::offset(vzl, dw, lane);
+  uint32_t offB[EB];
+  tile_offsets<CK, NP>(offB, vB, 0, bt, lane, ES);
+  const __amdgpu_buffer_rsrc_t empty = __builtin_amdgcn_make_buffer_rsrc((void *)p.x.p, (short)0, 0, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbdt = LR ? empty : row_buffer(vdt, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbz = row_buffer(vzl, b, L, D, ES);
+  const __amdgpu_buffer_rsrc_t rbB = row_buffer(vB, b, L, N, ES), rbC = row_buffer(vC, b, L, N, ES);
+  __amdgpu_buffer_rsrc_t rblr = empty;
+  uint32_t offLR = 0, tstepLR = 0;
+  bool rvLR = false;
+  if constexpr (LR) {
+    rblr = row_buffer(p.dtl, b, L, p.lowrank, ES);
+    lowrank_offsets(p.dtl, p.lowrank, lane, ES, offLR, tstepLR, rvLR);
+    lowrank_weights<float, CW>(S.wr, p.dtw, p.lowrank, dw, D, lane);
+  }
+  // Stores of the uniform layout go through buffers over one batch row (the host keeps each
+  // below 2^31 bytes): the output, the saved pre-gate output and the chunk states.
+  const int64_t ckrow = (int64_t)p.nchunks * p.D * NP;
+  const __amdgpu_buffer_rsrc_t rbo = p.write_out ? row_buffer(vout, b, L, D, ES) : empty;
+  const __amdgpu_buffer_rsrc_t rby = flat_buffer(p.ypre ? (const float *)p.ypre + b * p.L * p.D : p.x.p,
+                                                 p.ypre ? p.L * p.D * 4 : 0);
+  const __amdgpu_buffer_rsrc_t rbk = flat_buffer(p.ckpt ? (const float *)p.ckpt + b * ckrow : p.x.p,
+                                                 p.ckpt ? ckrow * 4 : 0);
+  const uint32_t offO = RT::offset(vout, dw, lane);
+  const uint32_t offY = (uint32_t)(ypre_index(!xt, 0, tj, dw + tc, p.L, p.D) * 4);
+  const uint32_t tstepY = (uint32_t)((xt ? 1 : (int)p.D) * CK * 4);
+  const uint32_t offK = (uint32_t)(((int64_t)d * NP + n) * 4);
+  // Every load is unconditional (branch-free), two chunks ahead of the chunk being staged; past
+  // the segment's end the prefetch re-reads its last chunk.
+  auto load = [&](Tiles &T, int k) {
+    const int t0 = (k < k1 ? k : k1 - 1) * CK;
+    if constexpr (LR) T.lr.load(rblr, offLR + (uint32_t)(t0 * (int)p.dtl.s1 * ES), tstepLR, rvLR);
+    if constexpr (UL) {
+      const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES), tb_ = (uint32_t)(t0 * (int)vB.s1 * ES);
+      T.x.load_buf(rbx, offX, tx_);
+      if constexpr (!LR) T.dt.load_buf(rbdt, offX, tx_);
+      T.B.load_buf(rbB, offB, tb_);
+      if (!SUM) T.C.load_buf(rbC, offB, tb_);
+      if (!SUM) T.z.load_buf(rbz, offZ, (uint32_t)(t0 * (int)vzl.s1 * ES));
+    } else {
+      T.x.load(vx, b, t0, L, dw, D, lane);
+      if constexpr (!LR) T.dt.load(vdt, b, t0, L, dw, D, lane);
+      T.B.load(vB, b, t0, L, 0, N, bt, lane);
+      if (!SUM) T.C.load(vC, b, t0, L, 0, N, ctt, lane);
+      if (!SUM) T.z.load(vzl, b, t0, L, dw, D, lane);
+    }
+  };
+
+  // Iteration k: stage chunk k (inert past k1: zero inputs, a = 1, b = 0) and compute its
+  // independent per-step values into `nx`, interleaved with the serial updates of chunk k - 1
+  // from `pv` (inert before k0); then the outputs of chunk k - 1.
+  auto iter = [&](Tiles &T, int k, ST &pv, ST &nx) {
+    const int t0 = k * CK;
+    const int Lc = k < k1 ? L : 0;
+    const bool ev = t0 + tj < Lc && tval;  // the row-tile element is a real (step, channel)
+    T.B.store(S.B, bt, lane, t0, Lc, 0, N);
+    if (!SUM) T.C.store(S.C, ctt, lane, t0, Lc, 0, N);
+    nx.x = ev ? T.x.v : 0.0f;
+    nx.z = T.z.v;
+    float dv;
+    if constexpr (LR) {
+      T.lr.store(S.lr, lane);
+      wave_lds_sync();
+      float a_[kLR], w_[kLR];
+      lds_row(&S.lr[tj][0], a_);
+      lds_row(&S.wr[tc][0], w_);
+      dv = 0.0f;
+#pragma unroll
+      for (int r = 0; r < kLR; ++r) dv = fmaf(a_[r], w_[r], dv);
+    } else {
+      dv = T.dt.v;
+    }
+    dv += biasv;
+    if (p.softplus) dv = softplusf(dv);
+    dv = ev ? dv : 0.0f;  // padded steps: delta 0 is the identity step
+    const float xv = nx.x;
+    wave_lds_sync();
+    load(T, k + 2);
+    float rB[CK];
+    lds_row(&S.B[n][0], rB);
+    if constexpr (!SUM) lds_row(&S.C[n][0], nx.C);
+
+    // Scheduling window: step t's independent work follows the update of step t - 2, and the
+    // update of step t follows the independent work of step t - 2 (ties, no instructions).
+    float dvs = dv, xvs = xv, hl1 = h, hl2 = h;
+    static_for<0, CK>([&](auto tcst) {
+      constexpr int t = decltype(tcst)::value;
+      if constexpr (t >= 2) {
+        order_after(dvs, hl2);
+        order_after(xvs, hl2);
+        order_after(h, nx.m[t - 2], nx.u[t - 2]);
+      }
+      // serial update of chunk k - 1 (ZOH: h <- h + (a - 1)(h + B x / A))
+      if constexpr (METHOD == 0) {
+        h = fmaf(pv.m[t], h + pv.u[t], h);
+        if constexpr (SUM) prod = fmaf(pv.m[t], prod, prod);
+      } else {
+        h = fmaf(pv.m[t], h, pv.u[t]);
+        if constexpr (SUM) prod *= pv.m[t];
+      }
+      if constexpr (!SUM) S.y[t][c][n] = pv.C[t] * h;
+      // independent values of chunk k
+      const float dtb = row_bcast<t>(dvs);
+      const float bxr = rB[t] * row_bcast<t>(xvs);
+      if constexpr (METHOD == 0) {
+        nx.m[t] = zoh_am1(dtb, ac);
+        nx.u[t] = bxr * ac.invA;
+      } else {
+        float coef;
+        disc<METHOD>(dtb, ac, nx.m[t], coef);
+        nx.u[t] = bcoef<METHOD>(dtb, coef) * bxr;
+      }
+      hl2 = hl1;
+      hl1 = h;
+    });
+    if constexpr (SUM) {
+      wave_lds_sync();
+      return;
+    }
+    const int kp = k - 1;  // the chunk whose outputs are now complete
+    const bool live = kp >= k0 && kp < k1;
+    wave_lds_sync();
+    // outputs of chunk k - 1: the lane of (step tj, channel tc) sums the partials over the states
+    float part[NP];
+    lds_row(&S.y[tj][tc][0], part);
+    float y = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) y += part[j];
+    const int tg = kp * CK + tj, dd = dw + tc;
+    const bool st = live && G::lead(lane) && tg < L && tval;
+    const float o0 = y + dskv * pv.x;
+    const float o = p.has_z ? o0 * (pv.z * sigmoidf(pv.z)) : o0;
+    if constexpr (UL) {  // branch-free: masked lanes store out of range (dropped)
+      const uint32_t kpc = (uint32_t)(kp < 0 ? 0 : kp);
+      buf_store<float>(rbk, offK + kpc * (uint32_t)(p.D * NP * 4), dval && live, h);
+      buf_store<float>(rby, offY + kpc * tstepY, st, o0);
+      buf_store<IT>(rbo, offO + kpc * (uint32_t)(CK * (int)vout.s1 * ES), st, o);
+    } else {
+      if (p.ckpt && dval && live) ((float *)p.ckpt)[((b * p.nchunks + kp) * p.D + d) * NP + n] = h;
+      if (st) {
+        if (p.ypre) ((float *)p.ypre)[ypre_index(!xt, b, tg, dd, p.L, p.D)] = o0;
+        if (p.write_out) Conv<IT>::store(vpw<IT>(vout) + b * vout.s0 + row_off<UL>(tg, dd, vout.s1, vout.s2), o);
+      }
+    }
+    wave_lds_sync();
+  };
+
+  Tiles T0, T1;
+  ST P0, P1;
+#pragma unroll
+  for (int t = 0; t < CK; ++t) {  // inert chunk k0 - 1: a - 1 = 0 (ZOH) / a = 1, b = 0
+    P1.m[t] = METHOD == 0 ? 0.0f : 1.0f;
+    P1.u[t] = 0.0f;
+    if constexpr (!SUM) P1.C[t] = 0.0f;
+  }
+  P1.x = P1.z = 0.0f;
+  load(T0, k0);
+  load(T1, k0 + 1);
+  for (int k = k0; k <= k1; k += 2) {
+    iter(T0, k, P1, P0);
+    iter(T1, k + 1, P0, P1);
+  }
+
+  if constexpr (SUM) {
+    if (dval && nval) {
+      ((float *)p.seg_P)[sidx] = prod;
+      ((float *)p.seg_E)[sidx] = h;
+    }
+  } else if (p.has_last && dval && nval && seg == p.nseg - 1) {
+    vstore<float>(p.last, b * p.last.s0 + d * p.last.s1 + n * p.last.s2, h);
+  }
+}
+
+// ------------------------------------------------------------------ launchers
 template <typename IT, int NP, int M, bool SUM, bool LR>
 static void fwd_pass(const FwdParams &p, dim3 grid, dim3 block, hipStream_t s) {
-  if (p.uniform) hipLaunchKernelGGL((k_fwd<IT, NP, M, true, SUM, LR>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((k_fwd<IT, NP, M, false, SUM, LR>), grid, block, 0, s, p);
+  if constexpr (sizeof(IT) == 8) {
+    if (p.uniform) hipLaunchKernelGGL((k_fwd<IT, NP, M, true, SUM, LR>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((k_fwd<IT, NP, M, false, SUM, LR>), grid, block, 0, s, p);
+  } else {
+    if (p.uniform) hipLaunchKernelGGL((k_fwdw<IT, NP, M, true, SUM, LR>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((k_fwdw<IT, NP, M, false, SUM, LR>), grid, block, 0, s, p);
+  }
 }
 
 template <typename IT, int NP, int M, bool LR>
 static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
   typedef typename Conv<IT>::CT CT;
-  constexpr int WPB = fwd_waves(sizeof(CT), NP);
+  constexpr int WPB = sizeof(IT) == 8 ? fwd_waves(sizeof(CT), NP) : kFwdwWaves;
   constexpr int DT = WPB * (kWave / NP);
   dim3 grid((unsigned)((p.D + DT - 1) / DT), (unsigned)(p.B * p.nseg));
   if (p.nseg > 1) {
@@ -322,10 +585,14 @@ static hipError_t launch_fwd_m(const FwdParams &p, int method, hipStream_t s) {
   }
 }
 
+// Float compute pads the state to at least 16 (row tiles); float64 keeps 8.
 template <typename IT>
 static hipError_t launch_fwd_n(const FwdParams &p, int method, int np, hipStream_t s) {
+  if (np != fused_np(p.N, sizeof(IT) == 8 ? 3 : 0)) return hipErrorInvalidValue;
   switch (np) {
-    case 8: return launch_fwd_m<IT, 8>(p, method, s);
+    case 8:
+      if constexpr (sizeof(IT) == 8) return launch_fwd_m<IT, 8>(p, method, s);
+      return hipErrorInvalidValue;
     case 16: return launch_fwd_m<IT, 16>(p, method, s);
     case 32: return launch_fwd_m<IT, 32>(p, method, s);
     default: return launch_fwd_m<IT, 64>(p, method, s);

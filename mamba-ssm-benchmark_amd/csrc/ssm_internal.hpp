@@ -19,6 +19,12 @@ constexpr int kCK = 16;
 constexpr int kThreads = 256;  // threads per workgroup of the simple (non-scan) kernels
 inline int chunk_steps(int) { return kCK; }
 inline int padded_n(int64_t n) { return n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32 : 64; }
+// State padding of the fused kernels: the float-compute kernels use row tiles (at least 16
+// states per channel); float64 (dtype code 3) keeps the 8-state minimum.
+inline int fused_np(int64_t n, int dtype) {
+  const int np = padded_n(n);
+  return dtype == 3 || np >= 16 ? np : 16;
+}
 // LDS rows read with 16-byte vector loads by lanes of different rows are padded by 16 bytes,
 // which spreads the lanes of a read over distinct banks.
 __host__ __device__ constexpr int ck_pad(int s) { return kCK + 16 / s; }
@@ -52,10 +58,12 @@ __host__ __device__ constexpr int bwd_fits(int s, int np, int w) {
 __host__ __device__ constexpr int bwd_waves(int s, int np) {
   return bwd_fits(s, np, 8) ? 8 : bwd_fits(s, np, 4) ? 4 : bwd_fits(s, np, 2) ? 2 : 1;
 }
+// Wavefronts per workgroup of the float-compute backward (row tiles, NP >= 16).
+__host__ __device__ constexpr int bwdw_waves(int np) { return np <= 32 ? 8 : 4; }
 // Channels per backward workgroup (= the channel tile of the dB / dC partial sums).
 inline int bwd_channels_per_block(int dtype, int np) {
-  const int s = dtype == 3 ? 8 : 4;
-  return bwd_waves(s, np) * (64 / np);
+  if (dtype == 3) return bwd_waves(8, np) * (64 / np);
+  return bwdw_waves(np) * (64 / np);
 }
 
 struct FwdParams {
@@ -90,6 +98,13 @@ __host__ __device__ inline int64_t ypre_index(bool dfast, int64_t b, int64_t t, 
 struct BwdParams {
   int64_t B, L, D, N;
   int nchunks, ntiles;
+  // Time segments (float kernels): grid row blockIdx.y = b * nseg + segment.  With nseg > 1 a
+  // summary pass writes each segment's (E, P) = (first-step decay times its zero-start adjoint,
+  // product of its decays), k_bwd_carry turns them into the adjoint entering each segment
+  // (seg_mu), and every partial over time (dA, dD, d_bias) gets one row per (b, segment).
+  int nseg, seg_chunks;
+  void *seg_mu, *seg_E;  // (B, nseg, D, NP) float64
+  void *seg_P;           // (B, nseg, D, NP) float32
   int softplus;
   int has_D, has_z, has_bias, has_h0, has_dlast, has_dh0;
   int uniform;  // as in FwdParams
@@ -100,12 +115,13 @@ struct BwdParams {
   const void *ckpt;
   const void *ypre;
   void *ws_dB, *ws_dC;  // (B, ntiles, L, NP) partial sums over the tile's channels
-  void *ws_dA;          // (B, D, NP) partial over time
-  void *ws_dD, *ws_db;  // (B, D)
+  void *ws_dA;          // (B, nseg, D, NP) partial over time
+  void *ws_dD, *ws_db;  // (B, nseg, D)
 };
 
 struct FinParams {
   int64_t B, L, D, N;
+  int64_t rows;  // partial rows of dA / dD / d_bias: B * nseg
   int ntiles, np;
   int has_D, has_bias;
   int a_log;  // A holds A_log: dA is written as the gradient of A_log, dA * A

@@ -97,6 +97,54 @@ template <> __device__ __forceinline__ float buf_load<f16_t>(__amdgpu_buffer_rsr
 template <> __device__ __forceinline__ double buf_load<double>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
 }
+// The same with a uniform (scalar) offset added by the hardware: a chunk's offset costs no VALU.
+template <typename IT> __device__ __forceinline__ float buf_load_s(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff);
+template <> __device__ __forceinline__ float buf_load_s<float>(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, (int)soff, 0));
+}
+template <> __device__ __forceinline__ float buf_load_s<bf16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+  return __uint_as_float(((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, (int)soff, 0)) << 16);
+}
+template <> __device__ __forceinline__ float buf_load_s<f16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+  return (float)__builtin_bit_cast(f16_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, (int)soff, 0));
+}
+__device__ __forceinline__ double buf_load_f64s(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+  return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, (int)soff, 0));
+}
+
+// Raw buffer stores.  A lane whose `ok` is false stores to an offset past the buffer's extent
+// (every row buffer the host allows spans less than 2^31 bytes), which the hardware discards:
+// a masked store needs no branch, so a chunk's code stays one basic block.
+constexpr uint32_t kDropOffset = 0x80000000u;
+template <typename IT> __device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t off, bool ok, float v);
+template <> __device__ __forceinline__ void buf_store<float>(__amdgpu_buffer_rsrc_t r, uint32_t off, bool ok, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)(ok ? off : kDropOffset), 0, 0);
+}
+template <> __device__ __forceinline__ void buf_store<bf16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off, bool ok, float v) {
+  bf16_t q;
+  Conv<bf16_t>::store(&q, v);
+  __builtin_amdgcn_raw_buffer_store_b16(q.bits, r, (int)(ok ? off : kDropOffset), 0, 0);
+}
+template <> __device__ __forceinline__ void buf_store<f16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off, bool ok, float v) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16_t)v), r, (int)(ok ? off : kDropOffset), 0, 0);
+}
+// Masked store with a uniform offset added by the hardware (`ok` false: dropped).
+template <typename IT> __device__ __forceinline__ void buf_store_s(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff, bool ok, float v);
+template <> __device__ __forceinline__ void buf_store_s<float>(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff, bool ok, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)(ok ? off : kDropOffset), (int)soff, 0);
+}
+template <> __device__ __forceinline__ void buf_store_s<bf16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff, bool ok, float v) {
+  bf16_t q;
+  Conv<bf16_t>::store(&q, v);
+  __builtin_amdgcn_raw_buffer_store_b16(q.bits, r, (int)(ok ? off : kDropOffset), (int)soff, 0);
+}
+template <> __device__ __forceinline__ void buf_store_s<f16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff, bool ok, float v) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16_t)v), r, (int)(ok ? off : kDropOffset), (int)soff, 0);
+}
+// A buffer over `bytes` bytes at `base` (0 bytes: every access is dropped / reads 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t flat_buffer(const void *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, kBufferFlags);
+}
 
 // Byte offsets (at t0 = 0) of the tile elements a lane stages, for a view with element size `esize`.
 template <int ROWS, int COLS, int E>

@@ -11,7 +11,7 @@ import os
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssmscan.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, EINVAL, EKEY, ESPACE, EHIP = 0, 1, 2, 3, 4
 ZOH, EULER, BILINEAR = 0, 1, 2
@@ -45,7 +45,7 @@ class BwdArgs(ctypes.Structure):
                 ("method", c_i32), ("dtype", c_i32),
                 ("x", Tensor), ("delta", Tensor), ("A", Tensor), ("Bm", Tensor), ("Cm", Tensor),
                 ("Dskip", Tensor), ("z", Tensor), ("delta_bias", Tensor),
-                ("delta_softplus", c_i32), ("reserved0", c_i32),
+                ("delta_softplus", c_i32), ("segments", c_i32),
                 ("h0", Tensor), ("saved", c_vp), ("dout", Tensor), ("dlast", Tensor),
                 ("dx", Tensor), ("ddelta", Tensor), ("dA", Tensor), ("dBm", Tensor), ("dCm", Tensor),
                 ("dD", Tensor), ("dz", Tensor), ("ddelta_bias", Tensor), ("dh0", Tensor),

@@ -136,7 +136,8 @@ def scan_forward(x, delta, A, Bm, Cm, D, z, delta_bias, h0, method, delta_softpl
         stream = _abi.stream_handle(dev)
         rc = timed_launch("ssm_fwd", stream, lambda: lib.ssm_fwd(ctypes.byref(args), stream))
     _abi.check(rc, "ssm_fwd")
-    state = ((xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, Wv, saved), (method, bool(delta_softplus), io, ct, bool(A_is_log)))
+    state = ((xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, Wv, saved),
+             (method, bool(delta_softplus), io, ct, bool(A_is_log), int(segments or 0)))
     return out, last, state
 
 
@@ -146,7 +147,7 @@ def scan_backward(tensors, settings, dout, dlast, dz=None, dB=None, dC=None):
     Returns (dx, ddelta, dA, dB, dC, dD, dz, ddelta_bias, dh0); with a delta projection,
     ddelta is the gradient of the projected (B, L, D) delta."""
     xs, ds, As, Bs, Cs, Dv, zs, bv, h0v, Wv, saved = tensors
-    method, softplus, io, ct, a_log = settings
+    method, softplus, io, ct, a_log, segments = settings
     if dout is None:
         dout = torch.zeros(xs.shape, dtype=io, device=xs.device)
     dout = _cast_keep(dout, io)
@@ -167,6 +168,7 @@ def scan_backward(tensors, settings, dout, dlast, dz=None, dB=None, dC=None):
     args = _abi.BwdArgs()
     _fill_common(args, xs, ds, As, Bs, Cs, Dv, zs, bv, softplus, h0v, method, io)
     args.saved = saved.data_ptr()
+    args.segments = segments
     args.dout, args.dlast = _abi.view(dout), _abi.view(dlast)
     args.dx, args.ddelta, args.dA = _abi.view(dx), _abi.view(dd), _abi.view(dA)
     args.dBm, args.dCm, args.dD = _abi.view(dB), _abi.view(dC), _abi.view(dD)
@@ -235,8 +237,9 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_
 
     Logical layouts as the reference: u, delta, z (B, L, D); A (D, N); B, C (B, L, N);
     h0 (B, D, N).  Pass ``x.transpose(1, 2)`` for channel-major (B, D, L) storage.
-    ``segments`` forces the number of time segments the forward scans in parallel (default:
-    chosen by the engine; more than one only when B x D is too small to fill the GPU).
+    ``segments`` forces the number of time segments the forward and the backward scan in
+    parallel (default: chosen by the engine; more than one only when B x D is too small to fill
+    the GPU).
     ``delta_proj`` (D, R): ``delta`` is then the low-rank (B, L, R) input and the scan uses
     delta @ delta_proj^T -- the dt_proj GEMM of models/mamba.py:76, done by the kernels while
     they stage delta for R <= 16 and dstate <= 16 with 16/32-bit inputs (no (B, L, D) delta in
