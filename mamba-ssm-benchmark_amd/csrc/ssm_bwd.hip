@@ -566,7 +566,6 @@ struct BwdwLds {
   float B[NP][CKP];
   float C[NP][CKP];
   float pn[RH][CW][2][NPP];  // (dx, ddelta) terms of half a chunk, per state
-  float pd[RH][CW][NP][2];   // (dB, dC) terms of half a chunk, per channel
   float lr[LR ? kCK : 1][lr_pad(4)];
   float wr[LR ? CW : 1][lr_pad(4)];
 };
@@ -578,8 +577,14 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   typedef RowTile<IT, NP, UL> RT;
   constexpr int CW = G::CW, CK = kCK, RH = WL::RH, WPB = bwdw_waves(NP), NT = WPB * kWave;
   constexpr bool M1 = METHOD == 0;
+  // (dB, dC) terms of half a chunk for every channel of the workgroup, by half: rows of CH
+  // channels padded to CHP (16-byte reads; the lanes of one write hit distinct banks).  After
+  // a barrier TPI threads sum each (step, quantity, state) row, IPT rows per thread.
+  constexpr int CH = WPB * CW, CHP = CH + 4, NITEM = RH * 2 * NP;
+  constexpr int TPI = NT >= NITEM ? NT / NITEM : 1, IPT = NITEM > NT ? NITEM / NT : 1, CPT = CH / TPI;
+  static_assert(TPI <= 2 && CPT % 4 == 0 && NITEM == IPT * (NT / TPI), "reduction layout");
   __shared__ __align__(16) WL lds_all[WPB];
-  __shared__ __align__(16) float dbc[2][WPB][RH][NP][2];  // per-wavefront (dB, dC) sums, by half parity
+  __shared__ __align__(16) float pdw[2][RH][2][NP][CHP];
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave, wv = tid / kWave;
@@ -810,8 +815,8 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
           dA_acc = fmaf(dtb, pD, fmaf(-dhc, bx[t], dA_acc));
           S.pn[tt][c][0][n] = dhc * rB[tt];
           S.pn[tt][c][1][n] = pD;
-          S.pd[tt][c][n][0] = dhc * row_bcast<t>(xvw);
-          S.pd[tt][c][n][1] = dyb * hh[t + 1];
+          pdw[half][tt][0][n][wv * CW + c] = dhc * row_bcast<t>(xvw);
+          pdw[half][tt][1][n][wv * CW + c] = dyb * hh[t + 1];
         }
       });
       if constexpr (!SUM) {
@@ -825,27 +830,21 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
           for (int j = 0; j < NP; ++j) sum += part[j];
           Rh[half] = sum;
         }
-        // (dB, dC): sum over the wavefront's channels, then over the workgroup's wavefronts
-        constexpr int NI = (RH * NP * 2 + kWave - 1) / kWave;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          const int e = lane + i * kWave;
-          if (e < RH * NP * 2) {
-            const int q = e % 2, nn = (e / 2) % NP, st = e / (2 * NP);
-            float v = 0.0f;
-#pragma unroll
-            for (int j = 0; j < CW; ++j) v += S.pd[st][j][nn][q];
-            dbc[half][wv][st][nn][q] = v;
-          }
-        }
+        // (dB, dC): sum over the workgroup's channels
         lds_barrier();
-        for (int e = tid; e < RH * NP * 2; e += NT) {
-          const int q = e % 2, nn = (e / 2) % NP, st = e / (2 * NP);
-          const int tg = t0 + half * RH + st;
-          float v = 0.0f;
 #pragma unroll
-          for (int w = 0; w < WPB; ++w) v += dbc[half][w][st][nn][q];
-          if (tg < Lc) ((float *)(q == 0 ? p.ws_dB : p.ws_dC))[((b * p.ntiles + tile) * p.L + tg) * NP + nn] = v;
+        for (int i = 0; i < IPT; ++i) {
+          const int item = tid / TPI + i * (NT / TPI), part = tid % TPI;
+          const int st = item / (2 * NP), q = (item / NP) % 2, nn = item % NP;
+          float v[CPT];
+          lds_row(&pdw[half][st][q][nn][part * CPT], v);
+          float sum = 0.0f;
+#pragma unroll
+          for (int j = 0; j < CPT; ++j) sum += v[j];
+          if constexpr (TPI == 2) sum += dpp_f<0xB1>(sum);  // the partner lane's channels (same bits in both)
+          const int tg = t0 + half * RH + st;
+          if (part == 0 && tg < Lc)
+            ((float *)(q == 0 ? p.ws_dB : p.ws_dC))[((b * p.ntiles + tile) * p.L + tg) * NP + nn] = sum;
         }
       }
     });
