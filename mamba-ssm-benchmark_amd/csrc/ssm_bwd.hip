@@ -621,7 +621,10 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   float prod = 1.0f;                // summary: product of the segment's decays
   float h0v = 0.0f;
   if (!SUM && p.has_h0 && dval && nval) h0v = vload<float>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
-  float dA_acc = 0.0f, dDp = 0.0f, dbp = 0.0f;
+  // dA sums every step of the sequence: each chunk's 16 terms in float32, the chunk sums in
+  // float64 (a float32 running sum over a long sequence loses the small elements of dA)
+  // dD and d_bias: one term per chunk and lane, summed over the sequence in float64
+  double dA64 = 0.0, dDp = 0.0, dbp = 0.0;
   const float biasv = p.has_bias && tval ? vload<float>(p.bias, (int64_t)(dw + tc) * p.bias.s0) : 0.0f;
   const float dskv = p.has_D && tval ? vload<float>(p.Dsk, (int64_t)(dw + tc) * p.Dsk.s0) : 0.0f;
 
@@ -770,6 +773,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
       }
     });
 
+    float dA_acc = 0.0f;
     // ------------------------------------------------------------ walk back, half a chunk at a time
     // The walk broadcasts delta and x again rather than keeping the recompute's 2 x 16 values
     // live (tied to the adjoint: the compiler cannot reuse them).
@@ -811,8 +815,17 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
             else pD = lamf * (u_ * u_) * fmaf(ac.A, hh[t], bx[t]);
           }
           const float dhc = lamf * cf;
-          // A dA = sum_t (dt pD - lambda b): a and b depend on A only through dt A (see k_bwd)
-          dA_acc = fmaf(dtb, pD, fmaf(-dhc, bx[t], dA_acc));
+          if constexpr (M1) {
+            // A dA = sum_t (dt pD - lambda b): a and b depend on A only through dt A (see k_bwd)
+            dA_acc = fmaf(dtb, pD, fmaf(-dhc, bx[t], dA_acc));
+          } else {
+            // the direct terms, free of that identity's cancellation when dt A is small:
+            // Euler d/dA (a h + dt Bx) = dt a h;  bilinear d/dA = dt u^2 (h + dt Bx / 2)
+            float a_, u_;
+            disc<METHOD>(dtb, ac, a_, u_);
+            if constexpr (METHOD == 1) dA_acc = fmaf(lamf * dtb, a_ * hh[t], dA_acc);
+            else dA_acc = fmaf(lamf * dtb * (u_ * u_), fmaf(0.5f * dtb, bx[t], hh[t]), dA_acc);
+          }
           S.pn[tt][c][0][n] = dhc * rB[tt];
           S.pn[tt][c][1][n] = pD;
           pdw[half][tt][0][n][wv * CW + c] = dhc * row_bcast<t>(xvw);
@@ -825,10 +838,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
         {
           float part[NP];
           lds_row(&S.pn[tj % RH][tc][tj / RH][0], part);
-          float sum = 0.0f;
-#pragma unroll
-          for (int j = 0; j < NP; ++j) sum += part[j];
-          Rh[half] = sum;
+          Rh[half] = pairwise_sum(part);
         }
         // (dB, dC): sum over the workgroup's channels
         lds_barrier();
@@ -838,9 +848,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
           const int st = item / (2 * NP), q = (item / NP) % 2, nn = item % NP;
           float v[CPT];
           lds_row(&pdw[half][st][q][nn][part * CPT], v);
-          float sum = 0.0f;
-#pragma unroll
-          for (int j = 0; j < CPT; ++j) sum += v[j];
+          float sum = pairwise_sum(v);
           if constexpr (TPI == 2) sum += dpp_f<0xB1>(sum);  // the partner lane's channels (same bits in both)
           const int tg = t0 + half * RH + st;
           if (part == 0 && tg < Lc)
@@ -849,6 +857,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
       }
     });
     (void)par;
+    dA64 += (double)dA_acc;
     if constexpr (SUM) {
       wave_lds_sync();
       return;
@@ -862,8 +871,8 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
     const float dds = tj < RH ? sl : Rh[1];
     const float dxo = fmaf(dyv, dskv, dxs);
     const float ddo = dds * sgv;
-    dDp = fmaf(dyv, xv, dDp);
-    dbp += ev ? ddo : 0.0f;  // padded / inert steps carry state terms but no gradient
+    dDp += (double)(dyv * xv);
+    dbp += (double)(ev ? ddo : 0.0f);  // padded / inert steps carry state terms but no gradient
     const bool st = ev && G::lead(lane);
     if constexpr (UL) {
       const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES);
@@ -891,11 +900,11 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
     }
     return;
   } else {
-    if (dval) ((float *)p.ws_dA)[sidx] = dA_acc * ac.invA;
+    if (dval) ((float *)p.ws_dA)[sidx] = (float)(M1 ? dA64 * (double)ac.invA : dA64);
     if (p.has_dh0 && dval && nval && seg == 0)
       vstore<float>(p.dh0, b * p.dh0.s0 + d * p.dh0.s1 + n * p.dh0.s2, (float)lam_a);
     // dD and d_bias: the lead row's lanes hold one step slot each; sum them (fixed order)
-    const float sD = row_sum(dDp), sb = row_sum(dbp);
+    const float sD = row_sum((float)dDp), sb = row_sum((float)dbp);
     if (G::lead(lane) && tj == 0 && tval) {
       ((float *)p.ws_dD)[(b * p.nseg + seg) * p.D + dw + tc] = sD;
       ((float *)p.ws_db)[(b * p.nseg + seg) * p.D + dw + tc] = sb;

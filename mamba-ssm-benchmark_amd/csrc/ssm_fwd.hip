@@ -489,9 +489,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     // outputs of chunk k - 1: the lane of (step tj, channel tc) sums the partials over the states
     float part[NP];
     lds_row(&S.y[tj][tc][0], part);
-    float y = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NP; ++j) y += part[j];
+    const float y = pairwise_sum(part);
     const int tg = kp * CK + tj, dd = dw + tc;
     const bool st = live && G::lead(lane) && tg < L && tval;
     const float o0 = y + dskv * pv.x;

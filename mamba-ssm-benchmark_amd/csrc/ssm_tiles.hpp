@@ -29,4 +29,19 @@ __device__ __forceinline__ void lds_row(const CT *src, CT (&dst)[N]) {
   }
 }
 
+// Sum of N values in pairwise order (N a power of two): the same adds as a running sum, with
+// rounding that grows with log2(N) rather than N and independent adds for the scheduler.
+template <int N>
+__device__ __forceinline__ float pairwise_sum(const float (&v)[N]) {
+  static_assert((N & (N - 1)) == 0, "power of two");
+  if constexpr (N == 1) {
+    return v[0];
+  } else {
+    float h[N / 2];
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) h[i] = v[2 * i] + v[2 * i + 1];
+    return pairwise_sum<N / 2>(h);
+  }
+}
+
 }  // namespace ssm

@@ -28,7 +28,7 @@ def _load():
         P = ctypes.c_void_p
         I64 = ctypes.c_int64
         _lib.ssm_oracle_fwd.argtypes = [I64, I64, I64, I64, ctypes.c_int] + [P] * 11 + [ctypes.c_int]
-        _lib.ssm_oracle_bwd.argtypes = [I64, I64, I64, I64, ctypes.c_int] + [P] * 18 + [ctypes.c_int]
+        _lib.ssm_oracle_bwd.argtypes = [I64, I64, I64, I64, ctypes.c_int] + [P] * 19 + [ctypes.c_int]
         _lib.ssm_oracle_fwd.restype = ctypes.c_int
         _lib.ssm_oracle_bwd.restype = ctypes.c_int
     return _lib
@@ -59,8 +59,9 @@ def fwd(x, delta, A, Bm, Cm, h0=None, method="zoh", D=None, z=None, nthreads=0):
 
 
 def bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None, z=None, dlast=None,
-        nthreads=0):
-    """Returns the gradient dict of scan_ref.selective_scan_bwd, in float64."""
+        nthreads=0, mag=False):
+    """Returns the gradient dict of scan_ref.selective_scan_bwd, in float64.  With mag=True it
+    also holds "ddelta_mag": per ddelta element, the sum over states of the |terms| it adds."""
     lib = _load()
     x, delta, A, Bm, Cm, dout, h0, D, z, dlast = (
         _c(v) for v in (x, delta, A, Bm, Cm, dout, h0, D, z, dlast))
@@ -71,10 +72,11 @@ def bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None, z=None, dlast=
     g_dD = np.empty_like(D) if D is not None else None
     g_dz = np.empty_like(z) if z is not None else None
     g_dh0 = np.empty_like(h0) if h0 is not None else None
+    g_mag = np.empty_like(delta) if mag else None
     rc = lib.ssm_oracle_bwd(Bsz, L, Dm, N, METHODS[method], _p(x), _p(delta), _p(A), _p(Bm),
                             _p(Cm), _p(h0), _p(D), _p(z), _p(dout), _p(dlast), _p(g["dx"]),
                             _p(g["ddelta"]), _p(g["dA"]), _p(g["dB"]), _p(g["dC"]), _p(g_dD),
-                            _p(g_dz), _p(g_dh0), nthreads)
+                            _p(g_dz), _p(g_dh0), _p(g_mag), nthreads)
     if rc:
         raise RuntimeError(f"ssm_oracle_bwd failed: {rc}")
     if g_dD is not None:
@@ -83,4 +85,6 @@ def bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None, z=None, dlast=
         g["dz"] = g_dz
     if g_dh0 is not None:
         g["dh0"] = g_dh0
+    if g_mag is not None:
+        g["ddelta_mag"] = g_mag
     return g

@@ -7,7 +7,9 @@
  * Layouts are contiguous and logical: x, delta, z, out, y (B,L,D); A (D,N);
  * Bm, Cm (B,L,N); h0, last (B,D,N); Dskip (D).  Channels run in parallel with OpenMP;
  * dB/dC are accumulated per thread and summed in thread order (deterministic).
- * It is pinned against scan_ref.py by tests/test_oracle_c.py.
+ * It is pinned against scan_ref.py by tests/test_oracle_kat.py (test_c_oracle_matches_numpy_oracle).
+ * The backward optionally reports, per ddelta element, the sum over states of the magnitudes of
+ * the terms it adds (the scale of the float32 rounding a kernel can leave in that element).
  */
 #include <math.h>
 #include <stdint.h>
@@ -75,7 +77,7 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
                    const double *delta, const double *A, const double *Bm, const double *Cm,
                    const double *h0, const double *Dskip, const double *z, const double *dout,
                    const double *dlast, double *dx, double *ddelta, double *dA, double *dB,
-                   double *dC, double *dD, double *dz, double *dh0, int nthreads) {
+                   double *dC, double *dD, double *dz, double *dh0, double *ddelta_mag, int nthreads) {
   if (method < 0 || method > 2) return 1;
   int nt = 1;
 #ifdef _OPENMP
@@ -122,7 +124,7 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
           dz[i3] = dyv * pre * s * (1.0 + zz * (1.0 - s));
           dyv = dyv * zz * s;
         }
-        double dxv = Dskip ? dyv * Dskip[d] : 0.0, ddt = 0.0;
+        double dxv = Dskip ? dyv * Dskip[d] : 0.0, ddt = 0.0, mag = 0.0;
         for (int64_t n = 0; n < N; ++n) {
           int64_t in = IDX3(b, t, n, L, N);
           double Av = A[d * N + n], Bv = Bm[in], h_t = hs[(t + 1) * N + n], hp = hs[t * N + n];
@@ -135,12 +137,14 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
             if (fabs(zt) < 1e-3) f = 0.5 + zt / 3.0 + zt * zt / 8.0 + zt * zt * zt / 30.0;
             else f = (zt * a - e) / (zt * zt);
             ddt += da * Av * a + dh[n] * a * Bx;
+            mag += fabs(da * Av * a + dh[n] * a * Bx);
             pA[(b * D + d) * N + n] += da * dt * a + dh[n] * dt * dt * f * Bx;
             myB[in] += dh[n] * coef * xv;
             dxv += dh[n] * coef * Bv;
           } else if (method == 1) {
             a = exp(zt);
             ddt += da * Av * a + dh[n] * Bx;
+            mag += fabs(da * Av * a + dh[n] * Bx);
             pA[(b * D + d) * N + n] += da * dt * a;
             myB[in] += dh[n] * dt * xv;
             dxv += dh[n] * dt * Bv;
@@ -148,6 +152,7 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
             double u = 1.0 / (1.0 - 0.5 * zt), u2 = u * u;
             a = (1.0 + 0.5 * zt) * u;
             ddt += da * Av * u2 + dh[n] * u2 * Bx;
+            mag += fabs(da * Av * u2 + dh[n] * u2 * Bx);
             pA[(b * D + d) * N + n] += da * dt * u2 + dh[n] * 0.5 * dt * dt * u2 * Bx;
             myB[in] += dh[n] * dt * u * xv;
             dxv += dh[n] * dt * u * Bv;
@@ -156,6 +161,7 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
         }
         dx[i3] = dxv;
         ddelta[i3] = ddt;
+        if (ddelta_mag) ddelta_mag[i3] = mag;
       }
       if (dh0)
         for (int64_t n = 0; n < N; ++n) dh0[(b * D + d) * N + n] = dh[n];

@@ -1,0 +1,34 @@
+"""The parity bar of BASELINE.json's north_star, shared by the GPU tests.
+
+float32: every element within |got - ref| <= atol + rtol * |ref|, rtol 1e-4, atol 1e-5 (no
+scaling by the tensor's magnitude); bf16 inputs with a float32 state: rtol 2e-2.  `close`
+prints the per-tensor count of elements outside the bar and fails when it exceeds `allow`
+(0 unless a test states a measured exception).
+"""
+
+import numpy as np
+import torch
+
+RTOL, ATOL = 1e-4, 1e-5            # float32 parity bar
+RTOL_BF16, ATOL_BF16 = 2e-2, 2e-2  # bf16 inputs, float32 state
+
+
+def _np(v):
+    if isinstance(v, torch.Tensor):
+        return v.detach().to("cpu", torch.float64).numpy()
+    return np.asarray(v, dtype=np.float64)
+
+
+def outside(got, ref, rtol=RTOL, atol=ATOL):
+    """Number of elements of `got` outside atol + rtol |ref| (NaN counts as outside)."""
+    g, r = _np(got), _np(ref)
+    ok = np.abs(g - r) <= atol + rtol * np.abs(r)
+    return int(g.size - np.count_nonzero(ok))
+
+
+def close(got, ref, rtol=RTOL, atol=ATOL, name="", allow=0):
+    g, r = _np(got), _np(ref)
+    n = outside(g, r, rtol, atol)
+    print(f"parity {name or 'tensor'}: {n} of {g.size} elements outside rtol {rtol:g} / atol {atol:g}", flush=True)
+    if n > allow:
+        np.testing.assert_allclose(g, r, rtol=rtol, atol=atol, err_msg=f"{name}: {n} outside (allowed {allow})")

@@ -1,7 +1,9 @@
 """Parity of the fused HIP engine (libssmscan.so, ssm_fwd / ssm_bwd) with the float64 oracle.
 
-Tolerances: float32 inputs rtol 1e-4 / atol 1e-5 on outputs and
-every gradient; bf16 inputs with a float32 state rtol 2e-2.  Shapes: the reference's own GPU
+Tolerances (tests/parity.py): float32 inputs rtol 1e-4 / atol 1e-5 on
+every element of the outputs and of every gradient, with no scaling by the tensor's magnitude;
+bf16 inputs with a float32 state rtol 2e-2.  Each check prints its count of elements outside
+the bar.  Shapes: the reference's own GPU
 test shapes (tests/test_triton.py:31), the BASELINE configs 0 and 1, and edge cases (L = 1,
 ragged L and D, dstate not a power of two, non-contiguous views, expanded A).
 """
@@ -17,22 +19,7 @@ from ssm_inputs import baseline_inputs, np64, triton_test_inputs
 
 pytestmark = pytest.mark.gpu
 
-RTOL, ATOL = 1e-4, 1e-5            # float32 parity bar
-RTOL_BF16, ATOL_BF16 = 2e-2, 2e-2  # bf16 inputs, float32 state
-
-
-def close(got, ref, rtol=RTOL, atol=ATOL, name=""):
-    """|got - ref| <= atol * max(1, rms(ref)) + rtol * |ref| elementwise.
-
-    The absolute term is taken relative to the tensor's RMS magnitude: for tensors of unit
-    scale (every output and most gradients) it is exactly atol.  It matters for gradients that
-    are sums of large, cancelling per-state terms: ddelta at BASELINE config 1 has RMS ~7 and
-    summands up to ~1e3, so a fixed 1e-5 lies below what float32 arithmetic can resolve there
-    (a float32 emulation of the same math with correctly rounded exp/expm1 leaves 229 of its
-    4.2M elements outside the fixed bound; the kernel leaves 1)."""
-    got = np64(got) if isinstance(got, torch.Tensor) else got
-    scale = max(1.0, float(np.sqrt(np.mean(np.square(ref))))) if np.size(ref) else 1.0
-    np.testing.assert_allclose(got, ref, rtol=rtol, atol=atol * scale, err_msg=name)
+from parity import ATOL, ATOL_BF16, RTOL, RTOL_BF16, close  # noqa: F401  (the north_star bar)
 
 
 def run_fused(ins, dev, method, D=None, z=None, bias=None, softplus=False, dout=None, dlast=None):
@@ -52,7 +39,8 @@ def run_fused(ins, dev, method, D=None, z=None, bias=None, softplus=False, dout=
     return out.detach(), last.detach(), grads
 
 
-def oracle(ins, method, D=None, z=None, bias=None, softplus=False, dout=None, dlast=None, use_c=False):
+def oracle(ins, method, D=None, z=None, bias=None, softplus=False, dout=None, dlast=None, use_c=False,
+           mag=False):
     x, delta, A, Bm, Cm, h0 = (np64(t) for t in ins)
     raw = delta
     if bias is not None:
@@ -60,8 +48,10 @@ def oracle(ins, method, D=None, z=None, bias=None, softplus=False, dout=None, dl
     d_eff = np.log1p(np.exp(raw)) if softplus else raw
     fwd = c_oracle.fwd if use_c else R.selective_scan_fwd
     out, _, last = fwd(x, d_eff, A, Bm, Cm, h0, method, np64(D), np64(z))
-    bwd = c_oracle.bwd if use_c else R.selective_scan_bwd
-    g = bwd(x, d_eff, A, Bm, Cm, np64(dout), h0, method, np64(D), np64(z), np64(dlast))
+    if use_c:
+        g = c_oracle.bwd(x, d_eff, A, Bm, Cm, np64(dout), h0, method, np64(D), np64(z), np64(dlast), mag=mag)
+    else:
+        g = R.selective_scan_bwd(x, d_eff, A, Bm, Cm, np64(dout), h0, method, np64(D), np64(z), np64(dlast))
     if softplus or bias is not None:
         dd_raw = g["ddelta"] * (1.0 / (1.0 + np.exp(-raw)) if softplus else 1.0)
         g["ddelta"] = dd_raw
@@ -141,12 +131,7 @@ def test_config1_fwd_bwd_matches_c_oracle(dev):
     ins = (t["u"], t["delta"], t["A"], t["Bm"], t["Cm"], None)
     got = run_fused(ins, dev, "zoh", D=t["D"], z=t["z"], dout=t["dy"])
     ref = oracle(ins, "zoh", D=t["D"], z=t["z"], dout=t["dy"], use_c=True)
-    check_all(got, ref)
-    # the fixed (unscaled) bound holds for all but at most 1 ppm of the elements of each tensor
-    for k, v in list(got[2].items()) + [("out", got[0]), ("last", got[1])]:
-        r = {"out": ref[0], "last": ref[1]}.get(k, ref[2].get(GRAD_MAP.get(k, k)))
-        bad = np.abs(np64(v) - r) > ATOL + RTOL * np.abs(r)
-        assert bad.sum() <= max(1, bad.size // 1_000_000), (k, int(bad.sum()))
+    check_all(got, ref)   # every element of every tensor within the bar (no exception at c1)
 
 
 def test_backward_is_bitwise_deterministic(dev):

@@ -1,7 +1,7 @@
 """RMSNorm kernels (ssm_scan.norm, csrc/ssm_norm.hip) against models/common.py:14-16.
 
 The reference expression in float64 (torch autograd for the gradients) on the same float32
-values: forward rtol 1e-5 / atol 1e-6, gradients rtol 1e-4 / atol 1e-5 x max(1, RMS); the
+values: forward rtol 1e-5 / atol 1e-6, gradients rtol 1e-4 / atol 1e-5 on every element; the
 float64 kernels through the same autograd function to 1e-12.  Also: rows with a stride (a
 column slice), bitwise-repeatable backward, and the dtypes that keep the torch expression.
 """
@@ -22,8 +22,7 @@ def ref64(x, w, eps):
 
 
 def close(got, ref, rtol, atol):
-    scale = max(1.0, ref.double().pow(2).mean().sqrt().item())
-    torch.testing.assert_close(got.double(), ref.double(), rtol=rtol, atol=atol * scale)
+    torch.testing.assert_close(got.double(), ref.double(), rtol=rtol, atol=atol)
 
 
 @pytest.mark.parametrize("shape", [(2, 37, 256), (1, 1, 64), (5, 3, 100), (3, 7, 1000), (4, 9, 1),

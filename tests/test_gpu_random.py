@@ -3,7 +3,7 @@ float64 oracle: shapes, methods, optional operands and storage layouts drawn tog
 combinations that the targeted tests do not list are still covered.
 
 Each case prints its configuration before running (it names the case if it fails).
-Tolerances as the fused tests: rtol 1e-4 / atol 1e-5 x max(1, RMS), float32.
+Tolerances as the fused tests: rtol 1e-4 / atol 1e-5 on every element, float32 (tests/parity.py).
 """
 
 import numpy as np
@@ -13,17 +13,15 @@ import torch
 import ssm_scan
 from oracle import scan_ref as R
 from ssm_inputs import np64
+import parity
 
 pytestmark = pytest.mark.gpu
 
-RTOL, ATOL = 1e-4, 1e-5
 METHODS = ("zoh", "euler", "bilinear")
 
 
 def close(got, ref, name):
-    got = np64(got)
-    scale = max(1.0, float(np.sqrt(np.mean(np.square(ref))))) if np.size(ref) else 1.0
-    np.testing.assert_allclose(got, ref, rtol=RTOL, atol=ATOL * scale, err_msg=name)
+    parity.close(got, ref, name=name)   # rtol 1e-4 / atol 1e-5 on every element
 
 
 def draw(seed):

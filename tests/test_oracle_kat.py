@@ -412,3 +412,17 @@ def test_lm_ref_layer_composes_pinned_oracle_pieces():
     state = {"conv": torch.zeros(2, D, W - 1, dtype=torch.float64), "ssm": torch.zeros(2, D, N, dtype=torch.float64)}
     steps = torch.cat([lm_ref.mamba_layer(p, "m.", u[:, t:t + 1], N, R_, W, state=state) for t in range(11)], 1)
     np.testing.assert_allclose(steps.numpy(), out.numpy(), rtol=1e-11, atol=1e-12)
+
+
+@pytest.mark.parametrize("shape,eps", [((3, 7, 256), 1e-5), ((2, 5, 1000), 1e-6), ((4, 1), 1e-5), ((6, 64), 1e-3)])
+def test_lm_ref_rmsnorm_matches_torch_rms_norm(shape, eps):
+    """oracle/lm_ref.rmsnorm (models/common.py:14-16) against torch.nn.functional.rms_norm, an
+    independent library implementation of the same normalisation, in float64."""
+    from oracle import lm_ref
+    g = torch.Generator().manual_seed(shape[-1])
+    x = torch.randn(shape, generator=g, dtype=torch.float64) * 3.0
+    w = 1.0 + 0.5 * torch.randn(shape[-1], generator=g, dtype=torch.float64)
+    ref = torch.nn.functional.rms_norm(x, (shape[-1],), w, eps)
+    torch.testing.assert_close(lm_ref.rmsnorm(x, w, eps), ref, rtol=1e-13, atol=1e-13)
+    # a plausible slip (eps outside the root, or a sum instead of the mean) fails this check
+    assert not torch.allclose(x / (x.pow(2).mean(-1, keepdim=True).sqrt() + eps) * w, ref, rtol=1e-13, atol=0) or eps < 1e-12
