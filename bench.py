@@ -18,8 +18,14 @@ small fixed-order reduction kernel) gives the roofline: algorithmic bytes per la
 average duration, against 8 TB/s.  The CPU baseline is the torch-CPU restatement of the
 reference's CPU path (oracle/cpu_chunked.py), timed on a bounded sample of the same workload.
 
+The default c1 run appends, as extra keys of the same line, the other two north_star targets
+(c2's L = 131072 fp32 forward time with the CPU baseline's seconds and cores and the GPU/CPU
+time fraction; c4's decode latency per layer at batch 64) and the long-sequence fwd+bwd times
+(`--no-extras` leaves them out).
+
 Other workloads (--workload): c0 (forward, B1 L512), c2 / c2bf16 (long-sequence forward),
 c3 (10-layer Mamba LM fwd+bwd), c4 (decode latency per layer at batch 64, HIP-graph replay),
+long (B1 D512 N16 fwd+bwd at L 4096 / 16384 / 65536, the reference's bench_scan shape),
 scans (the composed path's linear-scan algorithms and discretization, GB/s per kernel),
 copy (a plain device copy of known size, for PMC counter calibration).
 """
@@ -270,6 +276,78 @@ def bench_fwd(args, dev, B, L, dtype, workload):
     return rec
 
 
+REF_LONG_MS = {4096: 10.7207, 16384: 41.8723, 65536: 525.1975}   # results/csv/bench_scan.csv:25-27
+
+
+def bench_long(args, dev, lengths=(4096, 16384, 65536)):
+    """The reference's own scan benchmark shape (benchmarks/bench_scan.py:25-66): one layer's
+    scan at B1 D512 N16 fp32 for growing L, forward + backward of out.sum() (dy = ones), inputs
+    as its make_inputs (x, B, C ~ N(0,1) in (B, L, .) storage, delta ~ U[1e-3, 0.101], A =
+    -(1..16)), no D skip and no gate.  B x D alone leaves the GPU short of work, so forward
+    and backward walk time segments.  `value` is Mtok/s at the longest L; every length's
+    fwd+bwd and forward-only times are in `lengths`, beside the reference's published fused
+    Triton fwd+bwd times (RTX 3050 Laptop GPU)."""
+    import ssm_scan
+    D, N = 512, 16
+    per = {}
+    for L in lengths:
+        g = torch.Generator().manual_seed(0)
+        x = torch.randn(1, L, D, generator=g)
+        delta = torch.rand(1, L, D, generator=g) * 0.1 + 1e-3
+        A = -torch.arange(1, N + 1, dtype=torch.float32).repeat(D, 1)
+        Bm = torch.randn(1, L, N, generator=g)
+        Cm = torch.randn(1, L, N, generator=g)
+        leaves = [t.to(dev).requires_grad_() for t in (x, delta, A, Bm, Cm)]
+        dy = torch.ones(1, L, D, device=dev)
+
+        def step():
+            out = ssm_scan.selective_scan_fn(*leaves)
+            return torch.autograd.grad(out, leaves, dy)
+
+        def fwd():
+            with torch.no_grad():
+                return (ssm_scan.selective_scan_fn(*leaves),)
+
+        eager_ms, graph_ms, graph_ok = time_steps(step, args)
+        ms = min(eager_ms, graph_ms) if graph_ok else eager_ms
+        f_eager, f_graph, f_ok = time_steps(fwd, args)
+        with ssm_scan.KernelTimer() as timer:
+            for _ in range(min(args.steps, 20)):
+                step()
+        tt = timer.times_ms()
+        fwd_k, bwd_k = statistics.mean(tt["ssm_fwd"]), statistics.mean(tt["ssm_bwd"])
+        fb, bb = alg_bytes(1, L, D, N, gate=False, skip=False)
+        per[L] = {"fwd_bwd_ms": ms, "fwd_ms": min(f_eager, f_graph) if f_ok else f_eager,
+                  "kernels_ms": {"ssm_fwd": fwd_k, "ssm_bwd": bwd_k},
+                  "hbm_frac_bwd": bb / (bwd_k * 1e-3) / (HBM_PEAK_GBS * 1e9),
+                  "hbm_frac_fwd": fb / (fwd_k * 1e-3) / (HBM_PEAK_GBS * 1e9),
+                  "graph_matches_eager": graph_ok and f_ok,
+                  "reference_published_fwd_bwd_ms": REF_LONG_MS.get(L)}
+        del leaves, dy, x, delta, Bm, Cm
+        torch.cuda.empty_cache()
+    L = max(lengths)
+    top = per[L]
+    value = L / (top["fwd_bwd_ms"] * 1e-3) / 1e6
+    fb, bb = alg_bytes(1, L, D, N, gate=False, skip=False)
+    achieved = bb / (top["kernels_ms"]["ssm_bwd"] * 1e-3) / 1e9
+    ref = REF_LONG_MS.get(L)
+    return {"metric": f"selective-scan fwd+bwd Mtok/s, B1 L{L} D512 N16 fp32 (reference bench_scan shape)",
+            "value": value, "unit": "Mtok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": top["fwd_bwd_ms"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": value / (L / (ref * 1e-3) / 1e6) if ref else None,
+            "baseline_note": "vs the reference's published fused Triton fwd+bwd time at this shape "
+                             "(RTX 3050 Laptop GPU, results/csv/bench_scan.csv)",
+            "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "config 2 shape fwd+bwd: B1 D512 N16, L in "
+                                   + "/".join(str(v) for v in lengths) + ", zoh, no gate, no D skip, (B, L, D) "
+                                   "storage, dy = ones (bench_scan.py's out.sum().backward())",
+                       "batch": 1, "seqlen": L, "dim": D, "dstate": N, "method": "zoh"},
+            "lengths": {str(k): v for k, v in per.items()},
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                         "kernel": "ssm_bwd (summary, carry, main pass, finalize)", "alg_bytes_per_launch": bb}}
+
+
 def bench_lm(args, dev):
     """Config 3: the 10-layer byte-level Mamba LM (d_model 256, d_inner 512, N 16), forward +
     backward of the next-byte cross-entropy at B16 L512, float32, random init and random bytes.
@@ -516,17 +594,50 @@ def bench_copy(args, dev):
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup}
 
 
+def c1_extras(args, dev):
+    """The other north_star targets and the long-sequence fwd+bwd, measured in the default run
+    beside the c1 line: c2's L = 131072 fp32 forward against the CPU baseline, c4's decode
+    latency per layer at batch 64 (graph replay), and B1 D512 N16 fwd+bwd at L 4096..65536."""
+    sub = argparse.Namespace(**vars(args))
+    sub.steps, sub.warmup = min(args.steps, 20), min(args.warmup, 5)
+    sub.segments = 0
+    out = {}
+    c2 = bench_fwd(sub, dev, 1, 131072, torch.float32, "config 2: fwd B1 L131072 D512 N16")
+    cb = c2.get("cpu_baseline", {})
+    out["c2_fwd_L131072"] = {"ms": c2["ms_per_step"], "kernel_ms": c2["kernel_ms"],
+                             "hbm_frac": c2["roofline"]["frac"],
+                             "cpu_baseline_seconds": cb.get("seconds_full_forward"),
+                             "cpu_baseline_cores": cb.get("cores"), "cpu_baseline_kind": cb.get("kind"),
+                             "gpu_time_frac_of_cpu": c2.get("gpu_time_frac_of_cpu"), "target_frac": 0.02}
+    torch.cuda.empty_cache()
+    c4 = bench_decode(sub, dev)
+    out["c4_decode_us_per_layer"] = c4["value"]
+    out["c4_decode"] = {"us_per_layer": c4["value"], "ms_per_token_model": c4["ms_per_token_model"],
+                        "step_mode": "hip-graph replay", "batch": 64, "target_us_per_layer": 20.0,
+                        "cpu_baseline_us_per_layer": c4.get("cpu_baseline", {}).get("value")}
+    torch.cuda.empty_cache()
+    lg = bench_long(sub, dev)
+    out["long_fwd_bwd"] = {"Mtok_s_L65536": lg["value"], "vs_reference_published": lg["vs_baseline"],
+                           "lengths": {k: {"fwd_bwd_ms": v["fwd_bwd_ms"], "fwd_ms": v["fwd_ms"],
+                                           "reference_published_fwd_bwd_ms": v["reference_published_fwd_bwd_ms"]}
+                                       for k, v in lg["lengths"].items()}}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "c3", "c4", "scans", "copy"])
+    ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "c3", "c4", "long", "scans",
+                                                                 "copy"])
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--seqlen", type=int, default=131072)
     ap.add_argument("--segments", type=int, default=0, help="forward time segments (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="report the eager step (no HIP-graph replay)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="c1 only: skip the c2 / c4 / long-sequence keys appended to the line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): the hot path here is the "
@@ -538,6 +649,8 @@ def main():
     dev = torch.device("cuda", 0)
     if args.workload == "c1":
         rec = bench_c1(args, dev)
+        if not args.no_extras:
+            rec.update(c1_extras(args, dev))
     elif args.workload == "c0":
         rec = bench_fwd(args, dev, 1, 512, torch.float32, "config 0: fwd B1 L512 D512 N16 fp32")
     elif args.workload in ("c2", "c2bf16"):
@@ -547,6 +660,8 @@ def main():
         rec = bench_lm(args, dev)
     elif args.workload == "c4":
         rec = bench_decode(args, dev)
+    elif args.workload == "long":
+        rec = bench_long(args, dev)
     elif args.workload == "scans":
         rec = bench_scans(args, dev)
     else:

@@ -274,3 +274,45 @@ def test_generate_and_checkpoint_round_trip(dev):
     again = load_checkpoint(buf, dev)
     with torch.no_grad():
         assert torch.equal(again(prompt), model(prompt))
+
+
+# the row-resident kernel's shapes (the LM preset; dstate 8 bilinear) and the general kernel's:
+# dstate 12, conv width 5 and 6 (> 4), dim 640 and 768 (> 512)
+ORACLE_DECODE_SHAPES = [
+    dict(n_layers=10),
+    dict(n_layers=3, d_state=8, discretization="bilinear"),
+    dict(n_layers=3, d_state=12, d_conv=5, discretization="euler"),
+    dict(n_layers=2, d_model=384),
+    dict(n_layers=2, d_model=320, d_state=12, d_conv=6),
+]
+
+
+@pytest.mark.parametrize("shape", ORACLE_DECODE_SHAPES, ids=lambda s: "-".join(f"{k}{v}" for k, v in s.items()))
+def test_fast_decoder_matches_float64_reference(dev, shape):
+    """FastDecoder.step (in_proj GEMM, the fused decode launch, out_proj + residual GEMM per layer)
+    against the float64 restatement of the reference's recurrent decode (models/mamba.py:104-125,
+    lm_ref.lm_forward with states), batch 64, 8 tokens from random conv and ssm states: logits
+    after every token, then every layer's ssm and conv state.
+
+    Tolerances: states at the float32 bar (rtol 1e-4 / atol 1e-5); logits rtol 1e-4 with atol
+    1e-5 x max|logit| (logits are float32 GEMMs over d_model terms of the final hidden state)."""
+    from ssm_scan.decode import FastDecoder
+    from parity import close
+    torch.manual_seed(11)
+    model = MambaLM(**shape).to(dev).eval()
+    m = model.blocks[0].mixer
+    fast = FastDecoder(model)
+    B, T = 64, 8
+    states = _random_states(model, B, dev, 12)
+    rstates = [{"conv": s.conv.cpu().double().clone(), "ssm": s.ssm.cpu().double().clone()} for s in states]
+    p = {k: v.detach().cpu().double() for k, v in model.state_dict().items()}
+    toks = torch.randint(0, 256, (T, B, 1), generator=torch.Generator().manual_seed(13))
+    for t in range(T):
+        got = fast.step(toks[t].to(dev), states)
+        with torch.no_grad():
+            ref = lm_ref.lm_forward(p, toks[t], n_layers=shape["n_layers"], d_state=m.d_state, dt_rank=m.dt_rank,
+                                    d_conv=m.d_conv, states=rstates, method=m.discretization)[:, 0]
+        close(got, ref, rtol=1e-4, atol=1e-5 * float(ref.abs().max()), name=f"logits token {t}")
+    for i, (s, r) in enumerate(zip(states, rstates)):
+        close(s.ssm, r["ssm"], name=f"layer {i} ssm state")
+        close(s.conv, r["conv"], name=f"layer {i} conv state")
