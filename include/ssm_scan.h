@@ -324,6 +324,17 @@ int ssm_conv_bwd(const ssm_conv_args *args, void *stream);
 int ssm_norm_fwd(const ssm_norm_args *args, void *stream);   /* models/common.py:14-16 */
 int ssm_norm_bwd(const ssm_norm_args *args, void *stream);   /* autograd of :14-16 */
 
+/* ssm_fwd without allocation.  No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results as ssm_fwd, except that args->workspace and
+ * args->workspace_bytes are ignored: the long-sequence (segmented) path uses a fixed device
+ * array of SSM_FWD_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, and a forward
+ * whose ssm_fwd_workspace_bytes() exceeds it fails with SSM_ESPACE.  The stream must belong
+ * to the current device.  Calls on one GPU share the array: calls that overlap on one GPU
+ * race (serialize them, e.g. on one stream). */
+#define SSM_FWD_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024)
+int ssm_fwd_noalloc(const ssm_fwd_args *args, void *stream);
+
 /* ------------------------------------------------------------------ plans (host-only, exact integers)
  * The reference's integer planning functions, returned bit-exactly. */
 int64_t ssm_default_chunk(int64_t seqlen);                        /* models/scan.py:138-139 */

@@ -3,9 +3,11 @@
 // Host-only work lives here: argument validation (callable without a device, so the error
 // paths are testable on a CPU host), workspace sizing, the integer planning functions of the
 // reference, and dispatch to the kernel launchers.  No device memory is allocated and no
-// stream is synchronized.
+// stream is synchronized.  One file-scope device array (`scratch`, below) serves the
+// allocation-free forward ssm_fwd_noalloc.
 #include <algorithm>
 #include <math.h>
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -828,6 +830,72 @@ int ssm_norm_bwd(const ssm_norm_args *a, void *stream) {
   p.ws = a->workspace;
   hipError_t e = launch_norm(p, a->dtype, true, (hipStream_t)stream);
   return e == hipSuccess ? ok() : hip_fail(e, "ssm_norm_bwd");
+}
+
+// ------------------------------------------------------------------ forward without allocation
+// ssm_fwd with the long-sequence workspace taken from a fixed device array instead of the
+// caller's buffer, for callers that cannot allocate.  Every GPU the library runs on holds its
+// own copy of the array until the process ends; host code reaches it only through the address
+// hipGetSymbolAddress returns for the current device (the array's name is a host-side stand-in).
+// Calls on one GPU share it, so calls that overlap on one GPU race.
+
+}  // extern "C"
+
+static __device__ __align__(256) unsigned char scratch[SSM_FWD_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on the device that runs `stream` (which must be the
+// current device), looked up once per device.
+int scratch_address(void *stream, void **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "ssm_fwd_noalloc: hipGetDevice");
+  if (stream) {
+    hipDevice_t sdev = 0;
+    e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    if (e != hipSuccess) return hip_fail(e, "ssm_fwd_noalloc: hipStreamGetDevice");
+    if ((int)sdev != dev)
+      return fail(SSM_EINVAL, "ssm_fwd_noalloc: the stream belongs to device %d but device %d is current",
+                  (int)sdev, dev);
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail(SSM_EINVAL, "ssm_fwd_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "ssm_fwd_noalloc: hipGetSymbolAddress(scratch)");
+    if (!ptr) return fail(SSM_EHIP, "ssm_fwd_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SSM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ssm_fwd_noalloc(const ssm_fwd_args *a, void *stream) {
+  int rc = ssm_fwd_check(a);
+  if (rc) return rc;
+  const int64_t need = ssm_fwd_workspace_bytes(a);
+  if (need > (int64_t)SSM_FWD_NOALLOC_SCRATCH_BYTES)
+    return fail(SSM_ESPACE,
+                "ssm_fwd_noalloc: this forward needs %lld bytes of workspace, more than the fixed scratch of "
+                "%lld bytes; request fewer segments or call ssm_fwd with a workspace",
+                (long long)need, (long long)SSM_FWD_NOALLOC_SCRATCH_BYTES);
+  void *ptr = nullptr;
+  rc = scratch_address(stream, &ptr);
+  if (rc) return rc;
+  ssm_fwd_args b = *a;
+  b.workspace = ptr;
+  b.workspace_bytes = SSM_FWD_NOALLOC_SCRATCH_BYTES;
+  return ssm_fwd(&b, stream);
 }
 
 }  // extern "C"

@@ -137,6 +137,7 @@ _SIGS = {
     "ssm_conv_workspace_bytes": (c_i64, [ctypes.POINTER(ConvArgs)]),
     "ssm_norm_workspace_bytes": (c_i64, [ctypes.POINTER(NormArgs)]),
     "ssm_fwd": (c_i32, [ctypes.POINTER(FwdArgs), c_vp]),
+    "ssm_fwd_noalloc": (c_i32, [ctypes.POINTER(FwdArgs), c_vp]),
     "ssm_bwd": (c_i32, [ctypes.POINTER(BwdArgs), c_vp]),
     "ssm_step": (c_i32, [ctypes.POINTER(StepArgs), c_vp]),
     "ssm_decode_step": (c_i32, [ctypes.POINTER(DecodeArgs), c_vp]),

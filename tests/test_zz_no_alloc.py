@@ -1,0 +1,85 @@
+"""ssm_fwd_noalloc: the forward with its long-sequence workspace in the library's fixed device
+array instead of a caller buffer.  Called through the C ABI and checked bitwise against
+ssm_fwd with a caller workspace (same kernels), and against the float64 C oracle at the float32
+bar (rtol 1e-4 / atol 1e-5), on two calls in a row whose second input is smaller (the array
+keeps the first call's contents).  The size rejection is host logic and runs on the CPU.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+from oracle import c_oracle
+from parity import close
+from ssm_inputs import np64, triton_test_inputs
+from ssm_scan import _abi, hip_scan
+
+SCRATCH_BYTES = 8 * 1024 * 1024   # SSM_FWD_NOALLOC_SCRATCH_BYTES
+
+
+def _args(x, delta, A, Bm, Cm, D, z, h0, out, last, method, segments):
+    a = _abi.FwdArgs()
+    hip_scan._fill_common(a, x, delta, A, Bm, Cm, D, z, None, False, h0, method, x.dtype)
+    a.out, a.last = _abi.view(out), _abi.view(last)
+    a.segments = segments
+    return a
+
+
+def test_noalloc_rejects_a_workspace_beyond_the_scratch():
+    """B1 L16384 D512 N16 with 128 segments needs 3 x 128 x 512 x 16 x 4 B = 12 MiB > 8 MiB:
+    SSM_ESPACE before any device call; ssm_fwd_workspace_bytes states the size."""
+    B, L, D, N = 1, 16384, 512, 16
+    x, Bm, A = torch.zeros(B, L, D), torch.zeros(B, L, N), torch.zeros(D, N)
+    a = _args(x, x, A, Bm, Bm, None, None, None, x, None, hip_scan.METHODS["zoh"], 128)
+    lib = _abi.lib()
+    need = lib.ssm_fwd_workspace_bytes(ctypes.byref(a))
+    assert need > SCRATCH_BYTES
+    rc = lib.ssm_fwd_noalloc(ctypes.byref(a), None)
+    assert rc == _abi.ESPACE
+    msg = lib.ssm_last_error().decode()
+    assert "fixed scratch" in msg and str(need) in msg
+
+
+CASES = [  # (B, L, D, N, segments, method, gate): the second call is smaller than the first
+    (1, 8192, 256, 16, 16, "zoh", True),
+    (2, 1000, 64, 16, 5, "bilinear", False),
+]
+
+
+@pytest.mark.gpu
+def test_noalloc_forward_equals_ssm_fwd_on_consecutive_calls(dev):
+    lib = _abi.lib()
+    for B, L, D, N, segments, method, gate in CASES:
+        print(f"case B{B} L{L} D{D} N{N} segments {segments} {method} gate {gate}", flush=True)
+        x, delta, A, Bm, Cm, h0 = triton_test_inputs(B, L, D, N, True, seed=L)
+        g = torch.Generator().manual_seed(L + 1)
+        Dv = torch.randn(D, generator=g)
+        z = torch.randn(B, L, D, generator=g) if gate else None
+        ins = [None if t is None else t.to(dev) for t in (x, delta, A, Bm, Cm, Dv, z, h0)]
+        res = []
+        for entry in ("ssm_fwd", "ssm_fwd_noalloc"):
+            out = torch.empty(B, L, D, device=dev)
+            last = torch.empty(B, D, N, device=dev)
+            a = _args(*ins, out, last, hip_scan.METHODS[method], segments)
+            need = lib.ssm_fwd_workspace_bytes(ctypes.byref(a))
+            assert 0 < need <= SCRATCH_BYTES
+            stream = _abi.stream_handle(dev)
+            if entry == "ssm_fwd":
+                ws = torch.empty(need, dtype=torch.uint8, device=dev)
+                a.workspace, a.workspace_bytes = ws.data_ptr(), need
+                rc = lib.ssm_fwd(ctypes.byref(a), stream)
+            else:
+                torch.cuda.synchronize()
+                before = torch.cuda.memory_allocated(dev)
+                rc = lib.ssm_fwd_noalloc(ctypes.byref(a), stream)
+                assert torch.cuda.memory_allocated(dev) == before
+            _abi.check(rc, entry)
+            torch.cuda.synchronize()
+            res.append((out, last))
+        (o1, l1), (o2, l2) = res
+        assert torch.equal(o1, o2) and torch.equal(l1, l2)
+        rout, _, rlast = c_oracle.fwd(*(np64(t) for t in (x, delta, A, Bm, Cm, h0)), method=method,
+                                      D=np64(Dv), z=np64(z))
+        close(o2, rout, name="out")
+        close(l2, rlast, name="last")
