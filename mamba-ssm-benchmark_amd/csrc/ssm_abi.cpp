@@ -354,6 +354,7 @@ int ssm_bwd(const ssm_bwd_args *a, void *stream) {
   const ssm_tensor *bld[] = {&a->x, p.lowrank ? &a->x : &a->delta, &a->dout, &a->dx, &a->ddelta};
   p.uniform = uniform_layout(bld, 5, a->Bm, a->Cm, a->seqlen, a->dim, a->dstate, a->dtype, a->z) &&
               saved_rows_fit(w.f, a->seqlen, a->dim, a->dtype) &&
+              a->seqlen * w.f.np * state_size(a->dtype) < ((int64_t)1 << 31) &&  // dB / dC partial rows
               (!has(a->dz) || row_fits(a->dz, a->seqlen, a->dim, a->dtype == SSM_F64 ? 8 : a->dtype == SSM_F32 ? 4 : 2));
   p.ws_dB = ws + w.dB; p.ws_dC = ws + w.dC; p.ws_dA = ws + w.dA; p.ws_dD = ws + w.dD; p.ws_db = ws + w.db;
   p.nseg = w.sp.nseg; p.seg_chunks = w.sp.seg_chunks;

@@ -647,13 +647,18 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   uint32_t offB[EB];
   tile_offsets<CK, NP>(offB, vB, 0, bt, lane, ES);
   const __amdgpu_buffer_rsrc_t empty = flat_buffer(p.x.p, 0);
-  const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES);
-  const __amdgpu_buffer_rsrc_t rbdt = LR ? empty : row_buffer(vdt, b, L, D, ES);
-  const __amdgpu_buffer_rsrc_t rbg = row_buffer(vg, b, L, D, ES), rbz = row_buffer(vzl, b, L, D, ES);
-  const __amdgpu_buffer_rsrc_t rbB = row_buffer(vB, b, L, N, ES), rbC = row_buffer(vC, b, L, N, ES);
+  const RowRef rx = row_ref(vx, b, L, D, ES), rdt = row_ref(LR ? vx : vdt, b, L, D, ES);
+  const RowRef rg = row_ref(vg, b, L, D, ES), rz = row_ref(vzl, b, L, D, ES);
+  const RowRef rB = row_ref(vB, b, L, N, ES), rC = row_ref(vC, b, L, N, ES);
+  const RowRef rdx = row_ref(vdx, b, L, D, ES), rddt = row_ref(vddt, b, L, D, ES);
+  const RowRef rdz = row_ref(p.has_z ? vdz : vdx, b, L, D, ES);
   const int64_t ckrow = (int64_t)p.nchunks * p.D * NP;
-  const __amdgpu_buffer_rsrc_t rbk = flat_buffer((const float *)p.ckpt + b * ckrow, ckrow * 4);
-  const __amdgpu_buffer_rsrc_t rby = flat_buffer(ypre ? ypre + b * p.L * p.D : p.x.p, ypre ? p.L * p.D * 4 : 0);
+  const RowRef rk = flat_ref((const float *)p.ckpt + b * ckrow, ckrow * 4);
+  const RowRef ry = flat_ref(ypre ? ypre + b * p.L * p.D : p.x.p, ypre ? p.L * p.D * 4 : 0);
+  // the (b, tile) rows of the dB / dC partials, (L, NP) each (the host keeps them below 2^31 bytes)
+  const int64_t wrow = (b * p.ntiles + tile) * p.L * NP;
+  const RowRef rwB = flat_ref((const float *)p.ws_dB + wrow, p.L * NP * 4);
+  const RowRef rwC = flat_ref((const float *)p.ws_dC + wrow, p.L * NP * 4);
   const uint32_t offK = (uint32_t)((dval ? d : 0) * NP + n) * 4u;
   const uint32_t offY = (uint32_t)(ypre_index(!xt, 0, tj, dw + tc, p.L, p.D) * 4);
   const uint32_t tstepY = (uint32_t)((xt ? 1 : (int)p.D) * CK * 4);
@@ -674,20 +679,22 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
     const int t0 = kc * CK;
     if constexpr (LR) T.lr.load(rblr, offLR + (uint32_t)(t0 * (int)p.dtl.s1 * ES), tstepLR, rvLR);
     if constexpr (UL) {
-      const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES), tb_ = (uint32_t)(t0 * (int)vB.s1 * ES);
-      if constexpr (!SUM) T.x.v = buf_load_s<IT>(rbx, offX, tx_);
-      if constexpr (!LR) T.dt.v = buf_load_s<IT>(rbdt, offX, tx_);
-      T.g.v = buf_load_s<IT>(rbg, offX, tx_);
-      T.z.v = buf_load_s<IT>(rbz, offZ, (uint32_t)(t0 * (int)vzl.s1 * ES));
+      // the chunk offset goes into the range-checked vector offset: the ragged last chunk's
+      // lanes past the row read 0 (a scalar offset would escape the check)
+      const uint32_t ox = offX + (uint32_t)(t0 * (int)vx.s1 * ES), tb_ = (uint32_t)(t0 * (int)vB.s1 * ES);
+      if constexpr (!SUM) T.x.v = buf_load<IT>(rx.rsrc(), ox);
+      if constexpr (!LR) T.dt.v = buf_load<IT>(rdt.rsrc(), ox);
+      T.g.v = buf_load<IT>(rg.rsrc(), ox);
+      T.z.v = buf_load<IT>(rz.rsrc(), offZ + (uint32_t)(t0 * (int)vzl.s1 * ES));
       if constexpr (!SUM) {
 #pragma unroll
-        for (int i = 0; i < EB; ++i) T.B.v[i] = buf_load_s<IT>(rbB, offB[i], tb_);
+        for (int i = 0; i < EB; ++i) T.B.v[i] = buf_load<IT>(rB.rsrc(), offB[i] + tb_);
       }
 #pragma unroll
-      for (int i = 0; i < EB; ++i) T.C.v[i] = buf_load_s<IT>(rbC, offB[i], tb_);
+      for (int i = 0; i < EB; ++i) T.C.v[i] = buf_load<IT>(rC.rsrc(), offB[i] + tb_);
       if constexpr (!SUM) {
-        T.yp.v = buf_load_s<float>(rby, offY, (uint32_t)kc * tstepY);
-        T.ck = buf_load_s<float>(rbk, offK, (uint32_t)((kc > 0 ? kc - 1 : 0) * (int)p.D * NP * 4));
+        T.yp.v = buf_load<float>(ry.rsrc(), offY + (uint32_t)kc * tstepY);
+        T.ck = buf_load_s<float>(rk.rsrc(), offK, (uint32_t)((kc > 0 ? kc - 1 : 0) * (int)p.D * NP * 4));
       }
     } else {
       if constexpr (!SUM) T.x.load(vx, b, t0, L, dw, D, lane);
@@ -704,6 +711,35 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   };
 
   float Rh[2];  // the half chunks' state sums: lane (r, j) holds step 8 h + j % 8, quantity j / 8
+  // The (dB, dC) sums over the workgroup's channels are software-pipelined: a half chunk's LDS
+  // reads are issued right after its barrier, and summed and stored after the next half's walk,
+  // whose work hides their latency (the two wavefronts of a SIMD belong to one workgroup and
+  // reach the barrier together, so nothing else would).  dq_t: first step of the pending half;
+  // dq_L: the sequence length, 0 when nothing is pending (every store masked).
+  float dq[IPT][CPT];
+#pragma unroll
+  for (int i = 0; i < IPT; ++i)
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) dq[i][j] = 0.0f;
+  int dq_t = 0, dq_L = 0;
+  auto dq_flush = [&]() {
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+      const int item = tid / TPI + i * (NT / TPI), part = tid % TPI;
+      const int st = item / (2 * NP), q = (item / NP) % 2, nn = item % NP;
+      float sum = pairwise_sum(dq[i]);
+      if constexpr (TPI == 2) sum += dpp_f<0xB1>(sum);  // the partner lane's channels (same bits in both)
+      const int tg = dq_t + st;
+      if constexpr (UL) {  // two masked stores: q differs between the lanes of a wavefront
+        const uint32_t ow = (uint32_t)((st * NP + nn) * 4), tw = (uint32_t)(dq_t * NP * 4);
+        const bool ok = part == 0 && tg < dq_L;
+        buf_store_s<float>(rwB.rsrc(), ow, tw, ok && q == 0, sum);
+        buf_store_s<float>(rwC.rsrc(), ow, tw, ok && q == 1, sum);
+      } else if (part == 0 && tg < dq_L) {
+        ((float *)(q == 0 ? p.ws_dB : p.ws_dC))[((b * p.ntiles + tile) * p.L + tg) * NP + nn] = sum;
+      }
+    }
+  };
   auto chunk = [&](Tiles &T, int k) {
     const bool live = k >= k0;
     const int t0 = (live ? k : k0) * CK;
@@ -743,8 +779,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
       if constexpr (!SUM) {
         const float dzv = g0 * T.yp.v * sz * (1.0f + zv * (1.0f - sz));
         if constexpr (UL) {
-          buf_store_s<IT>(row_buffer(vdz, b, L, D, ES), offDZ, (uint32_t)(t0 * (int)vdz.s1 * ES), ev && G::lead(lane),
-                          dzv);
+          buf_store_s<IT>(rdz.rsrc(), offDZ, (uint32_t)(t0 * (int)vdz.s1 * ES), ev && G::lead(lane), dzv);
         } else if (ev && G::lead(lane)) {
           Conv<IT>::store(vpw<IT>(vdz) + b * vdz.s0 + (int64_t)(t0 + tj) * vdz.s1 + (int64_t)(dw + tc) * vdz.s2, dzv);
         }
@@ -833,6 +868,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
         }
       });
       if constexpr (!SUM) {
+        dq_flush();  // the previous half's (dB, dC) sums: their reads completed during this walk
         wave_lds_sync();
         // (dx, ddelta) of step 8 half + j % 8: lane (r, j) sums quantity j / 8 over the states
         {
@@ -840,20 +876,16 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
           lds_row(&S.pn[tj % RH][tc][tj / RH][0], part);
           Rh[half] = pairwise_sum(part);
         }
-        // (dB, dC): sum over the workgroup's channels
+        // (dB, dC): sum over the workgroup's channels -- the reads now, the sums after the next walk
         lds_barrier();
 #pragma unroll
         for (int i = 0; i < IPT; ++i) {
           const int item = tid / TPI + i * (NT / TPI), part = tid % TPI;
           const int st = item / (2 * NP), q = (item / NP) % 2, nn = item % NP;
-          float v[CPT];
-          lds_row(&pdw[half][st][q][nn][part * CPT], v);
-          float sum = pairwise_sum(v);
-          if constexpr (TPI == 2) sum += dpp_f<0xB1>(sum);  // the partner lane's channels (same bits in both)
-          const int tg = t0 + half * RH + st;
-          if (part == 0 && tg < Lc)
-            ((float *)(q == 0 ? p.ws_dB : p.ws_dC))[((b * p.ntiles + tile) * p.L + tg) * NP + nn] = sum;
+          lds_row(&pdw[half][st][q][nn][part * CPT], dq[i]);
         }
+        dq_t = t0 + half * RH;
+        dq_L = Lc;
       }
     });
     (void)par;
@@ -876,8 +908,8 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
     const bool st = ev && G::lead(lane);
     if constexpr (UL) {
       const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES);
-      buf_store_s<IT>(row_buffer(vdx, b, L, D, ES), offX, tx_, st, dxo);
-      buf_store_s<IT>(row_buffer(vddt, b, L, D, ES), offX, tx_, st, ddo);
+      buf_store_s<IT>(rdx.rsrc(), offX, tx_, st, dxo);
+      buf_store_s<IT>(rddt.rsrc(), offX, tx_, st, ddo);
     } else if (st) {
       const int tg = t0 + tj, dd = dw + tc;
       Conv<IT>::store(vpw<IT>(vdx) + b * vdx.s0 + (int64_t)tg * vdx.s1 + (int64_t)dd * vdx.s2, dxo);
@@ -890,24 +922,26 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   load(T0, k1 - 1);
   chunk(T0, k1 - 1);
   for (int k = k1 - 2; k >= k0 - 1; --k) chunk(T0, k);  // ends on an inert chunk
+  if constexpr (!SUM) dq_flush();  // the inert chunk's last half (every store masked)
 
   // lambda a of the segment's first step (an inert chunk after it already applied it: m_next = 0)
   const double lam_a = M1 ? lam + (double)m_next * lam : lam * (double)m_next;
+  const BwdParams &q = params_here<BwdParams>();  // fields read after the loop are loaded here
   if constexpr (SUM) {
     if (dval && nval) {
-      ((double *)p.seg_E)[sidx] = lam_a;
-      ((float *)p.seg_P)[sidx] = prod;
+      ((double *)q.seg_E)[sidx] = lam_a;
+      ((float *)q.seg_P)[sidx] = prod;
     }
     return;
   } else {
-    if (dval) ((float *)p.ws_dA)[sidx] = (float)(M1 ? dA64 * (double)ac.invA : dA64);
-    if (p.has_dh0 && dval && nval && seg == 0)
-      vstore<float>(p.dh0, b * p.dh0.s0 + d * p.dh0.s1 + n * p.dh0.s2, (float)lam_a);
+    if (dval) ((float *)q.ws_dA)[sidx] = (float)(M1 ? dA64 * (double)ac.invA : dA64);
+    if (q.has_dh0 && dval && nval && seg == 0)
+      vstore<float>(q.dh0, b * q.dh0.s0 + d * q.dh0.s1 + n * q.dh0.s2, (float)lam_a);
     // dD and d_bias: the lead row's lanes hold one step slot each; sum them (fixed order)
     const float sD = row_sum((float)dDp), sb = row_sum((float)dbp);
     if (G::lead(lane) && tj == 0 && tval) {
-      ((float *)p.ws_dD)[(b * p.nseg + seg) * p.D + dw + tc] = sD;
-      ((float *)p.ws_db)[(b * p.nseg + seg) * p.D + dw + tc] = sb;
+      ((float *)q.ws_dD)[(b * q.nseg + seg) * q.D + dw + tc] = sD;
+      ((float *)q.ws_db)[(b * q.nseg + seg) * q.D + dw + tc] = sb;
     }
   }
 }

@@ -146,6 +146,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t flat_buffer(const void *base, 
   return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, kBufferFlags);
 }
 
+// The kernel's parameter block (its only argument, at the start of the kernarg segment), read
+// through a pointer the compiler cannot see through: fields read after a long loop are loaded
+// there, instead of being loaded at entry and held (or spilled) across the loop.
+template <typename P>
+__device__ __forceinline__ const P &params_here() {
+  const __attribute__((address_space(4))) P *pk =
+      (const __attribute__((address_space(4))) P *)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(pk));
+  return *(const P *)pk;  // the loads keep the constant address space (scalar loads)
+}
+
+// A buffer kept as its base and extent, the descriptor rebuilt where it is used.  A kernel with
+// many buffers live across its chunk loop holds four SGPRs per descriptor and spills them (every
+// spilled SGPR costs a VALU lane write and read); the base takes two.  The empty asm makes the
+// base opaque at each use, so the compiler cannot hoist the descriptor out of the loop.
+struct RowRef {
+  const char *base;
+  int ext;
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc() const {
+    const char *b = base;
+    asm volatile("" : "+s"(b));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)b, (short)0, ext, kBufferFlags);
+  }
+};
+__device__ __forceinline__ RowRef row_ref(const KView &V, int64_t b, int L, int C, int esize) {
+  const int64_t ext = ((int64_t)(L - 1) * V.s1 + (int64_t)(C - 1) * V.s2 + 1) * esize;
+  return RowRef{(const char *)V.p + b * V.s0 * esize, (int)ext};
+}
+__device__ __forceinline__ RowRef flat_ref(const void *base, int64_t bytes) {
+  return RowRef{(const char *)base, (int)bytes};
+}
+
 // Byte offsets (at t0 = 0) of the tile elements a lane stages, for a view with element size `esize`.
 template <int ROWS, int COLS, int E>
 __device__ __forceinline__ void tile_offsets(uint32_t (&off)[E], const KView &V, int c0, bool tfast, int lane,
