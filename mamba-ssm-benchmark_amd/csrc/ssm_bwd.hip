@@ -788,6 +788,11 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
     const float hstart = k <= 0 ? h0v : T.ck;
     wave_lds_sync();
     load(T, k - 1);
+    // the chunk's B and C rows of this lane's state, read once: the recompute and the walk use
+    // them from its first step on
+    float rBa[CK], rCa[CK];
+    if constexpr (!SUM) lds_row(&S.B[n][0], rBa);
+    lds_row(&S.C[n][0], rCa);
 
     // ------------------------------------------------------------ recompute the chunk's states
     float am[CK], bx[CK], hh[CK + 1];
@@ -802,7 +807,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
         disc<METHOD>(dtb, ac, am[t], cf);
       }
       if constexpr (!SUM) {
-        bx[t] = S.B[n][t] * row_bcast<t>(xv);
+        bx[t] = rBa[t] * row_bcast<t>(xv);
         if constexpr (M1) hh[t + 1] = fmaf(am[t], fmaf(bx[t], ac.invA, hh[t]), hh[t]);
         else hh[t + 1] = fmaf(am[t], hh[t], bcoef<METHOD>(dtb, cf) * bx[t]);
       }
@@ -817,9 +822,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
     order_after(xvw, lamf);
     static_for_down<0, CK / RH>([&](auto hcst) {
       constexpr int half = decltype(hcst)::value;
-      float rC[RH], rB[RH];
-      lds_row(&S.C[n][half * RH], rC);
-      if constexpr (!SUM) lds_row(&S.B[n][half * RH], rB);
+      const float *rC = rCa + half * RH, *rB = rBa + half * RH;
       static_for_down<0, RH>([&](auto tcst) {
         constexpr int tt = decltype(tcst)::value;
         constexpr int t = half * RH + tt;
@@ -868,12 +871,13 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
         }
       });
       if constexpr (!SUM) {
-        dq_flush();  // the previous half's (dB, dC) sums: their reads completed during this walk
         wave_lds_sync();
-        // (dx, ddelta) of step 8 half + j % 8: lane (r, j) sums quantity j / 8 over the states
+        // (dx, ddelta) of step 8 half + j % 8: lane (r, j) sums quantity j / 8 over the states;
+        // the previous half's (dB, dC) sums (read during this walk) are formed meanwhile
         {
           float part[NP];
           lds_row(&S.pn[tj % RH][tc][tj / RH][0], part);
+          dq_flush();
           Rh[half] = pairwise_sum(part);
         }
         // (dB, dC): sum over the workgroup's channels -- the reads now, the sums after the next walk
