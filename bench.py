@@ -633,6 +633,7 @@ def main():
                                                                  "copy"])
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--seqlen", type=int, default=131072)
+    ap.add_argument("--lengths", default="4096,16384,65536", help="long: the sequence lengths")
     ap.add_argument("--segments", type=int, default=0, help="forward time segments (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="report the eager step (no HIP-graph replay)")
@@ -661,7 +662,7 @@ def main():
     elif args.workload == "c4":
         rec = bench_decode(args, dev)
     elif args.workload == "long":
-        rec = bench_long(args, dev)
+        rec = bench_long(args, dev, tuple(int(v) for v in args.lengths.split(",")))
     elif args.workload == "scans":
         rec = bench_scans(args, dev)
     else:
