@@ -98,6 +98,8 @@ template <> __device__ __forceinline__ double buf_load<double>(__amdgpu_buffer_r
   return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
 }
 // The same with a uniform (scalar) offset added by the hardware: a chunk's offset costs no VALU.
+// The range check covers the vector offset only, so these serve reads known to lie inside the
+// buffer; a read that may run past it puts its whole offset in `off` (buf_load).
 template <typename IT> __device__ __forceinline__ float buf_load_s(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff);
 template <> __device__ __forceinline__ float buf_load_s<float>(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, (int)soff, 0));
@@ -107,9 +109,6 @@ template <> __device__ __forceinline__ float buf_load_s<bf16_t>(__amdgpu_buffer_
 }
 template <> __device__ __forceinline__ float buf_load_s<f16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
   return (float)__builtin_bit_cast(f16_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, (int)soff, 0));
-}
-__device__ __forceinline__ double buf_load_f64s(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
-  return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, (int)soff, 0));
 }
 
 // Raw buffer stores.  A lane whose `ok` is false stores to an offset past the buffer's extent
