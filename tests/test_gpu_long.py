@@ -8,7 +8,8 @@ pass, carry over segment summaries, main pass) -- the structure of scan_chunked
   * the automatic choice at B1 D64 L8192;
   * BASELINE config 2 at its largest length, B1 L131072 D512 N16, float32 and bf16
     (rtol 1e-4 / atol 1e-5 float32; 2e-2 bf16), against the C fp64 oracle;
-  * the backward at B1 L65536 D512 N16 (gate + D skip), walked in time segments.
+  * the backward at B1 L65536 D512 N16 (gate + D skip), walked in time segments;
+  * forced segments with 16-bit inputs, and with a strided (non-uniform) layout.
 """
 
 import numpy as np
@@ -117,3 +118,50 @@ def test_long_sequence_backward_matches_c_oracle(dev):
           flush=True)
     assert np.all(err[bad] <= 2.0 ** -16 * m[bad]), "an outlier exceeds float32 resolution of its terms"
     assert bad.sum() <= bad.size // 1_000_000, int(bad.sum())
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float16, 4e-3)])
+def test_forced_segments_half_precision(dev, dtype, tol):
+    """16-bit x, delta, B, C, z with both passes in 4 time segments (gate, D skip, bias +
+    softplus, h0 and a gradient on the last state), against the oracle on the rounded inputs at
+    the 16-bit rounding of the outputs (as the unsegmented half-precision test)."""
+    B, L, D, N = 2, 150, 40, 16
+    x, delta, A, Bm, Cm, h0 = triton_test_inputs(B, L, D, N, True, seed=31)
+    g = torch.Generator().manual_seed(32)
+    Dv, bias = torch.randn(D, generator=g), torch.randn(D, generator=g) * 0.5 - 1.0
+    z = torch.randn(B, L, D, generator=g)
+    dout = torch.randn(B, L, D, generator=g).to(dtype)
+    dlast = torch.randn(B, D, N, generator=g)
+    lo = [t.to(dtype) for t in (x, delta, Bm, Cm, z)]
+    ins = (lo[0], lo[1], A, lo[2], lo[3], h0)
+    got = run_seg(ins, dev, "zoh", 4, D=Dv, z=lo[4], bias=bias, softplus=True, dout=dout, dlast=dlast)
+    ref = oracle(ins, "zoh", D=Dv, z=lo[4], bias=bias, softplus=True, dout=dout, dlast=dlast)
+    check_all(got, ref, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("method", ["zoh", "bilinear"])
+def test_forced_segments_strided_layout(dev, method):
+    """x and z as the two halves of one (B, L, 2D) buffer (row stride 2D, the in_proj split of
+    models/mamba.py:100) while delta is contiguous: not a uniform layout, so both passes take the
+    strided-address path, here in 3 time segments; every output and gradient at the bar."""
+    B, L, D, N = 2, 120, 32, 16
+    x, delta, A, Bm, Cm, h0 = triton_test_inputs(B, L, D, N, True, seed=41)
+    g = torch.Generator().manual_seed(42)
+    z = torch.randn(B, L, D, generator=g)
+    Dv = torch.randn(D, generator=g)
+    dout = torch.randn(B, L, D, generator=g)
+    xz = torch.cat([x, z], -1).to(dev).requires_grad_()
+    xg, zg = xz[..., :D], xz[..., D:]
+    assert xg.stride() == (L * 2 * D, 2 * D, 1)
+    leaves = [t.to(dev).requires_grad_() for t in (delta, A, Bm, Cm, Dv, h0)]
+    dg, Ag, Bg, Cg, Dg, hg = leaves
+    out, last = ssm_scan.selective_scan_fn(xg, dg, Ag, Bg, Cg, D=Dg, z=zg, h0=hg, method=method,
+                                           return_last_state=True, segments=3)
+    (out * dout.to(dev)).sum().backward()
+    rout, rlast, rg = oracle((x, delta, A, Bm, Cm, h0), method, D=Dv, z=z, dout=dout)
+    close(out, rout, name="out")
+    close(last, rlast, name="last")
+    close(xz.grad[..., :D], rg["dx"], name="dx")
+    close(xz.grad[..., D:], rg["dz"], name="dz")
+    for name, t in zip(("ddelta", "dA", "dB", "dC", "dD", "dh0"), leaves):
+        close(t.grad, rg[name], name=name)

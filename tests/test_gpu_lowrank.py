@@ -186,3 +186,16 @@ def test_lowrank_with_initial_state_and_last_gradient(dev):
         res.append([out.detach(), last.detach()] + [t.grad for t in leaves])
     for i, (a, b_) in enumerate(zip(*res)):
         close(a, np64(b_), name=str(i))
+
+
+def test_lowrank_backward_in_segments(dev):
+    """The projected-delta path with both passes in 5 time segments: outputs and every gradient
+    (incl. dW through the fused projection) against the float64 oracle."""
+    B, L, D, N, Rk = 2, 200, 32, 16, 16
+    ins = make(B, L, D, N, Rk, seed=51)
+    out, last, grads = run(dev, *ins, Rk, N, "zoh", segments=5)
+    rout, rlast, rg = oracle(*ins, Rk, N, "zoh")
+    close(out, rout, name="out")
+    close(last, rlast, name="last")
+    for k, v in grads.items():
+        close(v, rg[k], name=k)
