@@ -26,6 +26,7 @@ time fraction; c4's decode latency per layer at batch 64) and the long-sequence 
 Other workloads (--workload): c0 (forward, B1 L512), c2 / c2bf16 (long-sequence forward),
 c3 (10-layer Mamba LM fwd+bwd), c4 (decode latency per layer at batch 64, HIP-graph replay),
 long (B1 D512 N16 fwd+bwd at L 4096 / 16384 / 65536, the reference's bench_scan shape),
+refdecode (the reference's own decode benchmark: batch 1, 11 layers, bf16 autocast),
 scans (the composed path's linear-scan algorithms and discretization, GB/s per kernel),
 copy (a plain device copy of known size, for PMC counter calibration).
 """
@@ -468,6 +469,88 @@ def bench_decode(args, dev):
             "tokens_per_s": B / (ms * 1e-3), **({"cpu_baseline": rec_cpu} if rec_cpu else {})}
 
 
+REF_DECODE_MS = 0.9188  # results/csv/bench_decode.csv:9 (mamba, context 128, graph replay)
+
+
+def bench_refdecode(args, dev):
+    """The reference's own decode benchmark (benchmarks/bench_decode.py:27-61, the "mamba" preset
+    of models/lm.py:150-152): the 11-layer Mamba LM (d_model 256), batch 1, one token step inside
+    a bf16 autocast region with a bf16 conv state and a float32 SSM state (N(0,1)).  `value` is
+    the fused token step (FastDecoder: per layer one in_proj GEMM, the fused decode layer, one
+    out_proj + residual GEMM, computed in float32, the conv state kept in bf16) replayed from a
+    HIP graph; beside it the model's own decode path under autocast (the structure of
+    models/mamba.py: the engine's conv and scan step kernels between bf16 GEMMs), eager and
+    replayed.  The reference's published time is on an RTX 3050 Laptop GPU (0.919 ms/token,
+    graph replay)."""
+    from ssm_scan.block import MambaLM
+    from ssm_scan.decode import FastDecoder
+    torch.manual_seed(0)
+    model = MambaLM(n_layers=11).to(dev).eval()
+    g = torch.Generator().manual_seed(1)
+
+    def fresh_states(dtype):
+        st = model.init_state(1, 129, dev, dtype=dtype)
+        for s_ in st:
+            s_.conv.copy_(torch.randn(s_.conv.shape, generator=g))
+            s_.ssm.copy_(torch.randn(s_.ssm.shape, generator=g))
+        return st
+
+    tok = torch.randint(0, 256, (1, 1), generator=g).to(dev)
+    states = fresh_states(torch.bfloat16)
+
+    def module_step():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
+            return model(tok, states, 128)
+
+    fast = FastDecoder(model)
+    fstates = fresh_states(torch.bfloat16)
+
+    def fast_step():
+        with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
+            return fast.step(tok, fstates)
+
+    def timed(fn, n):
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / n
+
+    def graphed(step):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        return graph
+
+    n = max(args.decode_steps, 50)
+    eager_ms = timed(module_step, n)
+    graph_ms = timed(graphed(module_step).replay, n)
+    fast_eager_ms = timed(fast_step, n)
+    fast_graph_ms = timed(graphed(fast_step).replay, n)
+    return {"metric": "Mamba LM decode latency per token, batch 1, 11 layers, bf16 autocast (reference bench_decode)",
+            "value": fast_graph_ms, "unit": "ms/token", "n_gpus": 1, "steps": n, "warmup": 10,
+            "ms_per_step": fast_graph_ms, "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": fast_graph_ms / REF_DECODE_MS,
+            "baseline_note": "value / the reference's published 0.919 ms/token (RTX 3050 Laptop GPU, graph replay, "
+                             "results/csv/bench_decode.csv:9)",
+            "dtype": "f32", "data": "synthetic (random byte, random-init weights, N(0,1) states)",
+            "config": {"workload": "reference decode benchmark: mamba preset (11 Mamba layers, d_model 256), batch 1, "
+                                   "in a bf16 autocast region, conv state bf16, ssm state f32, HIP-graph replay of the "
+                                   "fused token step (float32 compute)",
+                       "batch": 1, "layers": 11, "d_model": 256, "d_inner": 512, "dstate": 16},
+            "fused_ms_per_token": {"eager": fast_eager_ms, "graph": fast_graph_ms},
+            "module_path_bf16_autocast_ms_per_token": {"eager": eager_ms, "graph": graph_ms}}
+
+
 def cpu_baseline_decode(model, B, budget_s=10.0):
     """The reference's decode step on the host: the torch-CPU restatement of models/mamba.py's
     recurrent step inside models/lm.py's LM (oracle/lm_ref, float32 here), one token for the
@@ -629,8 +712,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "c3", "c4", "long", "scans",
-                                                                 "copy"])
+    ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "c3", "c4", "long", "refdecode",
+                                                                 "scans", "copy"])
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--seqlen", type=int, default=131072)
     ap.add_argument("--lengths", default="4096,16384,65536", help="long: the sequence lengths")
@@ -661,6 +744,8 @@ def main():
         rec = bench_lm(args, dev)
     elif args.workload == "c4":
         rec = bench_decode(args, dev)
+    elif args.workload == "refdecode":
+        rec = bench_refdecode(args, dev)
     elif args.workload == "long":
         rec = bench_long(args, dev, tuple(int(v) for v in args.lengths.split(",")))
     elif args.workload == "scans":

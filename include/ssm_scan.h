@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 4
+#define SSM_ABI_VERSION 5
 
 enum { SSM_OK = 0, SSM_EINVAL = 1, SSM_EKEY = 2, SSM_ESPACE = 3, SSM_EHIP = 4 };
 
@@ -166,18 +166,20 @@ typedef struct ssm_step_args {
  *   x = silu(conv(conv_state, x) + conv_bias);  conv_state <- shifted  (models/mamba.py:104-107)
  *   dt, B, C = x_proj(x);  delta = softplus(dt_proj(dt) + dt_bias)     (:75-76)
  *   h <- a h + b (ssm_state, in place);  y = (C h + Dskip x) silu(z)   (:113-118, :124)
- * All tensors float32 and row-major; dstate <= 64; one workgroup per batch row. */
+ * All tensors float32 (the conv state float32 or bf16) and row-major; dstate <= 64; one
+ * workgroup per batch row. */
 typedef struct ssm_decode_args {
   int64_t batch, dim, dstate, width, dt_rank, d_model;
   int32_t method;          /* SSM_ZOH / SSM_EULER / SSM_BILINEAR */
-  int32_t reserved0;
+  int32_t conv_state_dtype; /* SSM_F32 or SSM_BF16 (the state of a bf16-autocast model) */
   float eps;               /* RMSNorm epsilon */
   float reserved1;
   const float *u;          /* (B, d_model) block input (the residual stream) */
   const float *xz;         /* (B, 2*dim) = u @ (W_in diag(norm_w))^T */
   const float *conv_w;     /* (dim, width) */
   const float *conv_b;     /* (dim,) */
-  float *conv_state;       /* (B, dim, width-1), updated in place */
+  void *conv_state;        /* (B, dim, width-1) of conv_state_dtype, updated in place (a bf16
+                              state stores the new inputs rounded to bf16) */
   const float *x_proj_wt;  /* (dim, dt_rank + 2*dstate): x_proj's weight transposed */
   const float *dt_proj_w;  /* (dim, dt_rank) */
   const float *dt_bias;    /* (dim,) */

@@ -683,6 +683,8 @@ int ssm_decode_check(const ssm_decode_args *a) {
   if (!a->u || !a->xz || !a->conv_w || !a->conv_b || !a->conv_state || !a->x_proj_wt || !a->dt_proj_w ||
       !a->dt_bias || !a->A_log || !a->Dskip || !a->ssm_state || !a->y)
     return fail(SSM_EINVAL, "a required decode tensor is missing");
+  if (a->conv_state_dtype != SSM_F32 && a->conv_state_dtype != SSM_BF16)
+    return fail(SSM_EINVAL, "conv_state_dtype %d: the conv state is float32 or bf16", a->conv_state_dtype);
   return ok();
 }
 
@@ -696,7 +698,8 @@ int ssm_decode_step(const ssm_decode_args *a, void *stream) {
   p.eps = a->eps;
   p.u = a->u; p.xz = a->xz; p.conv_w = a->conv_w; p.conv_b = a->conv_b; p.x_proj_wt = a->x_proj_wt;
   p.dt_proj_w = a->dt_proj_w; p.dt_bias = a->dt_bias; p.A_log = a->A_log; p.Dskip = a->Dskip;
-  p.conv_state = a->conv_state; p.ssm_state = a->ssm_state; p.y = a->y;
+  p.conv_state = a->conv_state; p.conv_bf16 = a->conv_state_dtype == SSM_BF16;
+  p.ssm_state = a->ssm_state; p.y = a->y;
   if (decode_shared_bytes(p) > 64 * 1024) return fail(SSM_EINVAL, "decode layer too wide for one workgroup");
   hipError_t e = launch_decode(p, a->method, (hipStream_t)stream);
   return e == hipSuccess ? ok() : hip_fail(e, "ssm_decode_step");

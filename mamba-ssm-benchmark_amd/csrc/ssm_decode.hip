@@ -15,6 +15,16 @@
 
 namespace ssm {
 
+// The conv state is float32, or bf16 (the state of a bf16-autocast model, models/mamba.py:86-91):
+// element j of the state at `base` read as float / written rounded to the state's type.
+__device__ __forceinline__ float cs_load(const DecodeParams &p, int64_t i) {
+  return p.conv_bf16 ? Conv<bf16_t>::load((const bf16_t *)p.conv_state + i) : ((const float *)p.conv_state)[i];
+}
+__device__ __forceinline__ void cs_store(const DecodeParams &p, int64_t i, float v) {
+  if (p.conv_bf16) Conv<bf16_t>::store((bf16_t *)p.conv_state + i, v);
+  else ((float *)p.conv_state)[i] = v;
+}
+
 constexpr int kDecThreads = 1024;  // 16 wavefronts per row: every phase is short, latency hides
 constexpr int kDecGroups = 16;     // channel groups of the x_proj partial sums
 
@@ -50,18 +60,18 @@ __global__ void __launch_bounds__(kDecThreads) k_decode(const DecodeParams p) {
   for (int d = tid; d < Dm; d += kDecThreads) {
     const float x = s * p.xz[b * 2 * Dm + d];
     zs[d] = s * p.xz[b * 2 * Dm + Dm + d];
-    float *st = p.conv_state + (b * Dm + d) * (W - 1);
+    const int64_t st = (b * Dm + d) * (W - 1);
     float cw[W], win[W > 1 ? W - 1 : 1];
 #pragma unroll
     for (int j = 0; j < W; ++j) cw[j] = p.conv_w[d * W + j];
 #pragma unroll
-    for (int j = 0; j < W - 1; ++j) win[j] = st[j];
+    for (int j = 0; j < W - 1; ++j) win[j] = cs_load(p, st + j);
     float acc = fmaf(cw[W - 1], x, p.conv_b[d]);
 #pragma unroll
     for (int j = 0; j < W - 1; ++j) acc = fmaf(cw[j], win[j], acc);
 #pragma unroll
-    for (int j = 0; j + 1 < W - 1; ++j) st[j] = win[j + 1];
-    if constexpr (W > 1) st[W - 2] = x;
+    for (int j = 0; j + 1 < W - 1; ++j) cs_store(p, st + j, win[j + 1]);
+    if constexpr (W > 1) cs_store(p, st + W - 2, x);
     xs[d] = acc * sigmoidf(acc);
   }
   __syncthreads();
@@ -159,7 +169,10 @@ __global__ void __launch_bounds__(kDecThreads) k_decode_row(const DecodeParams p
     return __builtin_amdgcn_make_buffer_rsrc((void *)q, (short)0, (int)(n * 4), kBufferFlags);
   };
   const auto ru = view(p.u + b * dm, dm), rxz = view(p.xz + b * 2 * Dm, 2 * Dm);
-  const auto rcs = view(p.conv_state + b * Dm * (W - 1), Dm * (W - 1)), rcw = view(p.conv_w, Dm * W);
+  const auto rcw = view(p.conv_w, Dm * W);
+  const int csz = p.conv_bf16 ? 2 : 4;  // conv state element bytes
+  const auto rcs = __builtin_amdgcn_make_buffer_rsrc((char *)p.conv_state + b * Dm * (W - 1) * csz, (short)0,
+                                                     (int)(Dm * (W - 1) * csz), kBufferFlags);
   const auto rcb = view(p.conv_b, Dm), rxp = view(p.x_proj_wt, (int64_t)Dm * P);
   const auto rdt = view(p.dt_proj_w, (int64_t)Dm * R), rdb = view(p.dt_bias, Dm), rds = view(p.Dskip, Dm);
   const auto rh = view(p.ssm_state + b * Dm * N, Dm * N), ral = view(p.A_log, Dm * N);
@@ -171,7 +184,10 @@ __global__ void __launch_bounds__(kDecThreads) k_decode_row(const DecodeParams p
 #pragma unroll
   for (int j = 0; j < W; ++j) cw[j] = ld(rcw, tid * W + j);
 #pragma unroll
-  for (int j = 0; j < W - 1; ++j) st[j] = ld(rcs, tid * (W - 1) + j);
+  for (int j = 0; j < W - 1; ++j) {
+    const uint32_t o = (uint32_t)(tid * (W - 1) + j);
+    st[j] = p.conv_bf16 ? buf_load<bf16_t>(rcs, o * 2u) : buf_load<float>(rcs, o * 4u);
+  }
   const float cb = ld(rcb, tid);
 
   // x_proj weight rows g + 16 k (rows past dim read 0; lanes past P read unused values)
@@ -264,10 +280,10 @@ __global__ void __launch_bounds__(kDecThreads) k_decode_row(const DecodeParams p
     }
   }
   if (tid < Dm) {
-    float *cst = p.conv_state + (b * Dm + tid) * (W - 1);
+    const int64_t cst = (b * Dm + tid) * (W - 1);
 #pragma unroll
-    for (int j = 0; j + 1 < W - 1; ++j) cst[j] = st[j + 1];
-    if constexpr (W > 1) cst[W - 2] = x;
+    for (int j = 0; j + 1 < W - 1; ++j) cs_store(p, cst + j, st[j + 1]);
+    if constexpr (W > 1) cs_store(p, cst + W - 2, x);
   }
 }
 

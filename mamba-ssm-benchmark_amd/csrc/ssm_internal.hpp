@@ -202,7 +202,9 @@ struct DecodeParams {
   int64_t B, dim, N, W, R, dm, P;  // P = R + 2 N
   float eps;
   const float *u, *xz, *conv_w, *conv_b, *x_proj_wt, *dt_proj_w, *dt_bias, *A_log, *Dskip;
-  float *conv_state, *ssm_state, *y;
+  void *conv_state;  // float32, or bf16 when conv_bf16
+  int conv_bf16;
+  float *ssm_state, *y;
 };
 
 // Runs the summary and carry passes first when p.nseg > 1.

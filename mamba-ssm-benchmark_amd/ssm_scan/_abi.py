@@ -11,7 +11,7 @@ import os
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssmscan.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, EINVAL, EKEY, ESPACE, EHIP = 0, 1, 2, 3, 4
 ZOH, EULER, BILINEAR = 0, 1, 2
@@ -65,7 +65,7 @@ class StepArgs(ctypes.Structure):
 
 class DecodeArgs(ctypes.Structure):
     _fields_ = [("batch", c_i64), ("dim", c_i64), ("dstate", c_i64), ("width", c_i64), ("dt_rank", c_i64),
-                ("d_model", c_i64), ("method", c_i32), ("reserved0", c_i32),
+                ("d_model", c_i64), ("method", c_i32), ("conv_state_dtype", c_i32),
                 ("eps", ctypes.c_float), ("reserved1", ctypes.c_float),
                 ("u", c_vp), ("xz", c_vp), ("conv_w", c_vp), ("conv_b", c_vp), ("conv_state", c_vp),
                 ("x_proj_wt", c_vp), ("dt_proj_w", c_vp), ("dt_bias", c_vp), ("A_log", c_vp), ("Dskip", c_vp),

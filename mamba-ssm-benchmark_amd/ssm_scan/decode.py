@@ -59,6 +59,7 @@ class FastDecoder:
         a.eps = L["eps"]
         a.u, a.xz, a.conv_w, a.conv_b = u.data_ptr(), xz.data_ptr(), L["conv_w"].data_ptr(), L["conv_b"].data_ptr()
         a.conv_state = state.conv.data_ptr()
+        a.conv_state_dtype = _abi.DTYPE_CODE[state.conv.dtype]
         a.x_proj_wt, a.dt_proj_w, a.dt_bias = L["x_proj_wt"].data_ptr(), L["dt_proj_w"].data_ptr(), L["dt_bias"].data_ptr()
         a.A_log, a.Dskip = L["A_log"].data_ptr(), L["Dskip"].data_ptr()
         a.ssm_state, a.y = state.ssm.data_ptr(), y.data_ptr()
@@ -68,21 +69,27 @@ class FastDecoder:
 
     @torch.no_grad()
     def step(self, tok, states):
-        """tok (B,) or (B, 1) byte ids; states from model.init_state (float32, contiguous),
-        updated in place.  Returns logits (B, V).
+        """tok (B,) or (B, 1) byte ids; states from model.init_state, contiguous, updated in
+        place: the SSM state float32, the conv state float32 or bf16 (the states of a model run
+        under bf16 autocast, models/mamba.py:86-91; the new conv inputs are stored rounded to
+        bf16).  Returns float32 logits (B, V).  The step computes in float32 also inside a bf16
+        autocast region (its results then differ from the autocast path's by the latter's bf16
+        rounding).
 
         The decode GEMMs are skinny (B rows); they are issued through rocBLAS, whose kernels
         for these shapes take a fraction of hipBLASLt's (torch's default), and torch's choice
         is restored afterwards."""
         for s in states:
-            if not (s.conv.is_contiguous() and s.ssm.is_contiguous() and s.conv.dtype == torch.float32):
-                raise ValueError("decode states must be contiguous float32")
+            if not (s.conv.is_contiguous() and s.ssm.is_contiguous() and s.ssm.dtype == torch.float32
+                    and s.conv.dtype in (torch.float32, torch.bfloat16)):
+                raise ValueError("decode states must be contiguous: ssm float32, conv float32 or bf16")
         prev = torch.backends.cuda.preferred_blas_library()
         torch.backends.cuda.preferred_blas_library("cublas")   # rocBLAS on ROCm
         try:
-            u = self.model.embed(tok.reshape(-1))          # a fresh buffer, updated in place
-            for L, s in zip(self.layers, states):
-                u = self._layer(L, u, s)
-            return self.model.head(self.model.norm_f(u))
+            with torch.autocast(device_type="cuda", enabled=False):
+                u = self.model.embed(tok.reshape(-1))      # a fresh buffer, updated in place
+                for L, s in zip(self.layers, states):
+                    u = self._layer(L, u, s)
+                return self.model.head(self.model.norm_f(u))
         finally:
             torch.backends.cuda.preferred_blas_library(prev)

@@ -207,7 +207,8 @@ def test_lowrank_delta_needs_small_dstate():
         _abi.check(_abi.lib().ssm_fwd_check(ctypes.byref(a)), "ssm_fwd")
 
 
-@pytest.mark.parametrize("field,value", [("dstate", 65), ("width", 9), ("method", 3), ("batch", 0), ("dt_rank", 300)])
+@pytest.mark.parametrize("field,value", [("dstate", 65), ("width", 9), ("method", 3), ("batch", 0), ("dt_rank", 300),
+                                         ("conv_state_dtype", 2), ("conv_state_dtype", 3)])
 def test_decode_layer_validation(field, value):
     """ssm_decode_check rejects out-of-range layer shapes before any launch."""
     a = _abi.DecodeArgs()

@@ -316,3 +316,50 @@ def test_fast_decoder_matches_float64_reference(dev, shape):
     for i, (s, r) in enumerate(zip(states, rstates)):
         close(s.ssm, r["ssm"], name=f"layer {i} ssm state")
         close(s.conv, r["conv"], name=f"layer {i} conv state")
+
+
+# the row-resident kernel (LM preset) and the general one (dstate 12, width 5)
+BF16_STATE_SHAPES = [dict(n_layers=4), dict(n_layers=2, d_state=12, d_conv=5)]
+
+
+@pytest.mark.parametrize("shape", BF16_STATE_SHAPES, ids=lambda s: "-".join(f"{k}{v}" for k, v in s.items()))
+def test_fast_decoder_bf16_conv_state(dev, shape):
+    """The states of a model run under bf16 autocast (conv state bf16, SSM state float32,
+    models/mamba.py:86-91): FastDecoder.step inside a bf16 autocast region computes in float32
+    and stores the new conv inputs rounded to bf16.  Checked, batch 16 and 6 tokens, against the
+    float64 restatement whose conv state is rounded to bf16 after every update the same way.
+
+    The rounding of a conv input to bf16 may fall on the other side of a rounding boundary in
+    float64 than in float32 (rarely); the tolerance is the north_star's bf16 bar (rtol 2e-2,
+    atol 2e-2 x max|.|), and the count of elements outside the float32 bar is printed."""
+    from ssm_scan.decode import FastDecoder
+    from parity import close, outside
+    torch.manual_seed(21)
+    model = MambaLM(**shape).to(dev).eval()
+    m = model.blocks[0].mixer
+    fast = FastDecoder(model)
+    B, T = 16, 6
+    g = torch.Generator().manual_seed(22)
+    states = model.init_state(B, 1, dev, dtype=torch.bfloat16)
+    for s_ in states:
+        s_.ssm.copy_(torch.randn(s_.ssm.shape, generator=g))
+        s_.conv.copy_(torch.randn(s_.conv.shape, generator=g))
+    assert states[0].conv.dtype == torch.bfloat16 and states[0].ssm.dtype == torch.float32
+    rstates = [{"conv": s_.conv.double().cpu(), "ssm": s_.ssm.double().cpu()} for s_ in states]
+    p = {k: v.detach().cpu().double() for k, v in model.state_dict().items()}
+    toks = torch.randint(0, 256, (T, B, 1), generator=g)
+    for t in range(T):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            got = fast.step(toks[t].to(dev), states)
+        assert got.dtype == torch.float32
+        with torch.no_grad():
+            ref = lm_ref.lm_forward(p, toks[t], n_layers=shape["n_layers"], d_state=m.d_state, dt_rank=m.dt_rank,
+                                    d_conv=m.d_conv, states=rstates, method=m.discretization)[:, 0]
+        for r in rstates:
+            r["conv"] = r["conv"].to(torch.bfloat16).double()
+        scale = float(ref.abs().max())
+        print(f"token {t}: logits outside the float32 bar: {outside(got, ref, 1e-4, 1e-5 * scale)}", flush=True)
+        close(got, ref, rtol=2e-2, atol=2e-2 * scale, name=f"logits token {t}")
+    for i, (s_, r) in enumerate(zip(states, rstates)):
+        close(s_.ssm, r["ssm"], rtol=2e-2, atol=2e-2, name=f"layer {i} ssm state")
+        close(s_.conv.float(), r["conv"], rtol=2e-2, atol=2e-2, name=f"layer {i} conv state")
