@@ -4,13 +4,15 @@
 Metric: selective-scan fwd+bwd Mtok/s and % HBM peak at B16 L512 D512 N16
 fp32 (config 1: z gate + D skip, upstream grad dy ~ N(0,1)).  A step is one forward and one
 backward of the fused scan over the batch, inputs resident in HBM.  W untimed warmup steps,
-then exactly K steps between two torch.cuda.synchronize() calls.  The step is timed in two
+then exactly K steps between two torch.cuda.synchronize() calls.  The step is timed in three
 launch modes in the same run: eager (Python + autograd launch every step; the kernels' HIP-event
-timer is off in the timed loop) and captured once in a HIP graph and replayed (the replayed
-outputs are checked bitwise against the eager step's).  `value` is the faster of the two and
-`step_mode` names it: the eager step is host-bound when the host is busy, while a graph replay
-adds a fixed launch gap of several microseconds.  `--eager` times the eager step only.  Both
-times are in the record.
+timer is off in the timed loop), captured once in a HIP graph and replayed, and 10 consecutive
+steps captured in one graph (as a training loop captures its iteration) replayed K/10 times;
+every replayed step's outputs are checked bitwise against the eager step's.  `value` is the
+fastest mode and `step_mode` names it: the eager step is host-bound when the host is busy, and
+each graph replay adds a fixed launch gap of several microseconds, which the 10-step graph
+pays once per 10 steps.  `--eager` times the eager step only.  Every mode's time is in the
+record.
 
 Per-entry device times come from HIP events recorded on the launch stream around every
 C-ABI call (ssm_scan.KernelTimer); the dominant entry (ssm_bwd: the backward kernel plus its
@@ -138,12 +140,18 @@ def flush_buffer(dev):
     return torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
 
 
-def time_steps(step, args):
+GRAPH_STEPS = 10  # consecutive steps captured in one graph by the multi-step graph mode
+
+
+def time_steps(step, args, multi=False):
     """(eager ms/step, graph-replay ms/step or None, replay outputs == eager outputs or None).
 
     Eager: W warmup steps, then K steps between two synchronizations.  Graph: the step captured
     once on a side stream and replayed W + K times; the replay's outputs are compared bitwise
-    with the eager step's (the kernels are deterministic)."""
+    with the eager step's (the kernels are deterministic).  multi=True: GRAPH_STEPS consecutive
+    steps captured in one graph (as a training loop captures its iteration), replayed so that
+    exactly K steps run in the timed region (K rounded up to a multiple of GRAPH_STEPS); every
+    step's outputs are compared with the eager step's."""
     for _ in range(args.warmup):
         ref = step()
     torch.cuda.synchronize()
@@ -160,18 +168,20 @@ def time_steps(step, args):
         for _ in range(2):
             step()
     torch.cuda.current_stream().wait_stream(side)
+    per = GRAPH_STEPS if multi else 1
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        gout = step()
-    for _ in range(args.warmup):
+        gouts = [step() for _ in range(per)]
+    reps = (args.steps + per - 1) // per
+    for _ in range(max(1, args.warmup // per)):
         graph.replay()
     torch.cuda.synchronize()
-    ok = all(torch.equal(a, b) for a, b in zip(gout, ref))
+    ok = all(torch.equal(a, b) for gout in gouts for a, b in zip(gout, ref))
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(reps):
         graph.replay()
     torch.cuda.synchronize()
-    return eager_ms, (time.perf_counter() - t0) * 1e3 / args.steps, ok
+    return eager_ms, (time.perf_counter() - t0) * 1e3 / (reps * per), ok
 
 
 def bench_c1(args, dev):
@@ -189,7 +199,16 @@ def bench_c1(args, dev):
         return torch.autograd.grad(out, leaves, dy)
 
     eager_ms, graph_ms, graph_ok = time_steps(step, args)
-    ms_step = min(eager_ms, graph_ms) if graph_ok else eager_ms
+    modes = {"eager launches": eager_ms}
+    if graph_ok:
+        modes["hip-graph replay of the fwd+bwd step"] = graph_ms
+    multi_ms = multi_ok = None
+    if not args.eager:
+        _, multi_ms, multi_ok = time_steps(step, args, multi=True)
+        if multi_ok:
+            modes[f"hip-graph replay of {GRAPH_STEPS} consecutive fwd+bwd steps"] = multi_ms
+    step_mode = min(modes, key=modes.get)
+    ms_step = modes[step_mode]
 
     with ssm_scan.KernelTimer() as timer:
         for _ in range(args.steps):
@@ -224,8 +243,9 @@ def bench_c1(args, dev):
                                "zoh, z gate + D skip, channel-major (B,D,L) storage",
                    "batch": B, "seqlen": L, "dim": D, "dstate": N, "method": "zoh"},
         "hbm_frac_step": (fb + bb) / (ms_step * 1e-3) / (HBM_PEAK_GBS * 1e9),
-        "step_mode": "hip-graph replay of the fwd+bwd step" if ms_step != eager_ms else "eager launches",
+        "step_mode": step_mode,
         "eager_ms_per_step": eager_ms, "graph_ms_per_step": graph_ms, "graph_matches_eager": graph_ok,
+        "graph_multi_ms_per_step": multi_ms, "graph_multi_matches_eager": multi_ok,
         "kernels_ms": {"ssm_fwd": fwd_ms, "ssm_bwd": bwd_ms, "ssm_fwd_cold": cold_f, "ssm_bwd_cold": cold_b},
         "kernels_ms_stats": kstats,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
