@@ -413,11 +413,12 @@ def bench_lm(args, dev):
 
 def bench_decode(args, dev):
     """Config 4: recurrent decode of the config-3 model at batch 64 (fp32 state ~ N(0,1), one
-    random byte per step).  The token step -- per layer one in_proj GEMM (RMSNorm weight
-    folded in), one fused ssm_decode_step launch and one out_proj + residual GEMM -- is
-    captured once in a HIP graph and replayed; 256 steps timed.  The module decode path
-    (models/mamba.py's structure: conv step and scan step kernels between torch ops) is timed
-    beside it, eager and graph-replayed."""
+    random byte per step).  The token step -- the block stack as one ssm_decode_stack call (two
+    launches per block, the in_proj and out_proj GEMMs inside), then the final norm and head --
+    is captured once in a HIP graph and replayed; 256 steps timed.  Beside it: the per-block
+    path (in_proj GEMM, the fused ssm_decode_step launch, out_proj + residual GEMM per block),
+    and the module decode path (models/mamba.py's structure: conv step and scan step kernels
+    between torch ops), eager and graph-replayed."""
     from ssm_scan.block import MambaLM
     from ssm_scan.decode import FastDecoder
     torch.manual_seed(0)
@@ -436,9 +437,13 @@ def bench_decode(args, dev):
             return model(tok, states, 0)
 
     fast = FastDecoder(model)
+    block = FastDecoder(model, path="block")
 
     def fast_step():
         return fast.step(tok, states)
+
+    def block_step():
+        return block.step(tok, states)
 
     def eager_time(step):
         for _ in range(3):
@@ -475,16 +480,19 @@ def bench_decode(args, dev):
     eager_ms = eager_time(module_step)
     module_graph_ms = graph_time(module_step)
     fast_eager_ms = eager_time(fast_step)
+    block_ms = graph_time(block_step)
     ms = graph_time(fast_step)
     rec_cpu = None if args.no_cpu_baseline else cpu_baseline_decode(model, B)
     return {"metric": "Mamba LM decode latency per token per layer, batch 64 (10 layers)", "value": ms * 1e3 / 10,
             "unit": "us/layer", "n_gpus": 1, "steps": args.decode_steps, "warmup": 20, "ms_per_step": ms,
             "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
             "data": "synthetic (random bytes, random-init weights, N(0,1) states)",
-            "config": {"workload": "config 4: recurrent decode step, HIP-graph replay of the 10-layer token step "
-                                   "(fused ssm_decode_step + 2 GEMMs per layer)",
+            "config": {"workload": f"config 4: recurrent decode step, HIP-graph replay of the 10-layer token step "
+                                   f"({fast.path} path: " + ("ssm_decode_stack, 2 launches per layer)" if fast.path == "stack"
+                                                             else "fused ssm_decode_step + 2 GEMMs per layer)"),
                        "batch": B, "layers": 10, "d_model": 256, "d_inner": 512, "dstate": 16, "conv_width": 4},
             "ms_per_token_model": ms, "fused_eager_ms_per_token_model": fast_eager_ms,
+            "block_path_graph_ms_per_token_model": block_ms,
             "module_path_ms_per_token_model": {"eager": eager_ms, "graph": module_graph_ms},
             "tokens_per_s": B / (ms * 1e-3), **({"cpu_baseline": rec_cpu} if rec_cpu else {})}
 
@@ -523,11 +531,16 @@ def bench_refdecode(args, dev):
             return model(tok, states, 128)
 
     fast = FastDecoder(model)
+    block = FastDecoder(model, path="block")
     fstates = fresh_states(torch.bfloat16)
 
     def fast_step():
         with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
             return fast.step(tok, fstates)
+
+    def block_step():
+        with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
+            return block.step(tok, fstates)
 
     def timed(fn, n):
         for _ in range(10):
@@ -555,6 +568,7 @@ def bench_refdecode(args, dev):
     eager_ms = timed(module_step, n)
     graph_ms = timed(graphed(module_step).replay, n)
     fast_eager_ms = timed(fast_step, n)
+    block_graph_ms = timed(graphed(block_step).replay, n)
     fast_graph_ms = timed(graphed(fast_step).replay, n)
     return {"metric": "Mamba LM decode latency per token, batch 1, 11 layers, bf16 autocast (reference bench_decode)",
             "value": fast_graph_ms, "unit": "ms/token", "n_gpus": 1, "steps": n, "warmup": 10,
@@ -565,9 +579,10 @@ def bench_refdecode(args, dev):
             "dtype": "f32", "data": "synthetic (random byte, random-init weights, N(0,1) states)",
             "config": {"workload": "reference decode benchmark: mamba preset (11 Mamba layers, d_model 256), batch 1, "
                                    "in a bf16 autocast region, conv state bf16, ssm state f32, HIP-graph replay of the "
-                                   "fused token step (float32 compute)",
+                                   f"fused token step (float32 compute, {fast.path} path)",
                        "batch": 1, "layers": 11, "d_model": 256, "d_inner": 512, "dstate": 16},
-            "fused_ms_per_token": {"eager": fast_eager_ms, "graph": fast_graph_ms},
+            "fused_ms_per_token": {"eager": fast_eager_ms, "graph": fast_graph_ms, "path": fast.path},
+            "block_path_graph_ms_per_token": block_graph_ms,
             "module_path_bf16_autocast_ms_per_token": {"eager": eager_ms, "graph": graph_ms}}
 
 

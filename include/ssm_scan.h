@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 5
+#define SSM_ABI_VERSION 6
 
 enum { SSM_OK = 0, SSM_EINVAL = 1, SSM_EKEY = 2, SSM_ESPACE = 3, SSM_EHIP = 4 };
 
@@ -179,7 +179,7 @@ typedef struct ssm_decode_args {
   const float *conv_w;     /* (dim, width) */
   const float *conv_b;     /* (dim,) */
   void *conv_state;        /* (B, dim, width-1) of conv_state_dtype, updated in place (a bf16
-                              state stores the new inputs rounded to bf16) */
+                              state stores the new inputs rounded to bf16; NULL when width is 1) */
   const float *x_proj_wt;  /* (dim, dt_rank + 2*dstate): x_proj's weight transposed */
   const float *dt_proj_w;  /* (dim, dt_rank) */
   const float *dt_bias;    /* (dim,) */
@@ -188,6 +188,47 @@ typedef struct ssm_decode_args {
   float *ssm_state;        /* (B, dim, dstate), updated in place */
   float *y;                /* (B, dim) output, the input of out_proj */
 } ssm_decode_args;
+
+/* ------------------------------------------------------------------ decode step of a block stack
+ * The recurrent decode step of a stack of Mamba blocks: the loop over blocks of
+ * models/lm.py:124-128 with states, each block x = x + mixer(norm1(x), state)
+ * (models/lm.py:82-83; RMSNorm models/common.py:14-16; the mixer models/mamba.py:93-124 at
+ * L = 1), in two launches per block plus one at the end.  Unlike ssm_decode_step, the in_proj
+ * and out_proj GEMMs are part of the step, tiled with the rest of the block over the whole GPU.
+ * u (B, d_model) holds the residual stream entering the first block and is replaced by the one
+ * leaving the last (the input of the final norm and head).  Every block has the same
+ * dimensions; tensors are float32 and row-major (conv states float32 or bf16), states are
+ * updated in place, and every sum runs in a fixed order (the step is deterministic).
+ * Supported: d_model <= 512, dim <= 1024, dstate 8 or 16, dt_rank 8, 16 or 32, width <= 4;
+ * ssm_decode_stack_check names the limit a shape breaks. */
+typedef struct ssm_decode_block {
+  const float *w_in_t;     /* (d_model, 2*dim): (W_in diag(norm_w))^T, the RMSNorm weight folded in */
+  const float *conv_w;     /* (dim, width) */
+  const float *conv_b;     /* (dim,) */
+  const float *x_proj_wt;  /* (dim, dt_rank + 2*dstate): x_proj's weight transposed */
+  const float *dt_proj_w;  /* (dim, dt_rank) */
+  const float *dt_bias;    /* (dim,) */
+  const float *A_log;      /* (dim, dstate): A = -exp(A_log) */
+  const float *Dskip;      /* (dim,) */
+  const float *w_out_t;    /* (dim, d_model): out_proj's weight transposed */
+  void *conv_state;        /* (B, dim, width-1) of conv_state_dtype, updated in place (may be
+                              NULL when width is 1) */
+  float *ssm_state;        /* (B, dim, dstate), updated in place */
+  float eps;               /* the block's RMSNorm epsilon */
+  int32_t reserved0;
+} ssm_decode_block;
+
+typedef struct ssm_decode_stack_args {
+  int64_t batch, dim, dstate, width, dt_rank, d_model;
+  int32_t method;          /* SSM_ZOH / SSM_EULER / SSM_BILINEAR */
+  int32_t conv_state_dtype; /* SSM_F32 or SSM_BF16 */
+  int32_t n_blocks;
+  int32_t reserved0;
+  const ssm_decode_block *blocks;  /* host array of n_blocks, read during the call only */
+  float *u;                /* (B, d_model) residual stream, replaced in place */
+  void *workspace;         /* device memory of ssm_decode_stack_workspace_bytes() */
+  int64_t workspace_bytes;
+} ssm_decode_stack_args;
 
 /* ------------------------------------------------------------------ linear scans
  * Replaces the scan algorithms of models/scan.py:70-165 (scan_sequential,
@@ -296,6 +337,7 @@ int ssm_fwd_check(const ssm_fwd_args *args);
 int ssm_bwd_check(const ssm_bwd_args *args);
 int ssm_step_check(const ssm_step_args *args);
 int ssm_decode_check(const ssm_decode_args *args);
+int ssm_decode_stack_check(const ssm_decode_stack_args *args);
 int ssm_lscan_check(const ssm_lscan_args *args);
 int ssm_lscan_bwd_check(const ssm_lscan_bwd_args *args);
 int ssm_disc_check(const ssm_disc_args *args);
@@ -311,12 +353,14 @@ int64_t ssm_lscan_bwd_workspace_bytes(const ssm_lscan_bwd_args *args);
 int64_t ssm_disc_workspace_bytes(const ssm_disc_args *args);
 int64_t ssm_conv_workspace_bytes(const ssm_conv_args *args);
 int64_t ssm_norm_workspace_bytes(const ssm_norm_args *args);
+int64_t ssm_decode_stack_workspace_bytes(const ssm_decode_stack_args *args);
 
 /* Launches (asynchronous on `stream`). */
 int ssm_fwd(const ssm_fwd_args *args, void *stream);
 int ssm_bwd(const ssm_bwd_args *args, void *stream);
 int ssm_step(const ssm_step_args *args, void *stream);
 int ssm_decode_step(const ssm_decode_args *args, void *stream);
+int ssm_decode_stack(const ssm_decode_stack_args *args, void *stream);
 int ssm_lscan(const ssm_lscan_args *args, void *stream);
 int ssm_lscan_bwd(const ssm_lscan_bwd_args *args, void *stream);
 int ssm_disc_fwd(const ssm_disc_args *args, void *stream);

@@ -680,7 +680,7 @@ int ssm_decode_check(const ssm_decode_args *a) {
   if (a->width < 1 || a->width > 8) return fail(SSM_EINVAL, "conv width %lld not in 1..8", (long long)a->width);
   if (a->dstate > 64 || a->dt_rank > 256 || a->dim > 8192)
     return fail(SSM_EINVAL, "decode layer dims out of range (dim <= 8192, dstate <= 64, dt_rank <= 256)");
-  if (!a->u || !a->xz || !a->conv_w || !a->conv_b || !a->conv_state || !a->x_proj_wt || !a->dt_proj_w ||
+  if (!a->u || !a->xz || !a->conv_w || !a->conv_b || (!a->conv_state && a->width > 1) || !a->x_proj_wt || !a->dt_proj_w ||
       !a->dt_bias || !a->A_log || !a->Dskip || !a->ssm_state || !a->y)
     return fail(SSM_EINVAL, "a required decode tensor is missing");
   if (a->conv_state_dtype != SSM_F32 && a->conv_state_dtype != SSM_BF16)
@@ -703,6 +703,116 @@ int ssm_decode_step(const ssm_decode_args *a, void *stream) {
   if (decode_shared_bytes(p) > 64 * 1024) return fail(SSM_EINVAL, "decode layer too wide for one workgroup");
   hipError_t e = launch_decode(p, a->method, (hipStream_t)stream);
   return e == hipSuccess ? ok() : hip_fail(e, "ssm_decode_step");
+}
+
+// ------------------------------------------------------------------ decode step of a block stack
+namespace {
+struct StackLayout {
+  int64_t nct, ndu, P;
+  int64_t off_ua, off_ub, off_du, off_xc, off_gate, off_part, total;
+};
+StackLayout stack_layout(const ssm_decode_stack_args *a) {
+  StackLayout l;
+  const int64_t B = a->batch, dm = a->d_model, Dm = a->dim;
+  l.nct = cdiv(Dm, kInCh);
+  l.ndu = cdiv(Dm, kScCh);
+  l.P = a->dt_rank + 2 * a->dstate;
+  int64_t o = 0;
+  l.off_ua = o; o += align256(B * dm * 4);
+  l.off_ub = o; o += align256(B * dm * 4);
+  l.off_du = o; o += align256(B * l.ndu * dm * 4);
+  l.off_xc = o; o += align256(B * Dm * 4);
+  l.off_gate = o; o += align256(B * Dm * 4);
+  l.off_part = o; o += align256(B * l.nct * l.P * 4);
+  l.total = o;
+  return l;
+}
+}  // namespace
+
+int ssm_decode_stack_check(const ssm_decode_stack_args *a) {
+  if (!a) return fail(SSM_EINVAL, "null args");
+  if (a->method < 0 || a->method > 2)
+    return fail(SSM_EINVAL, "unknown discretization %d (expected zoh=0, euler=1, bilinear=2)", a->method);
+  if (a->batch < 1 || a->dim < 1 || a->dstate < 1 || a->d_model < 1 || a->dt_rank < 1 || a->width < 1)
+    return fail(SSM_EINVAL, "empty decode stack dimensions");
+  if (a->n_blocks < 1 || !a->blocks) return fail(SSM_EINVAL, "no blocks");
+  if (!a->u) return fail(SSM_EINVAL, "u (the residual stream) is missing");
+  if (a->conv_state_dtype != SSM_F32 && a->conv_state_dtype != SSM_BF16)
+    return fail(SSM_EINVAL, "conv_state_dtype %d: the conv state is float32 or bf16", a->conv_state_dtype);
+  if (a->d_model > kStMaxDm) return fail(SSM_EINVAL, "d_model %lld > %d", (long long)a->d_model, kStMaxDm);
+  if (a->dim > kStMaxDim) return fail(SSM_EINVAL, "dim %lld > %d", (long long)a->dim, kStMaxDim);
+  if (a->dstate != 8 && a->dstate != 16) return fail(SSM_EINVAL, "dstate %lld not 8 or 16", (long long)a->dstate);
+  if (a->dt_rank != 8 && a->dt_rank != 16 && a->dt_rank != 32)
+    return fail(SSM_EINVAL, "dt_rank %lld not 8, 16 or 32", (long long)a->dt_rank);
+  if (a->width > 4) return fail(SSM_EINVAL, "conv width %lld > 4", (long long)a->width);
+  // every buffer element is addressed by a 32-bit byte offset (with a few rows of slack)
+  const StackLayout l = stack_layout(a);
+  const int64_t rows = a->batch + kInRows;
+  const int64_t widest = std::max({a->dim * a->dstate, l.ndu * a->d_model, l.nct * l.P, a->dim * a->width, a->d_model});
+  if (rows * widest * 4 >= (1LL << 31) || a->d_model * 2 * a->dim * 4 >= (1LL << 31))
+    return fail(SSM_EINVAL, "decode stack too large for 32-bit offsets (batch %lld)", (long long)a->batch);
+  for (int i = 0; i < a->n_blocks; ++i) {
+    const ssm_decode_block &k = a->blocks[i];
+    if (!k.w_in_t || !k.conv_w || !k.conv_b || !k.x_proj_wt || !k.dt_proj_w || !k.dt_bias || !k.A_log ||
+        !k.Dskip || !k.w_out_t || (!k.conv_state && a->width > 1) || !k.ssm_state)
+      return fail(SSM_EINVAL, "block %d: a required tensor is missing", i);
+  }
+  if (!a->workspace || a->workspace_bytes < l.total)
+    return fail(SSM_ESPACE, "decode stack workspace %lld bytes < %lld", (long long)a->workspace_bytes,
+                (long long)l.total);
+  return ok();
+}
+
+int64_t ssm_decode_stack_workspace_bytes(const ssm_decode_stack_args *a) {
+  if (!a || a->batch < 1 || a->dim < 1 || a->d_model < 1) return -1;
+  return stack_layout(a).total;
+}
+
+int ssm_decode_stack(const ssm_decode_stack_args *a, void *stream) {
+  int rc = ssm_decode_stack_check(a);
+  if (rc) return rc;
+  const StackLayout l = stack_layout(a);
+  const hipStream_t s = (hipStream_t)stream;
+  char *ws = (char *)a->workspace;
+  float *ua = (float *)(ws + l.off_ua), *ub = (float *)(ws + l.off_ub), *du = (float *)(ws + l.off_du);
+  float *xc = (float *)(ws + l.off_xc), *gate = (float *)(ws + l.off_gate), *part = (float *)(ws + l.off_part);
+  const int B = (int)a->batch, dm = (int)a->d_model, Dm = (int)a->dim;
+  // the residual stream entering block i lives in dst(i) (block 0: u itself); k_dec_in of
+  // block i rebuilds it from dst(i - 1) and block i - 1's partial sums
+  auto dst = [&](int i) { return i == 0 ? a->u : (i % 2 ? ua : ub); };
+  for (int i = 0; i < a->n_blocks; ++i) {
+    const ssm_decode_block &k = a->blocks[i];
+    DecInParams pi;
+    memset(&pi, 0, sizeof(pi));
+    pi.B = B; pi.dm = dm; pi.Dm = Dm; pi.P = (int)l.P;
+    pi.nrt = (int)cdiv(B, kInRows); pi.nct = (int)l.nct;
+    pi.ndu = i == 0 ? 0 : (int)l.ndu;
+    pi.write_u = i > 0;
+    pi.conv_bf16 = a->conv_state_dtype == SSM_BF16;
+    pi.eps = k.eps;
+    pi.u_src = i == 0 ? a->u : dst(i - 1);
+    pi.du = i == 0 ? nullptr : du;
+    pi.u_dst = i == 0 ? nullptr : dst(i);
+    pi.w_in_t = k.w_in_t; pi.conv_w = k.conv_w; pi.conv_b = k.conv_b; pi.x_proj_wt = k.x_proj_wt;
+    pi.conv_state = k.conv_state;
+    pi.xc = xc; pi.gate = gate; pi.part = part;
+    hipError_t e = launch_dec_in(pi, (int)a->width, s);
+    if (e != hipSuccess) return hip_fail(e, "ssm_decode_stack in-stage launch");
+    DecScanParams ps;
+    memset(&ps, 0, sizeof(ps));
+    ps.B = B; ps.dm = dm; ps.Dm = Dm; ps.N = (int)a->dstate; ps.R = (int)a->dt_rank; ps.P = (int)l.P;
+    ps.nrt = (int)cdiv(B, kScRows); ps.nct = (int)l.nct; ps.ndu = (int)l.ndu;
+    ps.xc = xc; ps.gate = gate; ps.part = part;
+    ps.dt_proj_w = k.dt_proj_w; ps.dt_bias = k.dt_bias; ps.A_log = k.A_log; ps.Dskip = k.Dskip;
+    ps.w_out_t = k.w_out_t; ps.ssm_state = k.ssm_state; ps.du = du;
+    e = launch_dec_scan(ps, a->method, s);
+    if (e != hipSuccess) return hip_fail(e, "ssm_decode_stack scan-stage launch");
+  }
+  DecOutParams po;
+  po.B = B; po.dm = dm; po.ndu = (int)l.ndu;
+  po.u_src = dst(a->n_blocks - 1); po.du = du; po.u_out = a->u;
+  hipError_t e = launch_dec_out(po, s);
+  return e == hipSuccess ? ok() : hip_fail(e, "ssm_decode_stack output launch");
 }
 
 // ------------------------------------------------------------------ causal depthwise conv

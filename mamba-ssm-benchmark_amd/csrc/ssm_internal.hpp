@@ -207,6 +207,38 @@ struct DecodeParams {
   float *ssm_state, *y;
 };
 
+// The decode step of a whole layer stack in two launches per layer (ssm_decode_stack).
+constexpr int kStThreads = 256;             // threads per workgroup of the stack kernels
+constexpr int kInRows = 4, kInCh = 32;      // k_dec_in tile: rows x channels (x and z columns)
+constexpr int kScRows = 2, kScCh = 64;      // k_dec_scan tile: rows x channels
+constexpr int kStMaxDm = 512, kStMaxDim = 1024;
+constexpr int kStMaxInTiles = kStMaxDim / kInCh;   // x_proj partial sums per row
+constexpr int kStMaxScTiles = kStMaxDim / kScCh;   // out_proj partial sums per row
+struct DecInParams {
+  int B, dm, Dm, P, nrt, nct, ndu, write_u, conv_bf16;
+  float eps;
+  const float *u_src;     // (B, dm) residual stream of the previous layer
+  const float *du;        // (B, ndu, dm) its out_proj partial sums (ndu = 0: none)
+  float *u_dst;           // (B, dm) the residual stream entering this layer (write_u)
+  const float *w_in_t;    // (dm, 2 Dm)
+  const float *conv_w, *conv_b, *x_proj_wt;
+  void *conv_state;
+  float *xc, *gate, *part;  // (B, Dm), (B, Dm), (B, nct, P)
+};
+struct DecScanParams {
+  int B, dm, Dm, N, R, P, nrt, nct, ndu;
+  const float *xc, *gate, *part, *dt_proj_w, *dt_bias, *A_log, *Dskip, *w_out_t;
+  float *ssm_state, *du;  // du: (B, ndu, dm)
+};
+struct DecOutParams {
+  int B, dm, ndu;
+  const float *u_src, *du;
+  float *u_out;
+};
+hipError_t launch_dec_in(const DecInParams &p, int W, hipStream_t s);
+hipError_t launch_dec_scan(const DecScanParams &p, int method, hipStream_t s);
+hipError_t launch_dec_out(const DecOutParams &p, hipStream_t s);
+
 // Runs the summary and carry passes first when p.nseg > 1.
 hipError_t launch_fwd(const FwdParams &p, int dtype, int method, int np, hipStream_t s);
 hipError_t launch_bwd(const BwdParams &p, int dtype, int method, int np, hipStream_t s);

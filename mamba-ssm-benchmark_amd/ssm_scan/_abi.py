@@ -11,7 +11,7 @@ import os
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssmscan.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 OK, EINVAL, EKEY, ESPACE, EHIP = 0, 1, 2, 3, 4
 ZOH, EULER, BILINEAR = 0, 1, 2
@@ -72,6 +72,20 @@ class DecodeArgs(ctypes.Structure):
                 ("ssm_state", c_vp), ("y", c_vp)]
 
 
+
+class DecodeBlock(ctypes.Structure):
+    _fields_ = [("w_in_t", c_vp), ("conv_w", c_vp), ("conv_b", c_vp), ("x_proj_wt", c_vp), ("dt_proj_w", c_vp),
+                ("dt_bias", c_vp), ("A_log", c_vp), ("Dskip", c_vp), ("w_out_t", c_vp),
+                ("conv_state", c_vp), ("ssm_state", c_vp), ("eps", ctypes.c_float), ("reserved0", c_i32)]
+
+
+class DecodeStackArgs(ctypes.Structure):
+    _fields_ = [("batch", c_i64), ("dim", c_i64), ("dstate", c_i64), ("width", c_i64), ("dt_rank", c_i64),
+                ("d_model", c_i64), ("method", c_i32), ("conv_state_dtype", c_i32),
+                ("n_blocks", c_i32), ("reserved0", c_i32),
+                ("blocks", ctypes.POINTER(DecodeBlock)), ("u", c_vp),
+                ("workspace", c_vp), ("workspace_bytes", c_i64)]
+
 class LscanArgs(ctypes.Structure):
     _fields_ = [("batch", c_i64), ("seqlen", c_i64), ("width", c_i64),
                 ("algo", c_i32), ("dtype", c_i32), ("reverse", c_i32), ("reserved0", c_i32),
@@ -123,6 +137,7 @@ _SIGS = {
     "ssm_bwd_check": (c_i32, [ctypes.POINTER(BwdArgs)]),
     "ssm_step_check": (c_i32, [ctypes.POINTER(StepArgs)]),
     "ssm_decode_check": (c_i32, [ctypes.POINTER(DecodeArgs)]),
+    "ssm_decode_stack_check": (c_i32, [ctypes.POINTER(DecodeStackArgs)]),
     "ssm_lscan_check": (c_i32, [ctypes.POINTER(LscanArgs)]),
     "ssm_lscan_bwd_check": (c_i32, [ctypes.POINTER(LscanBwdArgs)]),
     "ssm_disc_check": (c_i32, [ctypes.POINTER(DiscArgs)]),
@@ -136,11 +151,13 @@ _SIGS = {
     "ssm_disc_workspace_bytes": (c_i64, [ctypes.POINTER(DiscArgs)]),
     "ssm_conv_workspace_bytes": (c_i64, [ctypes.POINTER(ConvArgs)]),
     "ssm_norm_workspace_bytes": (c_i64, [ctypes.POINTER(NormArgs)]),
+    "ssm_decode_stack_workspace_bytes": (c_i64, [ctypes.POINTER(DecodeStackArgs)]),
     "ssm_fwd": (c_i32, [ctypes.POINTER(FwdArgs), c_vp]),
     "ssm_fwd_noalloc": (c_i32, [ctypes.POINTER(FwdArgs), c_vp]),
     "ssm_bwd": (c_i32, [ctypes.POINTER(BwdArgs), c_vp]),
     "ssm_step": (c_i32, [ctypes.POINTER(StepArgs), c_vp]),
     "ssm_decode_step": (c_i32, [ctypes.POINTER(DecodeArgs), c_vp]),
+    "ssm_decode_stack": (c_i32, [ctypes.POINTER(DecodeStackArgs), c_vp]),
     "ssm_lscan": (c_i32, [ctypes.POINTER(LscanArgs), c_vp]),
     "ssm_lscan_bwd": (c_i32, [ctypes.POINTER(LscanBwdArgs), c_vp]),
     "ssm_disc_fwd": (c_i32, [ctypes.POINTER(DiscArgs), c_vp]),

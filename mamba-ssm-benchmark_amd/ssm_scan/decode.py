@@ -1,16 +1,26 @@
-"""Fast recurrent decode of a Mamba LM: three launches per layer.
+"""Fast recurrent decode of a Mamba LM.
 
-Per layer the token step is
+The token step of the block stack runs as one C-ABI call (ssm_decode_stack): per block two
+launches spread over the whole GPU,
+    in-stage      the residual stream rebuilt from the previous block's out_proj partial sums,
+                  the RMSNorm scale, the in_proj GEMM tile (the norm weight folded into its
+                  columns), conv step + SiLU with the conv state, the SiLU(z) gate, x_proj
+                  partial sums
+    scan-stage    x_proj sums finished, dt_proj + softplus, the state update, D skip and gate,
+                  out_proj partial sums
+and one launch at the end for the last block's sums; which computes what models/mamba.py:93-124
+(L = 1 with a state) and the pre-norm residual blocks of models/lm.py:82-83,124-128 compute,
+in place of ~20 small launches per block.  Shapes past the stack kernels' limits (d_model > 512,
+dim > 1024, dstate not 8 or 16, dt_rank not 8, 16 or 32, conv width > 4) take the per-block
+path: three launches per block,
     xz = u @ (W_in diag(norm_w))^T          one GEMM (the block's RMSNorm weight folded in)
-    ssm_decode_step(...)                    one fused launch: RMSNorm scale, conv step + SiLU
-                                            with the conv state, x_proj, dt_proj + softplus, the
-                                            state update, D skip and SiLU(z) gate
+    ssm_decode_step(...)                    one fused launch: RMSNorm scale, conv step + SiLU,
+                                            x_proj, dt_proj + softplus, the state update, D
+                                            skip and SiLU(z) gate
     u += y @ W_out^T                        one GEMM with the residual, in place (addmm_)
-which computes what models/mamba.py:93-124 (L = 1 with a state) and the pre-norm residual
-block of models/lm.py compute, in place of ~20 small launches per layer.  The step is
-allocation-free apart from torch's caching allocator, so it can be captured in a HIP graph.
-The folded weights are taken from the model when the decoder is built; call refresh() after
-the model's parameters change.
+The step is allocation-free apart from torch's caching allocator, so it can be captured in a
+HIP graph.  The folded weights are taken from the model when the decoder is built; call
+refresh() after the model's parameters change.
 """
 
 import ctypes
@@ -21,12 +31,26 @@ from . import _abi
 from .hip_scan import METHODS
 
 
+STACK_LIMITS = dict(d_model=512, dim=1024, dstate=(8, 16), dt_rank=(8, 16, 32), width=4)
+
+
 class FastDecoder:
-    def __init__(self, model):
+    def __init__(self, model, path="auto"):
+        """path: "auto" (the stack path where the shape allows it), "stack" or "block"."""
         if next(model.parameters()).dtype != torch.float32:
             raise ValueError("the fused decode layer runs in float32")
+        if path not in ("auto", "stack", "block"):
+            raise ValueError(f"unknown decode path {path!r}")
         self.model = model
         self.refresh()
+        m0 = self.layers[0]["mixer"]
+        fits = (model.blocks[0].norm1.weight.numel() <= STACK_LIMITS["d_model"] and m0.d_inner <= STACK_LIMITS["dim"]
+                and m0.d_state in STACK_LIMITS["dstate"] and m0.dt_rank in STACK_LIMITS["dt_rank"]
+                and m0.d_conv <= STACK_LIMITS["width"])
+        if path == "stack" and not fits:
+            raise ValueError("the model's shape is past the stack decode kernels' limits")
+        self.path = "stack" if (path == "stack" or (path == "auto" and fits)) else "block"
+        self._ws = {}
 
     @torch.no_grad()
     def refresh(self):
@@ -46,6 +70,9 @@ class FastDecoder:
                 Dskip=m.D.contiguous(),
                 w_out_t=m.out_proj.weight.t(),
                 eps=blk.norm1.eps, mixer=m))
+            L = self.layers[-1]
+            L["w_in_tc"] = L["w_in"].t().contiguous()
+            L["w_out_tc"] = m.out_proj.weight.t().contiguous()
 
     def _layer(self, L, u, state):
         m = L["mixer"]
@@ -66,6 +93,35 @@ class FastDecoder:
         rc = _abi.lib().ssm_decode_step(ctypes.byref(a), _abi.stream_handle(u.device))
         _abi.check(rc, "ssm_decode_step")
         return u.addmm_(y, L["w_out_t"])     # residual in place: u is this step's own buffer
+
+    def _stack(self, u, states):
+        m = self.layers[0]["mixer"]
+        n = len(self.layers)
+        blocks = (_abi.DecodeBlock * n)()
+        for i, (L, st) in enumerate(zip(self.layers, states)):
+            k = blocks[i]
+            k.w_in_t, k.conv_w, k.conv_b = L["w_in_tc"].data_ptr(), L["conv_w"].data_ptr(), L["conv_b"].data_ptr()
+            k.x_proj_wt, k.dt_proj_w = L["x_proj_wt"].data_ptr(), L["dt_proj_w"].data_ptr()
+            k.dt_bias, k.A_log, k.Dskip = L["dt_bias"].data_ptr(), L["A_log"].data_ptr(), L["Dskip"].data_ptr()
+            k.w_out_t = L["w_out_tc"].data_ptr()
+            k.conv_state, k.ssm_state = st.conv.data_ptr(), st.ssm.data_ptr()
+            k.eps = L["eps"]
+        a = _abi.DecodeStackArgs()
+        a.batch, a.dim, a.dstate, a.width = u.shape[0], m.d_inner, m.d_state, m.d_conv
+        a.dt_rank, a.d_model = m.dt_rank, u.shape[1]
+        a.method = METHODS[m.discretization]
+        a.conv_state_dtype = _abi.DTYPE_CODE[states[0].conv.dtype]
+        a.n_blocks = n
+        a.blocks = blocks
+        a.u = u.data_ptr()
+        lib = _abi.lib()
+        need = lib.ssm_decode_stack_workspace_bytes(ctypes.byref(a))
+        key = (u.device, need)
+        if key not in self._ws:
+            self._ws[key] = torch.empty(need, dtype=torch.uint8, device=u.device)
+        a.workspace, a.workspace_bytes = self._ws[key].data_ptr(), need
+        _abi.check(lib.ssm_decode_stack(ctypes.byref(a), _abi.stream_handle(u.device)), "ssm_decode_stack")
+        return u
 
     @torch.no_grad()
     def step(self, tok, states):
@@ -88,8 +144,13 @@ class FastDecoder:
         try:
             with torch.autocast(device_type="cuda", enabled=False):
                 u = self.model.embed(tok.reshape(-1))      # a fresh buffer, updated in place
-                for L, s in zip(self.layers, states):
-                    u = self._layer(L, u, s)
+                if self.path == "stack":
+                    if len({s.conv.dtype for s in states}) != 1:
+                        raise ValueError("the stack path needs one conv state dtype for every block")
+                    u = self._stack(u, states)
+                else:
+                    for L, s in zip(self.layers, states):
+                        u = self._layer(L, u, s)
                 return self.model.head(self.model.norm_f(u))
         finally:
             torch.backends.cuda.preferred_blas_library(prev)

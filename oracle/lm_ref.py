@@ -39,7 +39,7 @@ def mamba_layer(p, pre, u, d_state, dt_rank, d_conv, state=None, method="zoh"):
         xc = F.pad(xc, (d_conv - 1, 0))
     else:
         xc = torch.cat([state["conv"], xc], dim=-1)
-        state["conv"] = xc[..., -(d_conv - 1):].clone()
+        state["conv"] = xc[..., xc.shape[-1] - (d_conv - 1):].clone()  # (B, D, 0) at width 1
     x = F.silu(F.conv1d(xc, p[pre + "conv.weight"], p[pre + "conv.bias"], groups=D)).transpose(1, 2)
     dt, Bm, Cm = F.linear(x, p[pre + "x_proj.weight"]).split([dt_rank, d_state, d_state], dim=-1)
     delta = F.softplus(F.linear(dt, p[pre + "dt_proj.weight"], p[pre + "dt_proj.bias"]))

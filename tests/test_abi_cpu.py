@@ -45,6 +45,7 @@ def test_library_exports_every_declared_function():
 def test_ctypes_layout_matches_c_header(tmp_path):
     structs = {"ssm_tensor": _abi.Tensor, "ssm_fwd_args": _abi.FwdArgs, "ssm_bwd_args": _abi.BwdArgs,
                "ssm_step_args": _abi.StepArgs, "ssm_decode_args": _abi.DecodeArgs, "ssm_lscan_args": _abi.LscanArgs,
+               "ssm_decode_block": _abi.DecodeBlock, "ssm_decode_stack_args": _abi.DecodeStackArgs,
                "ssm_lscan_bwd_args": _abi.LscanBwdArgs,
                "ssm_disc_args": _abi.DiscArgs, "ssm_conv_args": _abi.ConvArgs, "ssm_norm_args": _abi.NormArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
@@ -220,6 +221,59 @@ def test_decode_layer_validation(field, value):
     setattr(a, field, value)
     with pytest.raises(ValueError):
         _abi.check(_abi.lib().ssm_decode_check(ctypes.byref(a)), "ssm_decode_step")
+
+
+def _stack_args(n_blocks=2):
+    a = _abi.DecodeStackArgs()
+    a.batch, a.dim, a.dstate, a.width, a.dt_rank, a.d_model, a.method = 64, 512, 16, 4, 16, 256, 0
+    blocks = (_abi.DecodeBlock * n_blocks)()
+    for k in blocks:
+        for name, _ in _abi.DecodeBlock._fields_[:11]:
+            setattr(k, name, 16)   # non-null placeholders: the check never dereferences them
+        k.eps = 1e-5
+    a.n_blocks, a.blocks, a.u = n_blocks, blocks, 16
+    a.workspace = 16
+    a.workspace_bytes = _abi.lib().ssm_decode_stack_workspace_bytes(ctypes.byref(a))
+    a._keep = blocks
+    return a
+
+
+def test_decode_stack_workspace_layout():
+    """Workspace of the stack step: two residual-stream buffers, the out_proj partial sums over
+    64-channel tiles, the conv output and gate, the x_proj partial sums over 32-channel tiles,
+    each region rounded up to 256 bytes."""
+    a = _stack_args()
+    r = lambda v: -(-v // 256) * 256
+    B, dm, D, P = 64, 256, 512, 16 + 32
+    want = 2 * r(B * dm * 4) + r(B * (D // 64) * dm * 4) + 2 * r(B * D * 4) + r(B * (D // 32) * P * 4)
+    assert a.workspace_bytes == want
+    assert _abi.lib().ssm_decode_stack_check(ctypes.byref(a)) == 0
+
+
+@pytest.mark.parametrize("field,value", [("d_model", 513), ("dim", 1025), ("dstate", 12), ("dt_rank", 24),
+                                         ("width", 5), ("method", 3), ("batch", 0), ("n_blocks", 0),
+                                         ("conv_state_dtype", 2), ("workspace_bytes", 1024), ("workspace", None),
+                                         ("u", None), ("batch", 1 << 20)])
+def test_decode_stack_validation(field, value):
+    """ssm_decode_stack_check rejects shapes past the stack kernels' limits, a missing or short
+    workspace and offsets past 32 bits before any launch."""
+    a = _stack_args()
+    setattr(a, field, value)
+    with pytest.raises((ValueError, MemoryError)):
+        _abi.check(_abi.lib().ssm_decode_stack_check(ctypes.byref(a)), "ssm_decode_stack")
+
+
+@pytest.mark.parametrize("name", [f for f, _ in _abi.DecodeBlock._fields_[:11]])
+def test_decode_stack_block_tensors_required(name):
+    """Every block tensor is required, the conv state except at conv width 1 (an empty state)."""
+    a = _stack_args()
+    setattr(a.blocks[1], name, None)
+    with pytest.raises(ValueError):
+        _abi.check(_abi.lib().ssm_decode_stack_check(ctypes.byref(a)), "ssm_decode_stack")
+    if name == "conv_state":
+        a.width = 1
+        a.workspace_bytes = _abi.lib().ssm_decode_stack_workspace_bytes(ctypes.byref(a))
+        assert _abi.lib().ssm_decode_stack_check(ctypes.byref(a)) == 0
 
 
 def test_linear_scan_grid_limit():

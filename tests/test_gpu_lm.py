@@ -121,7 +121,7 @@ def test_fused_decode_layer_matches_module_decode(dev, shape):
     from ssm_scan.decode import FastDecoder
     torch.manual_seed(6)
     model = MambaLM(**shape).to(dev).eval()
-    fast = FastDecoder(model)
+    fast = FastDecoder(model, path="block")
     s_ref = _random_states(model, 64, dev, 7)
     s_fast = _clone(s_ref)
     toks = torch.randint(0, 256, (8, 64, 1), generator=torch.Generator().manual_seed(8)).to(dev)
@@ -136,12 +136,14 @@ def test_fused_decode_layer_matches_module_decode(dev, shape):
         np.testing.assert_allclose(np64(a.conv), np64(b_.conv), rtol=1e-5, atol=1e-6)
 
 
-def test_fused_decode_graph_replays_match_eager(dev):
+@pytest.mark.parametrize("path", ["stack", "block"])
+def test_fused_decode_graph_replays_match_eager(dev, path):
     """The token step captured in a HIP graph: every replay (with eager work between) equals the
-    eager step from the same states and token."""
+    eager step from the same states and token, bit for bit."""
     from ssm_scan.decode import FastDecoder
     model = build(9, n_layers=3).to(dev).eval()
-    fast = FastDecoder(model)
+    fast = FastDecoder(model, path=path)
+    assert fast.path == path
     states = _random_states(model, 16, dev, 10)
     tok = torch.zeros(16, 1, dtype=torch.long, device=dev)
     side = torch.cuda.Stream()
@@ -287,22 +289,27 @@ ORACLE_DECODE_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("shape", ORACLE_DECODE_SHAPES, ids=lambda s: "-".join(f"{k}{v}" for k, v in s.items()))
-def test_fast_decoder_matches_float64_reference(dev, shape):
-    """FastDecoder.step (in_proj GEMM, the fused decode launch, out_proj + residual GEMM per layer)
-    against the float64 restatement of the reference's recurrent decode (models/mamba.py:104-125,
-    lm_ref.lm_forward with states), batch 64, 8 tokens from random conv and ssm states: logits
-    after every token, then every layer's ssm and conv state.
+# the stack kernels' shapes: the LM preset; dstate 8 bilinear over a ragged batch; dim 240 and
+# 500 (ragged channel tiles), d_model 250 (not a multiple of 4), width 1 and 2; d_model 512
+# (two passes over d_model, dt_rank 32, dim 1024); a single block (the last-block sums in place)
+STACK_DECODE_SHAPES = [
+    (dict(n_layers=10), 64),
+    (dict(n_layers=3, d_state=8, discretization="bilinear"), 37),
+    (dict(n_layers=2, d_model=120, d_conv=1, discretization="euler"), 5),
+    (dict(n_layers=2, d_model=250, d_conv=2), 19),
+    (dict(n_layers=2, d_model=512), 64),
+    (dict(n_layers=1, d_model=128, d_state=8), 9),
+]
 
-    Tolerances: states at the float32 bar (rtol 1e-4 / atol 1e-5); logits rtol 1e-4 with atol
-    1e-5 x max|logit| (logits are float32 GEMMs over d_model terms of the final hidden state)."""
+
+def _decoder_vs_oracle(dev, shape, B, path, T=8):
     from ssm_scan.decode import FastDecoder
     from parity import close
     torch.manual_seed(11)
     model = MambaLM(**shape).to(dev).eval()
     m = model.blocks[0].mixer
-    fast = FastDecoder(model)
-    B, T = 64, 8
+    fast = FastDecoder(model, path=path)
+    assert fast.path == path
     states = _random_states(model, B, dev, 12)
     rstates = [{"conv": s.conv.cpu().double().clone(), "ssm": s.ssm.cpu().double().clone()} for s in states]
     p = {k: v.detach().cpu().double() for k, v in model.state_dict().items()}
@@ -316,6 +323,36 @@ def test_fast_decoder_matches_float64_reference(dev, shape):
     for i, (s, r) in enumerate(zip(states, rstates)):
         close(s.ssm, r["ssm"], name=f"layer {i} ssm state")
         close(s.conv, r["conv"], name=f"layer {i} conv state")
+
+
+@pytest.mark.parametrize("shape", ORACLE_DECODE_SHAPES, ids=lambda s: "-".join(f"{k}{v}" for k, v in s.items()))
+def test_fast_decoder_matches_float64_reference(dev, shape):
+    """FastDecoder.step's per-block path (in_proj GEMM, the fused decode launch, out_proj +
+    residual GEMM per block) against the float64 restatement of the reference's recurrent decode
+    (models/mamba.py:104-125, lm_ref.lm_forward with states), batch 64, 8 tokens from random conv
+    and ssm states: logits after every token, then every layer's ssm and conv state.
+
+    Tolerances: states at the float32 bar (rtol 1e-4 / atol 1e-5); logits rtol 1e-4 with atol
+    1e-5 x max|logit| (logits are float32 GEMMs over d_model terms of the final hidden state)."""
+    _decoder_vs_oracle(dev, shape, 64, "block")
+
+
+@pytest.mark.parametrize("shape,batch", STACK_DECODE_SHAPES,
+                         ids=lambda v: "-".join(f"{k}{x}" for k, x in v.items()) if isinstance(v, dict) else f"B{v}")
+def test_decode_stack_matches_float64_reference(dev, shape, batch):
+    """FastDecoder.step's stack path (ssm_decode_stack: two launches per block with the GEMMs
+    inside) against the same float64 restatement and at the same bar as the per-block path."""
+    _decoder_vs_oracle(dev, shape, batch, "stack")
+
+
+def test_decode_stack_limits_fall_back_to_blocks(dev):
+    """Shapes past the stack kernels' limits take the per-block path; asking for the stack path
+    with them is an error."""
+    from ssm_scan.decode import FastDecoder
+    model = MambaLM(n_layers=1, d_state=12).to(dev).eval()
+    assert FastDecoder(model).path == "block"
+    with pytest.raises(ValueError):
+        FastDecoder(model, path="stack")
 
 
 # the row-resident kernel (LM preset) and the general one (dstate 12, width 5)

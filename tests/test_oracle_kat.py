@@ -379,13 +379,15 @@ def test_discretize_vjp_matches_torch_autograd(method, tiny):
 
 # --------------------------------------------------------------------------- LM restatement
 
-def test_lm_ref_layer_composes_pinned_oracle_pieces():
+@pytest.mark.parametrize("W", [4, 2, 1])
+def test_lm_ref_layer_composes_pinned_oracle_pieces(W):
     """oracle/lm_ref.mamba_layer equals in_proj -> conv1d_causal -> selective_scan_fwd (D skip,
     SiLU gate) -> out_proj built from the pinned numpy oracle; its decode path (state carried
-    one token at a time) equals its full-sequence path."""
+    one token at a time) equals its full-sequence path, also at conv width 1 (an empty conv
+    state that stays empty)."""
     from oracle import lm_ref
     g = torch.Generator().manual_seed(0)
-    dm, D, N, R_, W = 8, 16, 4, 2, 4
+    dm, D, N, R_ = 8, 16, 4, 2
     p = {"m.in_proj.weight": torch.randn(2 * D, dm, generator=g, dtype=torch.float64) * 0.3,
          "m.conv.weight": torch.randn(D, 1, W, generator=g, dtype=torch.float64) * 0.5,
          "m.conv.bias": torch.randn(D, generator=g, dtype=torch.float64) * 0.1,
@@ -412,6 +414,7 @@ def test_lm_ref_layer_composes_pinned_oracle_pieces():
     state = {"conv": torch.zeros(2, D, W - 1, dtype=torch.float64), "ssm": torch.zeros(2, D, N, dtype=torch.float64)}
     steps = torch.cat([lm_ref.mamba_layer(p, "m.", u[:, t:t + 1], N, R_, W, state=state) for t in range(11)], 1)
     np.testing.assert_allclose(steps.numpy(), out.numpy(), rtol=1e-11, atol=1e-12)
+    assert state["conv"].shape == (2, D, W - 1)
 
 
 @pytest.mark.parametrize("shape,eps", [((3, 7, 256), 1e-5), ((2, 5, 1000), 1e-6), ((4, 1), 1e-5), ((6, 64), 1e-3)])
