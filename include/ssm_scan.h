@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 6
+#define SSM_ABI_VERSION 7
 
 enum { SSM_OK = 0, SSM_EINVAL = 1, SSM_EKEY = 2, SSM_ESPACE = 3, SSM_EHIP = 4 };
 
@@ -196,7 +196,11 @@ typedef struct ssm_decode_args {
  * L = 1), in two launches per block plus one at the end.  Unlike ssm_decode_step, the in_proj
  * and out_proj GEMMs are part of the step, tiled with the rest of the block over the whole GPU.
  * u (B, d_model) holds the residual stream entering the first block and is replaced by the one
- * leaving the last (the input of the final norm and head).  Every block has the same
+ * leaving the last (the input of the final norm and head).  Optionally the call also covers the
+ * token step's ends (models/lm.py:125,128): with `tokens`, the residual stream entering the
+ * first block is the tokens' embedding rows (u is then output only; an id outside
+ * [0, vocab) reads a zero row, where the reference's embedding raises); with `head_w_t`, the
+ * logits of the final RMSNorm and the head are written.  Every block has the same
  * dimensions; tensors are float32 and row-major (conv states float32 or bf16), states are
  * updated in place, and every sum runs in a fixed order (the step is deterministic).
  * Supported: d_model <= 512, dim <= 1024, dstate 8 or 16, dt_rank 8, 16 or 32, width <= 4;
@@ -228,6 +232,13 @@ typedef struct ssm_decode_stack_args {
   float *u;                /* (B, d_model) residual stream, replaced in place */
   void *workspace;         /* device memory of ssm_decode_stack_workspace_bytes() */
   int64_t workspace_bytes;
+  const int64_t *tokens;   /* (B,) token ids on the device, or NULL */
+  const float *embed;      /* (vocab, d_model) embedding table, read when tokens is set */
+  const float *head_w_t;   /* (d_model, vocab): (W_head diag(norm_f_w))^T, or NULL (no head) */
+  float *logits;           /* (B, vocab), written when head_w_t is set */
+  int64_t vocab;
+  float head_eps;          /* the final RMSNorm's epsilon */
+  int32_t reserved1;
 } ssm_decode_stack_args;
 
 /* ------------------------------------------------------------------ linear scans

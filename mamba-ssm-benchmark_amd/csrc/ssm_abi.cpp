@@ -757,6 +757,13 @@ int ssm_decode_stack_check(const ssm_decode_stack_args *a) {
         !k.Dskip || !k.w_out_t || (!k.conv_state && a->width > 1) || !k.ssm_state)
       return fail(SSM_EINVAL, "block %d: a required tensor is missing", i);
   }
+  if (a->tokens || a->head_w_t) {
+    if (a->vocab < 1) return fail(SSM_EINVAL, "vocab %lld: the embedding or head needs a vocabulary", (long long)a->vocab);
+    if ((a->batch + kInRows) * a->vocab * 4 >= (1LL << 31) || a->vocab * a->d_model * 4 >= (1LL << 31))
+      return fail(SSM_EINVAL, "vocabulary too large for 32-bit offsets (vocab %lld)", (long long)a->vocab);
+  }
+  if (a->tokens && !a->embed) return fail(SSM_EINVAL, "tokens given without the embedding table");
+  if (a->head_w_t && !a->logits) return fail(SSM_EINVAL, "head weight given without a logits buffer");
   if (!a->workspace || a->workspace_bytes < l.total)
     return fail(SSM_ESPACE, "decode stack workspace %lld bytes < %lld", (long long)a->workspace_bytes,
                 (long long)l.total);
@@ -777,9 +784,10 @@ int ssm_decode_stack(const ssm_decode_stack_args *a, void *stream) {
   float *ua = (float *)(ws + l.off_ua), *ub = (float *)(ws + l.off_ub), *du = (float *)(ws + l.off_du);
   float *xc = (float *)(ws + l.off_xc), *gate = (float *)(ws + l.off_gate), *part = (float *)(ws + l.off_part);
   const int B = (int)a->batch, dm = (int)a->d_model, Dm = (int)a->dim;
-  // the residual stream entering block i lives in dst(i) (block 0: u itself); k_dec_in of
-  // block i rebuilds it from dst(i - 1) and block i - 1's partial sums
-  auto dst = [&](int i) { return i == 0 ? a->u : (i % 2 ? ua : ub); };
+  // k_dec_in of block i rebuilds the residual stream entering it (block 0: u or the embedding
+  // rows; block i > 0: dst(i - 1) + block i - 1's partial sums) and stores it in dst(i), a
+  // workspace buffer: no launch reads rows that another of its workgroups writes
+  auto dst = [&](int i) { return i % 2 ? ub : ua; };
   for (int i = 0; i < a->n_blocks; ++i) {
     const ssm_decode_block &k = a->blocks[i];
     DecInParams pi;
@@ -787,12 +795,15 @@ int ssm_decode_stack(const ssm_decode_stack_args *a, void *stream) {
     pi.B = B; pi.dm = dm; pi.Dm = Dm; pi.P = (int)l.P;
     pi.nrt = (int)cdiv(B, kInRows); pi.nct = (int)l.nct;
     pi.ndu = i == 0 ? 0 : (int)l.ndu;
-    pi.write_u = i > 0;
+    pi.write_u = 1;
     pi.conv_bf16 = a->conv_state_dtype == SSM_BF16;
     pi.eps = k.eps;
+    pi.V = (int)a->vocab;
+    pi.tokens = i == 0 ? a->tokens : nullptr;
+    pi.embed = a->embed;
     pi.u_src = i == 0 ? a->u : dst(i - 1);
     pi.du = i == 0 ? nullptr : du;
-    pi.u_dst = i == 0 ? nullptr : dst(i);
+    pi.u_dst = dst(i);
     pi.w_in_t = k.w_in_t; pi.conv_w = k.conv_w; pi.conv_b = k.conv_b; pi.x_proj_wt = k.x_proj_wt;
     pi.conv_state = k.conv_state;
     pi.xc = xc; pi.gate = gate; pi.part = part;
@@ -808,10 +819,22 @@ int ssm_decode_stack(const ssm_decode_stack_args *a, void *stream) {
     e = launch_dec_scan(ps, a->method, s);
     if (e != hipSuccess) return hip_fail(e, "ssm_decode_stack scan-stage launch");
   }
-  DecOutParams po;
-  po.B = B; po.dm = dm; po.ndu = (int)l.ndu;
-  po.u_src = dst(a->n_blocks - 1); po.du = du; po.u_out = a->u;
-  hipError_t e = launch_dec_out(po, s);
+  hipError_t e;
+  if (a->head_w_t) {  // the last block's sums, the final norm and the head in one launch
+    DecInParams ph;
+    memset(&ph, 0, sizeof(ph));
+    ph.B = B; ph.dm = dm; ph.Dm = 1; ph.P = 1; ph.V = (int)a->vocab;
+    ph.nrt = (int)cdiv(B, kInRows); ph.nct = (int)cdiv(a->vocab, 64); ph.ndu = (int)l.ndu;
+    ph.write_u = 1; ph.eps = a->head_eps;
+    ph.u_src = dst(a->n_blocks - 1); ph.du = du; ph.u_dst = a->u;
+    ph.head_w_t = a->head_w_t; ph.logits = a->logits;
+    e = launch_dec_head(ph, s);
+  } else {
+    DecOutParams po;
+    po.B = B; po.dm = dm; po.ndu = (int)l.ndu;
+    po.u_src = dst(a->n_blocks - 1); po.du = du; po.u_out = a->u;
+    e = launch_dec_out(po, s);
+  }
   return e == hipSuccess ? ok() : hip_fail(e, "ssm_decode_stack output launch");
 }
 

@@ -12,7 +12,11 @@
 //               bias + softplus, the state update, C h, D skip and gate, and the out_proj
 //               partial sums over the tile's channels.
 //
-// k_dec_out adds the last layer's partial sums to its residual stream.  Every reduction runs
+// The token step's ends fold into the same kernels: block 0's k_dec_in may read the embedding
+// rows of the tokens as its residual stream (models/lm.py:125), and k_dec_head -- k_dec_in's
+// rebuild, RMSNorm scale and GEMM over vocabulary columns -- gives the logits of the final
+// norm and the head (models/lm.py:128); without a head, k_dec_out adds the last layer's partial
+// sums to its residual stream.  Every reduction runs
 // in a fixed order, so the step is deterministic.  A workgroup issues its global reads
 // (weights, states, partial sums) at entry, so each launch costs one memory round trip; the
 // workgroups that share a weight tile run on one XCD (blockIdx mod 8), so the tile is read
@@ -52,8 +56,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 // KQ passes of 256 over d_model; NDU >= the previous block's partial sums per row (0: none).
 // Roles: rebuild = element k = tid + 256 q of each of the 4 rows; RMSNorm and epilogue = row wv,
 // column lane (x channel c0 + lane for lane < 32, else z channel c0 + lane - 32); in_proj =
-// wavefront's quarter of k, lane's column; x_proj = row wv, output lane.
-template <int W, int KQ, int NDU>
+// wavefront's quarter of k, lane's column; x_proj = row wv, output lane.  HEAD: the columns
+// are the 64 vocabulary entries of tile ct and the epilogue stores the logits.
+template <int W, int KQ, int NDU, bool HEAD>
 __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
   constexpr int NWV = kStThreads / kWave;
   constexpr int KP = KQ * NWV * kInKB;        // padded d_model
@@ -69,19 +74,26 @@ __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
   const int b0 = rt * kInRows, c0 = ct * kInCh;
   const int B = p.B, dm = p.dm, Dm = p.Dm, P = p.P, ndu = p.ndu;
 
-  // every global read first, in the order of first use
-  const auto ru = flat_buffer(p.u_src, (int64_t)B * dm * 4);
+  // every global read first, in the order of first use: the residual stream (or the token's
+  // embedding row: an id outside the vocabulary reads a zero row) and the partial sums
+  const bool emb = p.tokens != nullptr;
+  const auto ru = emb ? flat_buffer(p.embed, (int64_t)p.V * dm * 4) : flat_buffer(p.u_src, (int64_t)B * dm * 4);
   const auto rdu = flat_buffer(p.du, (int64_t)B * ndu * dm * 4);
   float uv[kInRows][KQ], dv[kInRows][KQ][NDU > 0 ? NDU : 1];
 #pragma unroll
-  for (int r = 0; r < kInRows; ++r)
+  for (int r = 0; r < kInRows; ++r) {
+    const int b = b0 + r;  // rows past the batch read 0
+    int64_t row = b;
+    if (emb) row = b < B ? p.tokens[b] : -1;
+    const bool rok = row >= 0 && row < (emb ? p.V : B);
 #pragma unroll
     for (int q = 0; q < KQ; ++q) {
-      const int b = b0 + r, k = tid + q * kStThreads;  // rows past the batch read 0
-      uv[r][q] = ldf(ru, b * dm + k);
+      const int k = tid + q * kStThreads;
+      uv[r][q] = buf_load<float>(ru, rok ? (uint32_t)(row * dm + k) * 4u : kDropOffset);
 #pragma unroll
       for (int t = 0; t < NDU; ++t) dv[r][q][t] = t < ndu ? ldf(rdu, (b * ndu + t) * dm + k) : 0.f;
     }
+  }
 
   const int r = wv, j = lane, d = c0 + (j & (kInCh - 1)), b = b0 + r;
   const bool ok = b < B && d < Dm;
@@ -92,25 +104,26 @@ __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
   const int cst = (bc * Dm + dc) * (W - 1);
   float cw[W], st[W > 1 ? W - 1 : 1];
 #pragma unroll
-  for (int i = 0; i < W; ++i) cw[i] = ldf(rcw, dc * W + i);
+  for (int i = 0; i < W; ++i) cw[i] = HEAD ? 0.f : ldf(rcw, dc * W + i);
 #pragma unroll
   for (int i = 0; i < W - 1; ++i)
     st[i] = p.conv_bf16 ? buf_load<bf16_t>(rcs, (uint32_t)(cst + i) * 2u) : ldf(rcs, cst + i);
-  const float cb = ldf(rcb, dc);
+  const float cb = HEAD ? 0.f : ldf(rcb, dc);
   const auto rxp = flat_buffer(p.x_proj_wt, (int64_t)Dm * P * 4);
   float xpv[XPN];
 #pragma unroll
-  for (int i = 0; i < XPN; ++i) xpv[i] = ldf(rxp, c0 * P + tid + i * kStThreads);  // 0 past dim
+  for (int i = 0; i < XPN; ++i) xpv[i] = HEAD ? 0.f : ldf(rxp, c0 * P + tid + i * kStThreads);  // 0 past dim
 
-  // in_proj weight columns of this lane (a channel past dim reads a valid column whose results
-  // are never used), k split over the wavefronts
-  const auto rw = flat_buffer(p.w_in_t, (int64_t)dm * 2 * Dm * 4);
-  const int col = (lane < kInCh ? 0 : Dm) + min(c0 + (lane & (kInCh - 1)), Dm - 1);
+  // GEMM weight columns of this lane (a channel or vocabulary entry past the end reads a valid
+  // column whose results are never used), k split over the wavefronts
+  const int ncol = HEAD ? p.V : 2 * Dm;
+  const auto rw = flat_buffer(HEAD ? p.head_w_t : p.w_in_t, (int64_t)dm * ncol * 4);
+  const int col = HEAD ? min(ct * kWave + lane, p.V - 1) : (lane < kInCh ? 0 : Dm) + min(c0 + (lane & (kInCh - 1)), Dm - 1);
   float wr[KQ][kInKB];
 #pragma unroll
   for (int q = 0; q < KQ; ++q)
 #pragma unroll
-    for (int i = 0; i < kInKB; ++i) wr[q][i] = ldf(rw, ((q * NWV + wv) * kInKB + i) * 2 * Dm + col);  // 0 past d_model
+    for (int i = 0; i < kInKB; ++i) wr[q][i] = ldf(rw, ((q * NWV + wv) * kInKB + i) * ncol + col);  // 0 past d_model
 
   // residual stream of the 4 rows: u + the previous block's partial sums in order
 #pragma unroll
@@ -164,6 +177,11 @@ __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
   for (int rr = 0; rr < kInRows; ++rr) gsum[wv][rr][lane] = acc[rr];
   __syncthreads();
   const float v = s * (((gsum[0][r][j] + gsum[1][r][j]) + gsum[2][r][j]) + gsum[3][r][j]);
+  if constexpr (HEAD) {
+    const int vc = ct * kWave + lane;
+    stf(flat_buffer(p.logits, (int64_t)B * p.V * 4), b * p.V + vc, b < B && vc < p.V, v);
+    return;
+  }
 
   // conv step + SiLU (models/mamba.py:104-107) for x columns, the gate SiLU(z) for z columns
   const int io = b * Dm + d;
@@ -316,11 +334,20 @@ __global__ void __launch_bounds__(kStThreads) k_dec_out(const DecOutParams p) {
   p.u_out[i] = v;
 }
 
-template <int W, int KQ>
+template <int W, int KQ, bool HEAD = false>
 static void launch_in_q(const DecInParams &p, dim3 grid, hipStream_t s) {
-  if (p.ndu == 0) hipLaunchKernelGGL((k_dec_in<W, KQ, 0>), grid, dim3(kStThreads), 0, s, p);
-  else if (p.ndu <= kStMaxScTiles / 2) hipLaunchKernelGGL((k_dec_in<W, KQ, kStMaxScTiles / 2>), grid, dim3(kStThreads), 0, s, p);
-  else hipLaunchKernelGGL((k_dec_in<W, KQ, kStMaxScTiles>), grid, dim3(kStThreads), 0, s, p);
+  if (p.ndu == 0) hipLaunchKernelGGL((k_dec_in<W, KQ, 0, HEAD>), grid, dim3(kStThreads), 0, s, p);
+  else if (p.ndu <= kStMaxScTiles / 2)
+    hipLaunchKernelGGL((k_dec_in<W, KQ, kStMaxScTiles / 2, HEAD>), grid, dim3(kStThreads), 0, s, p);
+  else hipLaunchKernelGGL((k_dec_in<W, KQ, kStMaxScTiles, HEAD>), grid, dim3(kStThreads), 0, s, p);
+}
+
+// The final norm and the head: k_dec_in's rebuild, norm scale and GEMM over vocabulary tiles.
+hipError_t launch_dec_head(const DecInParams &p, hipStream_t s) {
+  const dim3 grid((unsigned)(p.nrt * p.nct));
+  if (p.dm > kStThreads) launch_in_q<1, 2, true>(p, grid, s);
+  else launch_in_q<1, 1, true>(p, grid, s);
+  return hipGetLastError();
 }
 
 template <int W>

@@ -216,7 +216,12 @@ constexpr int kStMaxInTiles = kStMaxDim / kInCh;   // x_proj partial sums per ro
 constexpr int kStMaxScTiles = kStMaxDim / kScCh;   // out_proj partial sums per row
 struct DecInParams {
   int B, dm, Dm, P, nrt, nct, ndu, write_u, conv_bf16;
+  int V;                  // vocabulary (embedding rows; head columns)
   float eps;
+  const int64_t *tokens;  // (B,) or null: the residual stream is the embedding rows of the tokens
+  const float *embed;     // (V, dm)
+  const float *head_w_t;  // (dm, V) head weight (the final norm's weight folded in)
+  float *logits;          // (B, V)
   const float *u_src;     // (B, dm) residual stream of the previous layer
   const float *du;        // (B, ndu, dm) its out_proj partial sums (ndu = 0: none)
   float *u_dst;           // (B, dm) the residual stream entering this layer (write_u)
@@ -238,6 +243,7 @@ struct DecOutParams {
 hipError_t launch_dec_in(const DecInParams &p, int W, hipStream_t s);
 hipError_t launch_dec_scan(const DecScanParams &p, int method, hipStream_t s);
 hipError_t launch_dec_out(const DecOutParams &p, hipStream_t s);
+hipError_t launch_dec_head(const DecInParams &p, hipStream_t s);
 
 // Runs the summary and carry passes first when p.nseg > 1.
 hipError_t launch_fwd(const FwdParams &p, int dtype, int method, int np, hipStream_t s);

@@ -11,7 +11,7 @@ import os
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssmscan.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK, EINVAL, EKEY, ESPACE, EHIP = 0, 1, 2, 3, 4
 ZOH, EULER, BILINEAR = 0, 1, 2
@@ -84,7 +84,9 @@ class DecodeStackArgs(ctypes.Structure):
                 ("d_model", c_i64), ("method", c_i32), ("conv_state_dtype", c_i32),
                 ("n_blocks", c_i32), ("reserved0", c_i32),
                 ("blocks", ctypes.POINTER(DecodeBlock)), ("u", c_vp),
-                ("workspace", c_vp), ("workspace_bytes", c_i64)]
+                ("workspace", c_vp), ("workspace_bytes", c_i64),
+                ("tokens", c_vp), ("embed", c_vp), ("head_w_t", c_vp), ("logits", c_vp), ("vocab", c_i64),
+                ("head_eps", ctypes.c_float), ("reserved1", c_i32)]
 
 class LscanArgs(ctypes.Structure):
     _fields_ = [("batch", c_i64), ("seqlen", c_i64), ("width", c_i64),

@@ -1,16 +1,17 @@
 """Fast recurrent decode of a Mamba LM.
 
-The token step of the block stack runs as one C-ABI call (ssm_decode_stack): per block two
-launches spread over the whole GPU,
+The whole token step runs as one C-ABI call (ssm_decode_stack): per block two launches spread
+over the whole GPU (block 0's first reads the tokens' embedding rows),
     in-stage      the residual stream rebuilt from the previous block's out_proj partial sums,
                   the RMSNorm scale, the in_proj GEMM tile (the norm weight folded into its
                   columns), conv step + SiLU with the conv state, the SiLU(z) gate, x_proj
                   partial sums
     scan-stage    x_proj sums finished, dt_proj + softplus, the state update, D skip and gate,
                   out_proj partial sums
-and one launch at the end for the last block's sums; which computes what models/mamba.py:93-124
-(L = 1 with a state) and the pre-norm residual blocks of models/lm.py:82-83,124-128 compute,
-in place of ~20 small launches per block.  Shapes past the stack kernels' limits (d_model > 512,
+and one launch at the end for the last block's sums, the final RMSNorm and the head (its weight
+with the norm's folded in); which computes what models/lm.py:124-128 computes at L = 1 with
+states (the blocks :82-83, the mixer models/mamba.py:93-124), in place of ~20 small launches
+per block.  Shapes past the stack kernels' limits (d_model > 512,
 dim > 1024, dstate not 8 or 16, dt_rank not 8, 16 or 32, conv width > 4) take the per-block
 path: three launches per block,
     xz = u @ (W_in diag(norm_w))^T          one GEMM (the block's RMSNorm weight folded in)
@@ -73,6 +74,8 @@ class FastDecoder:
             L = self.layers[-1]
             L["w_in_tc"] = L["w_in"].t().contiguous()
             L["w_out_tc"] = m.out_proj.weight.t().contiguous()
+        # the head with the final RMSNorm weight folded into its columns, (d_model, vocab)
+        self.head_w_t = (self.model.head.weight * self.model.norm_f.weight[None, :]).t().contiguous()
 
     def _layer(self, L, u, state):
         m = L["mixer"]
@@ -94,8 +97,14 @@ class FastDecoder:
         _abi.check(rc, "ssm_decode_step")
         return u.addmm_(y, L["w_out_t"])     # residual in place: u is this step's own buffer
 
-    def _stack(self, u, states):
+    def _stack(self, tok, states):
+        """The whole token step in one call: embedding rows, every block, the final norm and
+        the head; returns the logits."""
         m = self.layers[0]["mixer"]
+        B, dm = tok.numel(), self.head_w_t.shape[0]
+        tok = tok.reshape(-1).to(torch.long)
+        u = torch.empty(B, dm, dtype=torch.float32, device=tok.device)
+        logits = torch.empty(B, self.head_w_t.shape[1], dtype=torch.float32, device=tok.device)
         n = len(self.layers)
         blocks = (_abi.DecodeBlock * n)()
         for i, (L, st) in enumerate(zip(self.layers, states)):
@@ -114,6 +123,9 @@ class FastDecoder:
         a.n_blocks = n
         a.blocks = blocks
         a.u = u.data_ptr()
+        a.tokens, a.embed = tok.data_ptr(), self.model.embed.weight.data_ptr()
+        a.head_w_t, a.logits, a.vocab = self.head_w_t.data_ptr(), logits.data_ptr(), logits.shape[1]
+        a.head_eps = self.model.norm_f.eps
         lib = _abi.lib()
         need = lib.ssm_decode_stack_workspace_bytes(ctypes.byref(a))
         key = (u.device, need)
@@ -121,7 +133,7 @@ class FastDecoder:
             self._ws[key] = torch.empty(need, dtype=torch.uint8, device=u.device)
         a.workspace, a.workspace_bytes = self._ws[key].data_ptr(), need
         _abi.check(lib.ssm_decode_stack(ctypes.byref(a), _abi.stream_handle(u.device)), "ssm_decode_stack")
-        return u
+        return logits
 
     @torch.no_grad()
     def step(self, tok, states):
@@ -143,14 +155,13 @@ class FastDecoder:
         torch.backends.cuda.preferred_blas_library("cublas")   # rocBLAS on ROCm
         try:
             with torch.autocast(device_type="cuda", enabled=False):
-                u = self.model.embed(tok.reshape(-1))      # a fresh buffer, updated in place
                 if self.path == "stack":
                     if len({s.conv.dtype for s in states}) != 1:
                         raise ValueError("the stack path needs one conv state dtype for every block")
-                    u = self._stack(u, states)
-                else:
-                    for L, s in zip(self.layers, states):
-                        u = self._layer(L, u, s)
+                    return self._stack(tok, states)
+                u = self.model.embed(tok.reshape(-1))      # a fresh buffer, updated in place
+                for L, s in zip(self.layers, states):
+                    u = self._layer(L, u, s)
                 return self.model.head(self.model.norm_f(u))
         finally:
             torch.backends.cuda.preferred_blas_library(prev)

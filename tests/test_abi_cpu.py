@@ -263,6 +263,25 @@ def test_decode_stack_validation(field, value):
         _abi.check(_abi.lib().ssm_decode_stack_check(ctypes.byref(a)), "ssm_decode_stack")
 
 
+@pytest.mark.parametrize("change", ["tokens_without_embed", "head_without_logits", "no_vocab", "huge_vocab"])
+def test_decode_stack_ends_validation(change):
+    """The optional ends of the token step: tokens need the embedding table, a head needs a
+    logits buffer, and either needs a vocabulary whose offsets fit 32 bits."""
+    a = _stack_args()
+    a.tokens, a.embed, a.head_w_t, a.logits, a.vocab = 16, 16, 16, 16, 256
+    assert _abi.lib().ssm_decode_stack_check(ctypes.byref(a)) == 0
+    if change == "tokens_without_embed":
+        a.embed = None
+    elif change == "head_without_logits":
+        a.logits = None
+    elif change == "no_vocab":
+        a.vocab = 0
+    else:
+        a.vocab = 1 << 22
+    with pytest.raises(ValueError):
+        _abi.check(_abi.lib().ssm_decode_stack_check(ctypes.byref(a)), "ssm_decode_stack")
+
+
 @pytest.mark.parametrize("name", [f for f, _ in _abi.DecodeBlock._fields_[:11]])
 def test_decode_stack_block_tensors_required(name):
     """Every block tensor is required, the conv state except at conv width 1 (an empty state)."""

@@ -345,6 +345,29 @@ def test_decode_stack_matches_float64_reference(dev, shape, batch):
     _decoder_vs_oracle(dev, shape, batch, "stack")
 
 
+def test_decode_stack_token_outside_vocabulary_reads_zero_row(dev):
+    """A token id outside [0, vocab) reads a zero embedding row in the stack path (the reference's
+    embedding raises instead): the step equals the step of a model whose row 7 is zero, given
+    token 7 there: states, and the logits of every other vocabulary entry (the head is tied to the
+    embedding)."""
+    from ssm_scan.decode import FastDecoder
+    torch.manual_seed(31)
+    model = MambaLM(n_layers=2).to(dev).eval()
+    zeroed = MambaLM(n_layers=2).to(dev).eval()
+    zeroed.load_state_dict(model.state_dict())
+    with torch.no_grad():
+        zeroed.embed.weight[7].zero_()
+    s1 = _random_states(model, 6, dev, 32)
+    s2 = _clone(s1)
+    tok = torch.tensor([3, 300, -1, 5, 255, 1 << 40], device=dev)
+    got = FastDecoder(model, path="stack").step(tok, s1)
+    ref = FastDecoder(zeroed, path="stack").step(torch.tensor([3, 7, 7, 5, 255, 7], device=dev), s2)
+    keep = torch.arange(got.shape[1], device=dev) != 7
+    assert torch.equal(got[:, keep], ref[:, keep])
+    for a, b_ in zip(s1, s2):
+        assert torch.equal(a.ssm, b_.ssm) and torch.equal(a.conv, b_.conv)
+
+
 def test_decode_stack_limits_fall_back_to_blocks(dev):
     """Shapes past the stack kernels' limits take the per-block path; asking for the stack path
     with them is an error."""
