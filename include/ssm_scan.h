@@ -203,7 +203,8 @@ typedef struct ssm_decode_args {
  * logits of the final RMSNorm and the head are written.  Every block has the same
  * dimensions; tensors are float32 and row-major (conv states float32 or bf16), states are
  * updated in place, and every sum runs in a fixed order (the step is deterministic).
- * Supported: d_model <= 512, dim <= 1024, dstate 8 or 16, dt_rank 8, 16 or 32, width <= 4;
+ * Supported: d_model <= 512 and a multiple of 4, dim <= 1024, dstate 8 or 16, dt_rank 8, 16 or
+ * 32, width <= 4; u, embed, ssm_state, A_log and dt_proj_w 16-byte aligned;
  * ssm_decode_stack_check names the limit a shape breaks. */
 typedef struct ssm_decode_block {
   const float *w_in_t;     /* (d_model, 2*dim): (W_in diag(norm_w))^T, the RMSNorm weight folded in */

@@ -745,6 +745,7 @@ int ssm_decode_stack_check(const ssm_decode_stack_args *a) {
   if (a->dt_rank != 8 && a->dt_rank != 16 && a->dt_rank != 32)
     return fail(SSM_EINVAL, "dt_rank %lld not 8, 16 or 32", (long long)a->dt_rank);
   if (a->width > 4) return fail(SSM_EINVAL, "conv width %lld > 4", (long long)a->width);
+  if (a->d_model % 4) return fail(SSM_EINVAL, "d_model %lld not a multiple of 4", (long long)a->d_model);
   // every buffer element is addressed by a 32-bit byte offset (with a few rows of slack)
   const StackLayout l = stack_layout(a);
   const int64_t rows = a->batch + kInRows;
@@ -756,7 +757,10 @@ int ssm_decode_stack_check(const ssm_decode_stack_args *a) {
     if (!k.w_in_t || !k.conv_w || !k.conv_b || !k.x_proj_wt || !k.dt_proj_w || !k.dt_bias || !k.A_log ||
         !k.Dskip || !k.w_out_t || (!k.conv_state && a->width > 1) || !k.ssm_state)
       return fail(SSM_EINVAL, "block %d: a required tensor is missing", i);
+    if (((uintptr_t)k.ssm_state | (uintptr_t)k.A_log | (uintptr_t)k.dt_proj_w) % 16)
+      return fail(SSM_EINVAL, "block %d: ssm_state, A_log and dt_proj_w must be 16-byte aligned", i);
   }
+  if (((uintptr_t)a->u | (uintptr_t)a->embed) % 16) return fail(SSM_EINVAL, "u and embed must be 16-byte aligned");
   if (a->tokens || a->head_w_t) {
     if (a->vocab < 1) return fail(SSM_EINVAL, "vocab %lld: the embedding or head needs a vocabulary", (long long)a->vocab);
     if ((a->batch + kInRows) * a->vocab * 4 >= (1LL << 31) || a->vocab * a->d_model * 4 >= (1LL << 31))

@@ -41,6 +41,17 @@ __device__ __forceinline__ float ldf(__amdgpu_buffer_rsrc_t r, int idx) { return
 __device__ __forceinline__ void stf(__amdgpu_buffer_rsrc_t r, int idx, bool ok, float v) {
   buf_store<float>(r, (uint32_t)idx * 4u, ok, v);
 }
+// Elements idx .. idx + 3 (idx a multiple of 4 from a 16-byte aligned base; 0 past the extent).
+__device__ __forceinline__ float4 ldf4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+}
+__device__ __forceinline__ void stf4(__amdgpu_buffer_rsrc_t r, uint32_t off, bool ok, float4 v) {
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  const u4 q = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+  __builtin_amdgcn_raw_buffer_store_b128(q, r, (int)(ok ? off : kDropOffset), 0, 0);
+}
+__device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
 
 constexpr int kInKB = 64;  // in_proj k values per wavefront per pass (4 wavefronts: 256 per pass)
 
@@ -79,19 +90,19 @@ __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
   const bool emb = p.tokens != nullptr;
   const auto ru = emb ? flat_buffer(p.embed, (int64_t)p.V * dm * 4) : flat_buffer(p.u_src, (int64_t)B * dm * 4);
   const auto rdu = flat_buffer(p.du, (int64_t)B * ndu * dm * 4);
-  float uv[kInRows][KQ], dv[kInRows][KQ][NDU > 0 ? NDU : 1];
-#pragma unroll
-  for (int r = 0; r < kInRows; ++r) {
-    const int b = b0 + r;  // rows past the batch read 0
+  // rebuild role: row wv, elements k4 .. k4 + 3, k4 = 4 lane + 256 q (d_model a multiple of 4)
+  float4 uv[KQ], dv[KQ][NDU > 0 ? NDU : 1];
+  {
+    const int b = b0 + wv;  // rows past the batch read 0
     int64_t row = b;
     if (emb) row = b < B ? p.tokens[b] : -1;
     const bool rok = row >= 0 && row < (emb ? p.V : B);
 #pragma unroll
     for (int q = 0; q < KQ; ++q) {
-      const int k = tid + q * kStThreads;
-      uv[r][q] = buf_load<float>(ru, rok ? (uint32_t)(row * dm + k) * 4u : kDropOffset);
+      const int k4 = 4 * lane + q * kStThreads;
+      uv[q] = ldf4(ru, rok ? (uint32_t)(row * dm + k4) * 4u : kDropOffset);
 #pragma unroll
-      for (int t = 0; t < NDU; ++t) dv[r][q][t] = t < ndu ? ldf(rdu, (b * ndu + t) * dm + k) : 0.f;
+      for (int t = 0; t < NDU; ++t) dv[q][t] = ldf4(rdu, t < ndu ? (uint32_t)((b * ndu + t) * dm + k4) * 4u : kDropOffset);
     }
   }
 
@@ -125,19 +136,17 @@ __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
 #pragma unroll
     for (int i = 0; i < kInKB; ++i) wr[q][i] = ldf(rw, ((q * NWV + wv) * kInKB + i) * ncol + col);  // 0 past d_model
 
-  // residual stream of the 4 rows: u + the previous block's partial sums in order
+  // residual stream of row wv: u + the previous block's partial sums in order
 #pragma unroll
-  for (int rr = 0; rr < kInRows; ++rr) {
+  for (int q = 0; q < KQ; ++q) {
+    const int k4 = 4 * lane + q * kStThreads;
+    float4 v = uv[q];
 #pragma unroll
-    for (int q = 0; q < KQ; ++q) {
-      const int k = tid + q * kStThreads;
-      float v = uv[rr][q];
-#pragma unroll
-      for (int t = 0; t < NDU; ++t) v += dv[rr][q][t];
-      v = k < dm ? v : 0.f;
-      if (p.write_u && ct == 0) stf(flat_buffer(p.u_dst, (int64_t)B * dm * 4), (b0 + rr) * dm + k, b0 + rr < B && k < dm, v);
-      us[rr][k] = v;
-    }
+    for (int t = 0; t < NDU; ++t) v = add4(v, dv[q][t]);
+    if (k4 >= dm) v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (p.write_u && ct == 0)
+      stf4(flat_buffer(p.u_dst, (int64_t)B * dm * 4), (uint32_t)((b0 + wv) * dm + k4) * 4u, b0 + wv < B && k4 < dm, v);
+    *(float4 *)&us[wv][k4] = v;
   }
 #pragma unroll
   for (int i = 0; i < XPN; ++i) {
@@ -229,7 +238,24 @@ __global__ void __launch_bounds__(kStThreads) k_dec_scan(const DecScanParams p) 
   const int b0 = rt * kScRows, c0 = c2 * kScCh;
   const int B = p.B, dm = p.dm, Dm = p.Dm, P = p.P, nct = p.nct;
 
-  // every global read first
+  // every global read first, the states (the longest to arrive) leading
+  const int pr = tid >> 1, half = tid & 1, r = pr / kScCh, dl = pr % kScCh;
+  const int b = b0 + r, d = c0 + dl;
+  const bool ok = b < B && d < Dm;
+  const int bc = min(b, B - 1), dc = min(d, Dm - 1), n0 = half * NPH, r0 = half * RHALF;
+  const auto rh = flat_buffer(p.ssm_state, (int64_t)B * Dm * N * 4);
+  const auto ral = flat_buffer(p.A_log, (int64_t)Dm * N * 4);
+  float hr[NPH], lr[NPH];
+#pragma unroll
+  for (int i = 0; i < NPH; i += 4) {
+    const float4 h4 = ldf4(rh, (uint32_t)((bc * Dm + dc) * N + n0 + i) * 4u);
+    hr[i] = h4.x; hr[i + 1] = h4.y; hr[i + 2] = h4.z; hr[i + 3] = h4.w;
+  }
+#pragma unroll
+  for (int i = 0; i < NPH; i += 4) {
+    const float4 a4 = ldf4(ral, (uint32_t)(dc * N + n0 + i) * 4u);
+    lr[i] = a4.x; lr[i + 1] = a4.y; lr[i + 2] = a4.z; lr[i + 3] = a4.w;
+  }
   float pv[NCT];
   if (wv < kScRows) {
     const auto rpart = flat_buffer(p.part, (int64_t)B * nct * P * 4);
@@ -237,25 +263,17 @@ __global__ void __launch_bounds__(kStThreads) k_dec_scan(const DecScanParams p) 
 #pragma unroll
     for (int t = 0; t < NCT; ++t) pv[t] = t < nct ? ldf(rpart, (b * nct + t) * P + lane) : 0.f;
   }
-  const int pr = tid >> 1, half = tid & 1, r = pr / kScCh, dl = pr % kScCh;
-  const int b = b0 + r, d = c0 + dl;
-  const bool ok = b < B && d < Dm;
-  const int bc = min(b, B - 1), dc = min(d, Dm - 1), n0 = half * NPH, r0 = half * RHALF;
   const auto rdt = flat_buffer(p.dt_proj_w, (int64_t)Dm * R * 4);
   float wdt[RHALF];
 #pragma unroll
-  for (int i = 0; i < RHALF; ++i) wdt[i] = ldf(rdt, dc * R + r0 + i);
+  for (int i = 0; i < RHALF; i += 4) {
+    const float4 w4 = ldf4(rdt, (uint32_t)(dc * R + r0 + i) * 4u);
+    wdt[i] = w4.x; wdt[i + 1] = w4.y; wdt[i + 2] = w4.z; wdt[i + 3] = w4.w;
+  }
   const float dtb = ldf(flat_buffer(p.dt_bias, (int64_t)Dm * 4), dc);
   const float dsk = ldf(flat_buffer(p.Dskip, (int64_t)Dm * 4), dc);
   const float xcv = ldf(flat_buffer(p.xc, (int64_t)B * Dm * 4), bc * Dm + dc);
   const float gv = ldf(flat_buffer(p.gate, (int64_t)B * Dm * 4), bc * Dm + dc);
-  const auto rh = flat_buffer(p.ssm_state, (int64_t)B * Dm * N * 4);
-  const auto ral = flat_buffer(p.A_log, (int64_t)Dm * N * 4);
-  float hr[NPH], lr[NPH];
-#pragma unroll
-  for (int i = 0; i < NPH; ++i) hr[i] = ldf(rh, (bc * Dm + dc) * N + n0 + i);
-#pragma unroll
-  for (int i = 0; i < NPH; ++i) lr[i] = ldf(ral, dc * N + n0 + i);
   const auto rwo = flat_buffer(p.w_out_t, (int64_t)Dm * dm * 4);
   float wo[KQ][kScCh];
 #pragma unroll
@@ -300,7 +318,8 @@ __global__ void __launch_bounds__(kStThreads) k_dec_scan(const DecScanParams p) 
   y += __shfl_xor(y, 1);
   if (half == 0) ys[r][dl] = ok ? fmaf(dsk, xcv, y) * gv : 0.f;
 #pragma unroll
-  for (int i = 0; i < NPH; ++i) stf(rh, (b * Dm + d) * N + n0 + i, ok, hr[i]);
+  for (int i = 0; i < NPH; i += 4)
+    stf4(rh, (uint32_t)((b * Dm + d) * N + n0 + i) * 4u, ok, make_float4(hr[i], hr[i + 1], hr[i + 2], hr[i + 3]));
   __syncthreads();
 
   // out_proj partial sums over this tile's channels (channels past dim hold 0)

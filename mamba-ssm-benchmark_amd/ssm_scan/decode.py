@@ -11,7 +11,7 @@ over the whole GPU (block 0's first reads the tokens' embedding rows),
 and one launch at the end for the last block's sums, the final RMSNorm and the head (its weight
 with the norm's folded in); which computes what models/lm.py:124-128 computes at L = 1 with
 states (the blocks :82-83, the mixer models/mamba.py:93-124), in place of ~20 small launches
-per block.  Shapes past the stack kernels' limits (d_model > 512,
+per block.  Shapes past the stack kernels' limits (d_model > 512 or not a multiple of 4,
 dim > 1024, dstate not 8 or 16, dt_rank not 8, 16 or 32, conv width > 4) take the per-block
 path: three launches per block,
     xz = u @ (W_in diag(norm_w))^T          one GEMM (the block's RMSNorm weight folded in)
@@ -45,7 +45,8 @@ class FastDecoder:
         self.model = model
         self.refresh()
         m0 = self.layers[0]["mixer"]
-        fits = (model.blocks[0].norm1.weight.numel() <= STACK_LIMITS["d_model"] and m0.d_inner <= STACK_LIMITS["dim"]
+        dm = model.blocks[0].norm1.weight.numel()
+        fits = (dm <= STACK_LIMITS["d_model"] and dm % 4 == 0 and m0.d_inner <= STACK_LIMITS["dim"]
                 and m0.d_state in STACK_LIMITS["dstate"] and m0.dt_rank in STACK_LIMITS["dt_rank"]
                 and m0.d_conv <= STACK_LIMITS["width"])
         if path == "stack" and not fits:

@@ -253,7 +253,7 @@ def test_decode_stack_workspace_layout():
 @pytest.mark.parametrize("field,value", [("d_model", 513), ("dim", 1025), ("dstate", 12), ("dt_rank", 24),
                                          ("width", 5), ("method", 3), ("batch", 0), ("n_blocks", 0),
                                          ("conv_state_dtype", 2), ("workspace_bytes", 1024), ("workspace", None),
-                                         ("u", None), ("batch", 1 << 20)])
+                                         ("u", None), ("batch", 1 << 20), ("d_model", 250), ("u", 8)])
 def test_decode_stack_validation(field, value):
     """ssm_decode_stack_check rejects shapes past the stack kernels' limits, a missing or short
     workspace and offsets past 32 bits before any launch."""

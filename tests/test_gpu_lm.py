@@ -290,13 +290,13 @@ ORACLE_DECODE_SHAPES = [
 
 
 # the stack kernels' shapes: the LM preset; dstate 8 bilinear over a ragged batch; dim 240 and
-# 500 (ragged channel tiles), d_model 250 (not a multiple of 4), width 1 and 2; d_model 512
+# 488 (ragged channel tiles), width 1 and 2; d_model 512
 # (two passes over d_model, dt_rank 32, dim 1024); a single block (the last-block sums in place)
 STACK_DECODE_SHAPES = [
     (dict(n_layers=10), 64),
     (dict(n_layers=3, d_state=8, discretization="bilinear"), 37),
     (dict(n_layers=2, d_model=120, d_conv=1, discretization="euler"), 5),
-    (dict(n_layers=2, d_model=250, d_conv=2), 19),
+    (dict(n_layers=2, d_model=244, d_conv=2), 19),
     (dict(n_layers=2, d_model=512), 64),
     (dict(n_layers=1, d_model=128, d_state=8), 9),
 ]
@@ -372,10 +372,11 @@ def test_decode_stack_limits_fall_back_to_blocks(dev):
     """Shapes past the stack kernels' limits take the per-block path; asking for the stack path
     with them is an error."""
     from ssm_scan.decode import FastDecoder
-    model = MambaLM(n_layers=1, d_state=12).to(dev).eval()
-    assert FastDecoder(model).path == "block"
-    with pytest.raises(ValueError):
-        FastDecoder(model, path="stack")
+    for shape in (dict(d_state=12), dict(d_model=250)):
+        model = MambaLM(n_layers=1, **shape).to(dev).eval()
+        assert FastDecoder(model).path == "block"
+        with pytest.raises(ValueError):
+            FastDecoder(model, path="stack")
 
 
 # the row-resident kernel (LM preset) and the general one (dstate 12, width 5)
