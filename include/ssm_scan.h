@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 7
+#define SSM_ABI_VERSION 8
 
 enum { SSM_OK = 0, SSM_EINVAL = 1, SSM_EKEY = 2, SSM_ESPACE = 3, SSM_EHIP = 4 };
 
@@ -199,15 +199,19 @@ typedef struct ssm_decode_args {
  * leaving the last (the input of the final norm and head).  Optionally the call also covers the
  * token step's ends (models/lm.py:125,128): with `tokens`, the residual stream entering the
  * first block is the tokens' embedding rows (u is then output only; an id outside
- * [0, vocab) reads a zero row, where the reference's embedding raises); with `head_w_t`, the
- * logits of the final RMSNorm and the head are written.  Every block has the same
- * dimensions; tensors are float32 and row-major (conv states float32 or bf16), states are
- * updated in place, and every sum runs in a fixed order (the step is deterministic).
- * Supported: d_model <= 512 and a multiple of 4, dim <= 1024, dstate 8 or 16, dt_rank 8, 16 or
- * 32, width <= 4; u, embed, ssm_state, A_log and dt_proj_w 16-byte aligned;
+ * [0, vocab) reads a zero row, where the reference's embedding raises); with `head_w4`, the
+ * logits of the final RMSNorm and the head are written.  The GEMM weights come in a layout of
+ * four consecutive k per column (w_in4, w_out4, head_w4), so a lane reads 16 bytes at a time.
+ * Every block has the same dimensions; tensors are float32 and row-major (conv states float32
+ * or bf16), states are updated in place, and every sum runs in a fixed order (the step is
+ * deterministic).
+ * Supported: d_model <= 512, dim <= 1024, both multiples of 4, dstate 8 or 16, dt_rank 8, 16
+ * or 32, width <= 4; u, embed and every weight read four floats at a time (w_in4, w_out4,
+ * head_w4, A_log, dt_proj_w) and ssm_state 16-byte aligned;
  * ssm_decode_stack_check names the limit a shape breaks. */
 typedef struct ssm_decode_block {
-  const float *w_in_t;     /* (d_model, 2*dim): (W_in diag(norm_w))^T, the RMSNorm weight folded in */
+  const float *w_in4;      /* (d_model/4, 2*dim, 4): element [g][c][j] = W[c][4g + j] for
+                              W = W_in diag(norm_w), in_proj with the RMSNorm weight folded in */
   const float *conv_w;     /* (dim, width) */
   const float *conv_b;     /* (dim,) */
   const float *x_proj_wt;  /* (dim, dt_rank + 2*dstate): x_proj's weight transposed */
@@ -215,7 +219,7 @@ typedef struct ssm_decode_block {
   const float *dt_bias;    /* (dim,) */
   const float *A_log;      /* (dim, dstate): A = -exp(A_log) */
   const float *Dskip;      /* (dim,) */
-  const float *w_out_t;    /* (dim, d_model): out_proj's weight transposed */
+  const float *w_out4;     /* (dim/4, d_model, 4): element [g][c][j] = W_out[c][4g + j] */
   void *conv_state;        /* (B, dim, width-1) of conv_state_dtype, updated in place (may be
                               NULL when width is 1) */
   float *ssm_state;        /* (B, dim, dstate), updated in place */
@@ -235,8 +239,9 @@ typedef struct ssm_decode_stack_args {
   int64_t workspace_bytes;
   const int64_t *tokens;   /* (B,) token ids on the device, or NULL */
   const float *embed;      /* (vocab, d_model) embedding table, read when tokens is set */
-  const float *head_w_t;   /* (d_model, vocab): (W_head diag(norm_f_w))^T, or NULL (no head) */
-  float *logits;           /* (B, vocab), written when head_w_t is set */
+  const float *head_w4;    /* (d_model/4, vocab, 4): element [g][v][j] = W[v][4g + j] for
+                              W = W_head diag(norm_f_w), or NULL (no head) */
+  float *logits;           /* (B, vocab), written when head_w4 is set */
   int64_t vocab;
   float head_eps;          /* the final RMSNorm's epsilon */
   int32_t reserved1;

@@ -745,7 +745,8 @@ int ssm_decode_stack_check(const ssm_decode_stack_args *a) {
   if (a->dt_rank != 8 && a->dt_rank != 16 && a->dt_rank != 32)
     return fail(SSM_EINVAL, "dt_rank %lld not 8, 16 or 32", (long long)a->dt_rank);
   if (a->width > 4) return fail(SSM_EINVAL, "conv width %lld > 4", (long long)a->width);
-  if (a->d_model % 4) return fail(SSM_EINVAL, "d_model %lld not a multiple of 4", (long long)a->d_model);
+  if (a->d_model % 4 || a->dim % 4)
+    return fail(SSM_EINVAL, "d_model %lld and dim %lld must be multiples of 4", (long long)a->d_model, (long long)a->dim);
   // every buffer element is addressed by a 32-bit byte offset (with a few rows of slack)
   const StackLayout l = stack_layout(a);
   const int64_t rows = a->batch + kInRows;
@@ -754,20 +755,22 @@ int ssm_decode_stack_check(const ssm_decode_stack_args *a) {
     return fail(SSM_EINVAL, "decode stack too large for 32-bit offsets (batch %lld)", (long long)a->batch);
   for (int i = 0; i < a->n_blocks; ++i) {
     const ssm_decode_block &k = a->blocks[i];
-    if (!k.w_in_t || !k.conv_w || !k.conv_b || !k.x_proj_wt || !k.dt_proj_w || !k.dt_bias || !k.A_log ||
-        !k.Dskip || !k.w_out_t || (!k.conv_state && a->width > 1) || !k.ssm_state)
+    if (!k.w_in4 || !k.conv_w || !k.conv_b || !k.x_proj_wt || !k.dt_proj_w || !k.dt_bias || !k.A_log ||
+        !k.Dskip || !k.w_out4 || (!k.conv_state && a->width > 1) || !k.ssm_state)
       return fail(SSM_EINVAL, "block %d: a required tensor is missing", i);
-    if (((uintptr_t)k.ssm_state | (uintptr_t)k.A_log | (uintptr_t)k.dt_proj_w) % 16)
-      return fail(SSM_EINVAL, "block %d: ssm_state, A_log and dt_proj_w must be 16-byte aligned", i);
+    if (((uintptr_t)k.ssm_state | (uintptr_t)k.A_log | (uintptr_t)k.dt_proj_w | (uintptr_t)k.w_in4 |
+         (uintptr_t)k.w_out4) % 16)
+      return fail(SSM_EINVAL, "block %d: ssm_state, A_log, dt_proj_w, w_in4 and w_out4 must be 16-byte aligned", i);
   }
-  if (((uintptr_t)a->u | (uintptr_t)a->embed) % 16) return fail(SSM_EINVAL, "u and embed must be 16-byte aligned");
-  if (a->tokens || a->head_w_t) {
+  if (((uintptr_t)a->u | (uintptr_t)a->embed | (uintptr_t)a->head_w4) % 16)
+    return fail(SSM_EINVAL, "u, embed and head_w4 must be 16-byte aligned");
+  if (a->tokens || a->head_w4) {
     if (a->vocab < 1) return fail(SSM_EINVAL, "vocab %lld: the embedding or head needs a vocabulary", (long long)a->vocab);
     if ((a->batch + kInRows) * a->vocab * 4 >= (1LL << 31) || a->vocab * a->d_model * 4 >= (1LL << 31))
       return fail(SSM_EINVAL, "vocabulary too large for 32-bit offsets (vocab %lld)", (long long)a->vocab);
   }
   if (a->tokens && !a->embed) return fail(SSM_EINVAL, "tokens given without the embedding table");
-  if (a->head_w_t && !a->logits) return fail(SSM_EINVAL, "head weight given without a logits buffer");
+  if (a->head_w4 && !a->logits) return fail(SSM_EINVAL, "head weight given without a logits buffer");
   if (!a->workspace || a->workspace_bytes < l.total)
     return fail(SSM_ESPACE, "decode stack workspace %lld bytes < %lld", (long long)a->workspace_bytes,
                 (long long)l.total);
@@ -808,7 +811,7 @@ int ssm_decode_stack(const ssm_decode_stack_args *a, void *stream) {
     pi.u_src = i == 0 ? a->u : dst(i - 1);
     pi.du = i == 0 ? nullptr : du;
     pi.u_dst = dst(i);
-    pi.w_in_t = k.w_in_t; pi.conv_w = k.conv_w; pi.conv_b = k.conv_b; pi.x_proj_wt = k.x_proj_wt;
+    pi.w_in4 = k.w_in4; pi.conv_w = k.conv_w; pi.conv_b = k.conv_b; pi.x_proj_wt = k.x_proj_wt;
     pi.conv_state = k.conv_state;
     pi.xc = xc; pi.gate = gate; pi.part = part;
     hipError_t e = launch_dec_in(pi, (int)a->width, s);
@@ -819,19 +822,19 @@ int ssm_decode_stack(const ssm_decode_stack_args *a, void *stream) {
     ps.nrt = (int)cdiv(B, kScRows); ps.nct = (int)l.nct; ps.ndu = (int)l.ndu;
     ps.xc = xc; ps.gate = gate; ps.part = part;
     ps.dt_proj_w = k.dt_proj_w; ps.dt_bias = k.dt_bias; ps.A_log = k.A_log; ps.Dskip = k.Dskip;
-    ps.w_out_t = k.w_out_t; ps.ssm_state = k.ssm_state; ps.du = du;
+    ps.w_out4 = k.w_out4; ps.ssm_state = k.ssm_state; ps.du = du;
     e = launch_dec_scan(ps, a->method, s);
     if (e != hipSuccess) return hip_fail(e, "ssm_decode_stack scan-stage launch");
   }
   hipError_t e;
-  if (a->head_w_t) {  // the last block's sums, the final norm and the head in one launch
+  if (a->head_w4) {  // the last block's sums, the final norm and the head in one launch
     DecInParams ph;
     memset(&ph, 0, sizeof(ph));
     ph.B = B; ph.dm = dm; ph.Dm = 1; ph.P = 1; ph.V = (int)a->vocab;
     ph.nrt = (int)cdiv(B, kInRows); ph.nct = (int)cdiv(a->vocab, 64); ph.ndu = (int)l.ndu;
     ph.write_u = 1; ph.eps = a->head_eps;
     ph.u_src = dst(a->n_blocks - 1); ph.du = du; ph.u_dst = a->u;
-    ph.head_w_t = a->head_w_t; ph.logits = a->logits;
+    ph.head_w4 = a->head_w4; ph.logits = a->logits;
     e = launch_dec_head(ph, s);
   } else {
     DecOutParams po;

@@ -125,16 +125,18 @@ __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
 #pragma unroll
   for (int i = 0; i < XPN; ++i) xpv[i] = HEAD ? 0.f : ldf(rxp, c0 * P + tid + i * kStThreads);  // 0 past dim
 
-  // GEMM weight columns of this lane (a channel or vocabulary entry past the end reads a valid
-  // column whose results are never used), k split over the wavefronts
+  // GEMM weight column of this lane, four k per read from the (d_model / 4, ncol, 4) layout (a
+  // channel or vocabulary entry past the end reads a valid column whose results are never
+  // used), k split over the wavefronts
   const int ncol = HEAD ? p.V : 2 * Dm;
-  const auto rw = flat_buffer(HEAD ? p.head_w_t : p.w_in_t, (int64_t)dm * ncol * 4);
+  const auto rw = flat_buffer(HEAD ? p.head_w4 : p.w_in4, (int64_t)dm * ncol * 4);
   const int col = HEAD ? min(ct * kWave + lane, p.V - 1) : (lane < kInCh ? 0 : Dm) + min(c0 + (lane & (kInCh - 1)), Dm - 1);
-  float wr[KQ][kInKB];
+  float4 wr[KQ][kInKB / 4];
 #pragma unroll
   for (int q = 0; q < KQ; ++q)
 #pragma unroll
-    for (int i = 0; i < kInKB; ++i) wr[q][i] = ldf(rw, ((q * NWV + wv) * kInKB + i) * ncol + col);  // 0 past d_model
+    for (int i = 0; i < kInKB / 4; ++i)  // 0 past d_model
+      wr[q][i] = ldf4(rw, (uint32_t)(((q * NWV + wv) * (kInKB / 4) + i) * ncol + col) * 16u);
 
   // residual stream of row wv: u + the previous block's partial sums in order
 #pragma unroll
@@ -169,19 +171,30 @@ __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
 #pragma unroll
   for (int rr = 0; rr < kInRows; ++rr) acc[rr] = 0.f;
 #pragma unroll
-  for (int q = 0; q < KQ; ++q)
+  for (int q = 0; q < KQ; ++q) {
+    const int kb = (q * NWV + wv) * kInKB;
+    float4 un[kInRows];  // the next k group's stream values, read one group ahead
 #pragma unroll
-    for (int i = 0; i < kInKB; i += 4) {
-      const int k = (q * NWV + wv) * kInKB + i;
+    for (int rr = 0; rr < kInRows; ++rr) un[rr] = *(const float4 *)&us[rr][kb];
+#pragma unroll
+    for (int i = 0; i < kInKB / 4; ++i) {
+      float4 uc[kInRows];
+#pragma unroll
+      for (int rr = 0; rr < kInRows; ++rr) uc[rr] = un[rr];
+      if (i + 1 < kInKB / 4) {
+#pragma unroll
+        for (int rr = 0; rr < kInRows; ++rr) un[rr] = *(const float4 *)&us[rr][kb + 4 * (i + 1)];
+      }
+      const float4 w = wr[q][i];
 #pragma unroll
       for (int rr = 0; rr < kInRows; ++rr) {
-        const float4 u4 = *(const float4 *)&us[rr][k];
-        acc[rr] = fmaf(wr[q][i], u4.x, acc[rr]);
-        acc[rr] = fmaf(wr[q][i + 1], u4.y, acc[rr]);
-        acc[rr] = fmaf(wr[q][i + 2], u4.z, acc[rr]);
-        acc[rr] = fmaf(wr[q][i + 3], u4.w, acc[rr]);
+        acc[rr] = fmaf(w.x, uc[rr].x, acc[rr]);
+        acc[rr] = fmaf(w.y, uc[rr].y, acc[rr]);
+        acc[rr] = fmaf(w.z, uc[rr].z, acc[rr]);
+        acc[rr] = fmaf(w.w, uc[rr].w, acc[rr]);
       }
     }
+  }
 #pragma unroll
   for (int rr = 0; rr < kInRows; ++rr) gsum[wv][rr][lane] = acc[rr];
   __syncthreads();
@@ -274,12 +287,13 @@ __global__ void __launch_bounds__(kStThreads) k_dec_scan(const DecScanParams p) 
   const float dsk = ldf(flat_buffer(p.Dskip, (int64_t)Dm * 4), dc);
   const float xcv = ldf(flat_buffer(p.xc, (int64_t)B * Dm * 4), bc * Dm + dc);
   const float gv = ldf(flat_buffer(p.gate, (int64_t)B * Dm * 4), bc * Dm + dc);
-  const auto rwo = flat_buffer(p.w_out_t, (int64_t)Dm * dm * 4);
-  float wo[KQ][kScCh];
+  const auto rwo = flat_buffer(p.w_out4, (int64_t)Dm * dm * 4);  // (dim / 4, d_model, 4)
+  float4 wo[KQ][kScCh / 4];
 #pragma unroll
   for (int q = 0; q < KQ; ++q)
 #pragma unroll
-    for (int i = 0; i < kScCh; ++i) wo[q][i] = ldf(rwo, (c0 + i) * dm + tid + q * kStThreads);  // 0 past dim
+    for (int i = 0; i < kScCh / 4; ++i)  // 0 past dim
+      wo[q][i] = ldf4(rwo, (uint32_t)((c0 / 4 + i) * dm + tid + q * kStThreads) * 16u);
 
   // x_proj outputs of the 2 rows: the partial sums in order
   if (wv < kScRows) {
@@ -332,11 +346,11 @@ __global__ void __launch_bounds__(kStThreads) k_dec_scan(const DecScanParams p) 
       float a = 0.f;
 #pragma unroll
       for (int i = 0; i < kScCh; i += 4) {
-        const float4 y4 = *(const float4 *)&ys[rr][i];
-        a = fmaf(y4.x, wo[q][i], a);
-        a = fmaf(y4.y, wo[q][i + 1], a);
-        a = fmaf(y4.z, wo[q][i + 2], a);
-        a = fmaf(y4.w, wo[q][i + 3], a);
+        const float4 y4 = *(const float4 *)&ys[rr][i], w = wo[q][i / 4];
+        a = fmaf(y4.x, w.x, a);
+        a = fmaf(y4.y, w.y, a);
+        a = fmaf(y4.z, w.z, a);
+        a = fmaf(y4.w, w.w, a);
       }
       stf(rdu, ((b0 + rr) * p.ndu + c2) * dm + jo, b0 + rr < B && jo < dm, a);
     }

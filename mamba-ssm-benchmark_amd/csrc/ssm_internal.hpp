@@ -220,19 +220,20 @@ struct DecInParams {
   float eps;
   const int64_t *tokens;  // (B,) or null: the residual stream is the embedding rows of the tokens
   const float *embed;     // (V, dm)
-  const float *head_w_t;  // (dm, V) head weight (the final norm's weight folded in)
+  const float *head_w4;   // (dm / 4, V, 4) head weight (the final norm's weight folded in)
   float *logits;          // (B, V)
   const float *u_src;     // (B, dm) residual stream of the previous layer
   const float *du;        // (B, ndu, dm) its out_proj partial sums (ndu = 0: none)
   float *u_dst;           // (B, dm) the residual stream entering this layer (write_u)
-  const float *w_in_t;    // (dm, 2 Dm)
+  const float *w_in4;     // (dm / 4, 2 Dm, 4)
   const float *conv_w, *conv_b, *x_proj_wt;
   void *conv_state;
   float *xc, *gate, *part;  // (B, Dm), (B, Dm), (B, nct, P)
 };
 struct DecScanParams {
   int B, dm, Dm, N, R, P, nrt, nct, ndu;
-  const float *xc, *gate, *part, *dt_proj_w, *dt_bias, *A_log, *Dskip, *w_out_t;
+  const float *xc, *gate, *part, *dt_proj_w, *dt_bias, *A_log, *Dskip;
+  const float *w_out4;    // (Dm / 4, dm, 4)
   float *ssm_state, *du;  // du: (B, ndu, dm)
 };
 struct DecOutParams {

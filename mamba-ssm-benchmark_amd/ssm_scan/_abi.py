@@ -11,7 +11,7 @@ import os
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssmscan.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 OK, EINVAL, EKEY, ESPACE, EHIP = 0, 1, 2, 3, 4
 ZOH, EULER, BILINEAR = 0, 1, 2
@@ -74,8 +74,8 @@ class DecodeArgs(ctypes.Structure):
 
 
 class DecodeBlock(ctypes.Structure):
-    _fields_ = [("w_in_t", c_vp), ("conv_w", c_vp), ("conv_b", c_vp), ("x_proj_wt", c_vp), ("dt_proj_w", c_vp),
-                ("dt_bias", c_vp), ("A_log", c_vp), ("Dskip", c_vp), ("w_out_t", c_vp),
+    _fields_ = [("w_in4", c_vp), ("conv_w", c_vp), ("conv_b", c_vp), ("x_proj_wt", c_vp), ("dt_proj_w", c_vp),
+                ("dt_bias", c_vp), ("A_log", c_vp), ("Dskip", c_vp), ("w_out4", c_vp),
                 ("conv_state", c_vp), ("ssm_state", c_vp), ("eps", ctypes.c_float), ("reserved0", c_i32)]
 
 
@@ -85,7 +85,7 @@ class DecodeStackArgs(ctypes.Structure):
                 ("n_blocks", c_i32), ("reserved0", c_i32),
                 ("blocks", ctypes.POINTER(DecodeBlock)), ("u", c_vp),
                 ("workspace", c_vp), ("workspace_bytes", c_i64),
-                ("tokens", c_vp), ("embed", c_vp), ("head_w_t", c_vp), ("logits", c_vp), ("vocab", c_i64),
+                ("tokens", c_vp), ("embed", c_vp), ("head_w4", c_vp), ("logits", c_vp), ("vocab", c_i64),
                 ("head_eps", ctypes.c_float), ("reserved1", c_i32)]
 
 class LscanArgs(ctypes.Structure):

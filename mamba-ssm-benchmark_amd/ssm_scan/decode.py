@@ -35,6 +35,13 @@ from .hip_scan import METHODS
 STACK_LIMITS = dict(d_model=512, dim=1024, dstate=(8, 16), dt_rank=(8, 16, 32), width=4)
 
 
+def _four_k(w):
+    """(n, k) weight -> (k / 4, n, 4): element [g][c][j] = w[c][4 g + j] (four consecutive k of a
+    column in 16 bytes), the layout the stack kernels read; k a multiple of 4."""
+    n, k = w.shape
+    return w.reshape(n, k // 4, 4).permute(1, 0, 2).contiguous()
+
+
 class FastDecoder:
     def __init__(self, model, path="auto"):
         """path: "auto" (the stack path where the shape allows it), "stack" or "block"."""
@@ -43,16 +50,17 @@ class FastDecoder:
         if path not in ("auto", "stack", "block"):
             raise ValueError(f"unknown decode path {path!r}")
         self.model = model
-        self.refresh()
-        m0 = self.layers[0]["mixer"]
+        m0 = model.blocks[0].mixer
         dm = model.blocks[0].norm1.weight.numel()
         fits = (dm <= STACK_LIMITS["d_model"] and dm % 4 == 0 and m0.d_inner <= STACK_LIMITS["dim"]
+                and m0.d_inner % 4 == 0
                 and m0.d_state in STACK_LIMITS["dstate"] and m0.dt_rank in STACK_LIMITS["dt_rank"]
                 and m0.d_conv <= STACK_LIMITS["width"])
         if path == "stack" and not fits:
             raise ValueError("the model's shape is past the stack decode kernels' limits")
         self.path = "stack" if (path == "stack" or (path == "auto" and fits)) else "block"
         self._ws = {}
+        self.refresh()
 
     @torch.no_grad()
     def refresh(self):
@@ -72,11 +80,12 @@ class FastDecoder:
                 Dskip=m.D.contiguous(),
                 w_out_t=m.out_proj.weight.t(),
                 eps=blk.norm1.eps, mixer=m))
-            L = self.layers[-1]
-            L["w_in_tc"] = L["w_in"].t().contiguous()
-            L["w_out_tc"] = m.out_proj.weight.t().contiguous()
-        # the head with the final RMSNorm weight folded into its columns, (d_model, vocab)
-        self.head_w_t = (self.model.head.weight * self.model.norm_f.weight[None, :]).t().contiguous()
+            if self.path == "stack":
+                L = self.layers[-1]
+                L["w_in4"] = _four_k(L["w_in"])
+                L["w_out4"] = _four_k(m.out_proj.weight)
+        if self.path == "stack":  # the head with the final RMSNorm weight folded into its columns
+            self.head_w4 = _four_k(self.model.head.weight * self.model.norm_f.weight[None, :])
 
     def _layer(self, L, u, state):
         m = L["mixer"]
@@ -102,18 +111,18 @@ class FastDecoder:
         """The whole token step in one call: embedding rows, every block, the final norm and
         the head; returns the logits."""
         m = self.layers[0]["mixer"]
-        B, dm = tok.numel(), self.head_w_t.shape[0]
+        B, dm, V = tok.numel(), self.model.head.weight.shape[1], self.model.head.weight.shape[0]
         tok = tok.reshape(-1).to(torch.long)
         u = torch.empty(B, dm, dtype=torch.float32, device=tok.device)
-        logits = torch.empty(B, self.head_w_t.shape[1], dtype=torch.float32, device=tok.device)
+        logits = torch.empty(B, V, dtype=torch.float32, device=tok.device)
         n = len(self.layers)
         blocks = (_abi.DecodeBlock * n)()
         for i, (L, st) in enumerate(zip(self.layers, states)):
             k = blocks[i]
-            k.w_in_t, k.conv_w, k.conv_b = L["w_in_tc"].data_ptr(), L["conv_w"].data_ptr(), L["conv_b"].data_ptr()
+            k.w_in4, k.conv_w, k.conv_b = L["w_in4"].data_ptr(), L["conv_w"].data_ptr(), L["conv_b"].data_ptr()
             k.x_proj_wt, k.dt_proj_w = L["x_proj_wt"].data_ptr(), L["dt_proj_w"].data_ptr()
             k.dt_bias, k.A_log, k.Dskip = L["dt_bias"].data_ptr(), L["A_log"].data_ptr(), L["Dskip"].data_ptr()
-            k.w_out_t = L["w_out_tc"].data_ptr()
+            k.w_out4 = L["w_out4"].data_ptr()
             k.conv_state, k.ssm_state = st.conv.data_ptr(), st.ssm.data_ptr()
             k.eps = L["eps"]
         a = _abi.DecodeStackArgs()
@@ -125,7 +134,7 @@ class FastDecoder:
         a.blocks = blocks
         a.u = u.data_ptr()
         a.tokens, a.embed = tok.data_ptr(), self.model.embed.weight.data_ptr()
-        a.head_w_t, a.logits, a.vocab = self.head_w_t.data_ptr(), logits.data_ptr(), logits.shape[1]
+        a.head_w4, a.logits, a.vocab = self.head_w4.data_ptr(), logits.data_ptr(), V
         a.head_eps = self.model.norm_f.eps
         lib = _abi.lib()
         need = lib.ssm_decode_stack_workspace_bytes(ctypes.byref(a))

@@ -268,7 +268,7 @@ def test_decode_stack_ends_validation(change):
     """The optional ends of the token step: tokens need the embedding table, a head needs a
     logits buffer, and either needs a vocabulary whose offsets fit 32 bits."""
     a = _stack_args()
-    a.tokens, a.embed, a.head_w_t, a.logits, a.vocab = 16, 16, 16, 16, 256
+    a.tokens, a.embed, a.head_w4, a.logits, a.vocab = 16, 16, 16, 16, 256
     assert _abi.lib().ssm_decode_stack_check(ctypes.byref(a)) == 0
     if change == "tokens_without_embed":
         a.embed = None
