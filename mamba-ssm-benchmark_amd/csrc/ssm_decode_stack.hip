@@ -166,35 +166,32 @@ __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
   }
   const float s = rsqrtf(wave_sum(ss) / (float)dm + p.eps);
 
-  // in_proj: this wavefront's quarter of k for the 4 rows, then the quarters in order
-  float acc[kInRows];
+  // in_proj on the matrix cores, this wavefront's quarter of k for the 4 rows:
+  // v_mfma_f32_4x4x1f32 computes 16 blocks of (4 rows x 1 k) x (1 k x 4 columns); lane l gives
+  // row l % 4's stream value and the weight of its own column l, and receives the 4 rows' sums
+  // of column l.  Four accumulators (k mod 4) keep four independent chains in flight; they and
+  // then the wavefronts' quarters are added in a fixed order.
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  f32x4 cacc[4];
 #pragma unroll
-  for (int rr = 0; rr < kInRows; ++rr) acc[rr] = 0.f;
+  for (int c = 0; c < 4; ++c) cacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int ur = lane & (kInRows - 1);
 #pragma unroll
   for (int q = 0; q < KQ; ++q) {
     const int kb = (q * NWV + wv) * kInKB;
-    float4 un[kInRows];  // the next k group's stream values, read one group ahead
-#pragma unroll
-    for (int rr = 0; rr < kInRows; ++rr) un[rr] = *(const float4 *)&us[rr][kb];
 #pragma unroll
     for (int i = 0; i < kInKB / 4; ++i) {
-      float4 uc[kInRows];
-#pragma unroll
-      for (int rr = 0; rr < kInRows; ++rr) uc[rr] = un[rr];
-      if (i + 1 < kInKB / 4) {
-#pragma unroll
-        for (int rr = 0; rr < kInRows; ++rr) un[rr] = *(const float4 *)&us[rr][kb + 4 * (i + 1)];
-      }
+      const float4 u4 = *(const float4 *)&us[ur][kb + 4 * i];
       const float4 w = wr[q][i];
-#pragma unroll
-      for (int rr = 0; rr < kInRows; ++rr) {
-        acc[rr] = fmaf(w.x, uc[rr].x, acc[rr]);
-        acc[rr] = fmaf(w.y, uc[rr].y, acc[rr]);
-        acc[rr] = fmaf(w.z, uc[rr].z, acc[rr]);
-        acc[rr] = fmaf(w.w, uc[rr].w, acc[rr]);
-      }
+      cacc[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(u4.x, w.x, cacc[0], 0, 0, 0);
+      cacc[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(u4.y, w.y, cacc[1], 0, 0, 0);
+      cacc[2] = __builtin_amdgcn_mfma_f32_4x4x1f32(u4.z, w.z, cacc[2], 0, 0, 0);
+      cacc[3] = __builtin_amdgcn_mfma_f32_4x4x1f32(u4.w, w.w, cacc[3], 0, 0, 0);
     }
   }
+  float acc[kInRows];
+#pragma unroll
+  for (int rr = 0; rr < kInRows; ++rr) acc[rr] = (cacc[0][rr] + cacc[1][rr]) + (cacc[2][rr] + cacc[3][rr]);
 #pragma unroll
   for (int rr = 0; rr < kInRows; ++rr) gsum[wv][rr][lane] = acc[rr];
   __syncthreads();
