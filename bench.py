@@ -250,7 +250,7 @@ def bench_c1(args, dev):
         "kernels_ms_stats": kstats,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic("ssm_bwd_c1"),
-                     "kernel": "ssm_bwd (k_bwd + k_bwd_finalize)", "alg_bytes_per_launch": bb,
+                     "kernel": "ssm_bwd (k_bwdw + k_bwd_finalize)", "alg_bytes_per_launch": bb,
                      "fwd_achieved": fb / (fwd_ms * 1e-3) / 1e9},
     }
     if not args.no_cpu_baseline:
