@@ -291,7 +291,8 @@ ORACLE_DECODE_SHAPES = [
 
 # the stack kernels' shapes: the LM preset; dstate 8 bilinear over a ragged batch; dim 240 and
 # 488 (ragged channel tiles), width 1 and 2; d_model 512
-# (two passes over d_model, dt_rank 32, dim 1024); a single block (the last-block sums in place)
+# (two passes over d_model, dt_rank 32, dim 1024); a single block; batch 1 with a vocabulary of
+# 300 (a ragged last vocabulary tile of the head)
 STACK_DECODE_SHAPES = [
     (dict(n_layers=10), 64),
     (dict(n_layers=3, d_state=8, discretization="bilinear"), 37),
@@ -299,6 +300,7 @@ STACK_DECODE_SHAPES = [
     (dict(n_layers=2, d_model=244, d_conv=2), 19),
     (dict(n_layers=2, d_model=512), 64),
     (dict(n_layers=1, d_model=128, d_state=8), 9),
+    (dict(n_layers=2, vocab_size=300), 1),
 ]
 
 
