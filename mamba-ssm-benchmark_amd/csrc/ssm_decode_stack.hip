@@ -13,14 +13,13 @@
 //               partial sums over the tile's channels.
 //
 // The token step's ends fold into the same kernels: block 0's k_dec_in may read the embedding
-// rows of the tokens as its residual stream (models/lm.py:125), and k_dec_head -- k_dec_in's
-// rebuild, RMSNorm scale and GEMM over vocabulary columns -- gives the logits of the final
-// norm and the head (models/lm.py:128); without a head, k_dec_out adds the last layer's partial
-// sums to its residual stream.  Every reduction runs
-// in a fixed order, so the step is deterministic.  A workgroup issues its global reads
-// (weights, states, partial sums) at entry, so each launch costs one memory round trip; the
-// workgroups that share a weight tile run on one XCD (blockIdx mod 8), so the tile is read
-// into one L2.
+// rows of the tokens as its residual stream (models/lm.py:125), and k_dec_in with its head
+// epilogue (HEAD: the rebuild, RMSNorm scale and GEMM over vocabulary columns) gives the logits
+// of the final norm and the head (models/lm.py:128); without a head, k_dec_out adds the last
+// layer's partial sums to its residual stream.  Every reduction runs in a fixed order, so the
+// step is deterministic.  A workgroup issues its global reads (states, weights, partial sums)
+// at entry, so each launch costs one memory round trip; the workgroups that share a weight tile
+// run on one XCD (blockIdx mod 8), so the tile is read into one L2.
 #include "ssm_device.hpp"
 #include "ssm_dpp.hpp"
 #include "ssm_internal.hpp"
@@ -65,10 +64,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // KQ passes of 256 over d_model; NDU >= the previous block's partial sums per row (0: none).
-// Roles: rebuild = element k = tid + 256 q of each of the 4 rows; RMSNorm and epilogue = row wv,
-// column lane (x channel c0 + lane for lane < 32, else z channel c0 + lane - 32); in_proj =
-// wavefront's quarter of k, lane's column; x_proj = row wv, output lane.  HEAD: the columns
-// are the 64 vocabulary entries of tile ct and the epilogue stores the logits.
+// Roles: rebuild and RMSNorm = row wv (lane: elements 4 lane .. 4 lane + 3 of each pass);
+// epilogue = row wv, column lane (x channel c0 + lane for lane < 32, else z channel
+// c0 + lane - 32); in_proj = the wavefront's quarter of k for the 4 rows on the matrix cores,
+// lane's column; x_proj = row wv, output lane.  HEAD: the columns are the 64 vocabulary entries
+// of tile ct and the epilogue stores the logits.
 template <int W, int KQ, int NDU, bool HEAD>
 __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
   constexpr int NWV = kStThreads / kWave;
