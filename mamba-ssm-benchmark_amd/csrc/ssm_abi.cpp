@@ -115,7 +115,7 @@ bool saved_rows_fit(const FwdLayout &f, int64_t L, int64_t D, int dtype) {
 // channels-per-wavefront) wavefronts leave the GPU short of work (fewer than kSegEnough); then
 // enough segments for about kSegTarget wavefronts, each at least kSegMinChunks chunks long.  A
 // positive `requested` overrides the choice (clamped to the valid range).
-constexpr int64_t kSegEnough = 2048, kSegTarget = 4096, kSegMinChunks = 4;
+constexpr int64_t kSegEnough = 2048, kSegTarget = 6144, kSegMinChunks = 4;
 
 struct SegPlan {
   int nseg, seg_chunks;
@@ -154,7 +154,7 @@ BwdLayout bwd_layout(const ssm_bwd_args *a) {
   const int64_t part = align256(a->batch * w.ntiles * a->seqlen * w.f.np * ss);
   w.dB = off; off += part;
   w.dC = off; off += part;
-  w.dA = off; off += align256(rows * a->dim * w.f.np * ss);
+  w.dA = off; off += align256(rows * a->dim * w.f.np * 8);  // float64 partials
   w.dD = off; off += align256(rows * a->dim * ss);
   w.db = off; off += align256(rows * a->dim * ss);
   const int64_t segs = w.sp.nseg > 1 ? rows * a->dim * w.f.np : 0;

@@ -425,7 +425,7 @@ k_bwd(const BwdParams p) {
     chunk(T1, k - 1);
   }
 
-  if (dval) ((CT *)p.ws_dA)[(b * p.D + d) * NP + n] = dA_acc * ac.invA;
+  if (dval) ((double *)p.ws_dA)[(b * p.D + d) * NP + n] = (double)(dA_acc * ac.invA);
   if (p.has_dh0 && dval && nval)
     vstore<CT>(p.dh0, b * p.dh0.s0 + d * p.dh0.s1 + n * p.dh0.s2,
                (CT)(M1 ? fma(dh64, (double)a_next, dh64) : dh64 * (double)a_next));
@@ -532,9 +532,11 @@ __global__ void __launch_bounds__(256) k_bwd_finalize(const FinParams p) {
   const int64_t j = i - nBC;
   if (j < nDN) {
     const int64_t d = j / p.N, nn = j % p.N;
-    CT s = fin_sum((const CT *)p.ws_dA + d * p.np + nn, p.D * p.np, p.rows);
-    if (p.a_log) s *= -exp(vload<CT>(p.A, d * p.A.s0 + nn * p.A.s1));  // dA_log = dA * A
-    vstore<CT>(p.dA, d * p.dA.s0 + nn * p.dA.s1, s);
+    // the row partials are float64 (each sums a row's or segment's steps): their sum, then one
+    // rounding to the output type
+    double s = fin_sum((const double *)p.ws_dA + d * p.np + nn, p.D * p.np, p.rows);
+    if (p.a_log) s *= -exp((double)vload<CT>(p.A, d * p.A.s0 + nn * p.A.s1));  // dA_log = dA * A
+    vstore<CT>(p.dA, d * p.dA.s0 + nn * p.dA.s1, (CT)s);
     return;
   }
   const int64_t k = j - nDN;
@@ -938,7 +940,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
     }
     return;
   } else {
-    if (dval) ((float *)q.ws_dA)[sidx] = (float)(M1 ? dA64 * (double)ac.invA : dA64);
+    if (dval) ((double *)q.ws_dA)[sidx] = M1 ? dA64 * (double)ac.invA : dA64;
     if (q.has_dh0 && dval && nval && seg == 0)
       vstore<float>(q.dh0, b * q.dh0.s0 + d * q.dh0.s1 + n * q.dh0.s2, (float)lam_a);
     // dD and d_bias: the lead row's lanes hold one step slot each; sum them (fixed order)

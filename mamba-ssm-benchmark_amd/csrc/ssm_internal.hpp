@@ -115,7 +115,7 @@ struct BwdParams {
   const void *ckpt;
   const void *ypre;
   void *ws_dB, *ws_dC;  // (B, ntiles, L, NP) partial sums over the tile's channels
-  void *ws_dA;          // (B, nseg, D, NP) partial over time
+  void *ws_dA;          // (B, nseg, D, NP) float64 partials over time
   void *ws_dD, *ws_db;  // (B, nseg, D)
 };
 

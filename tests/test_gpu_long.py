@@ -93,7 +93,7 @@ def test_config2_longest_forward_matches_c_oracle(dev, dtype):
 def test_long_sequence_backward_matches_c_oracle(dev):
     """The reference's long-sequence fwd+bwd benchmark shape (benchmarks/bench_scan.py:35-66:
     B1 D512 N16, here at L = 65536) with the z gate and D skip: one batch row of 512 channels
-    leaves the GPU short of work, so the backward walks 32 time segments from the adjoints its
+    leaves the GPU short of work, so the backward walks 48 time segments from the adjoints its
     summary and carry passes hand them.  Every gradient against the C float64 oracle."""
     L = 65536
     t = baseline_inputs(1, L, 512, 16, gate=True, with_dy=True)
