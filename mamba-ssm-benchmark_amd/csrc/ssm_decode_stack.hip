@@ -18,8 +18,8 @@
 // of the final norm and the head (models/lm.py:128); without a head, k_dec_out adds the last
 // layer's partial sums to its residual stream.  Every reduction runs in a fixed order, so the
 // step is deterministic.  A workgroup issues its global reads (states, weights, partial sums)
-// at entry, so each launch costs one memory round trip; the workgroups that share a weight tile
-// run on one XCD (blockIdx mod 8), so the tile is read into one L2.
+// at entry, so each launch costs one memory round trip; workgroups are grouped on XCDs
+// (blockIdx mod 8) by the weight tiles and rows they share, so each is read into few L2s.
 #include "ssm_device.hpp"
 #include "ssm_dpp.hpp"
 #include "ssm_internal.hpp"
@@ -80,8 +80,19 @@ __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
   __shared__ float xcs[kInRows][kInCh];
   __shared__ float xps[kInCh * kWave];        // x_proj weight rows of the tile, (kInCh, P) row-major
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid >> 6;
-  const int L = xcd_linear(blockIdx.x, gridDim.x);
-  const int ct = L / p.nrt, rt = L - ct * p.nrt;
+  // XCD grouping: where the grid allows, XCD x takes row half x / 4 and column quarter x % 4,
+  // so each XCD's L2 holds a quarter of the weight tiles and half of the partial-sum rows;
+  // otherwise the workgroups sharing a weight tile run on one XCD
+  int ct, rt;
+  if (p.nrt % 2 == 0 && p.nct % 4 == 0 && gridDim.x % 8 == 0) {
+    const int x = blockIdx.x & 7, s = blockIdx.x >> 3, hr = p.nrt / 2;
+    rt = (x >> 2) * hr + s % hr;
+    ct = (x & 3) * (p.nct / 4) + s / hr;
+  } else {
+    const int L = xcd_linear(blockIdx.x, gridDim.x);
+    ct = L / p.nrt;
+    rt = L - ct * p.nrt;
+  }
   const int b0 = rt * kInRows, c0 = ct * kInCh;
   const int B = p.B, dm = p.dm, Dm = p.Dm, P = p.P, ndu = p.ndu;
 
