@@ -263,6 +263,24 @@ def test_decode_stack_validation(field, value):
         _abi.check(_abi.lib().ssm_decode_stack_check(ctypes.byref(a)), "ssm_decode_stack")
 
 
+@pytest.mark.parametrize("shape", [dict(), dict(d_model=128, d_state=8), dict(d_model=512), dict(d_model=520),
+                                   dict(d_model=250), dict(d_state=12), dict(d_state=32), dict(d_conv=5),
+                                   dict(d_conv=1), dict(d_model=384), dict(d_model=256, expand=3)])
+def test_decoder_path_choice_agrees_with_the_library(shape):
+    """FastDecoder takes the stack path exactly for the shapes ssm_decode_stack_check accepts
+    (the Python limits and the C ones describe the same kernels)."""
+    from ssm_scan.block import MambaLM
+    from ssm_scan.decode import FastDecoder
+    model = MambaLM(n_layers=1, **shape)
+    m = model.blocks[0].mixer
+    a = _stack_args(n_blocks=1)
+    a.batch, a.dim, a.dstate, a.width, a.dt_rank = 8, m.d_inner, m.d_state, m.d_conv, m.dt_rank
+    a.d_model = model.blocks[0].norm1.weight.numel()
+    a.workspace_bytes = _abi.lib().ssm_decode_stack_workspace_bytes(ctypes.byref(a))
+    accepted = _abi.lib().ssm_decode_stack_check(ctypes.byref(a)) == 0
+    assert (FastDecoder(model).path == "stack") == accepted, (shape, _abi.lib().ssm_last_error())
+
+
 @pytest.mark.parametrize("change", ["tokens_without_embed", "head_without_logits", "no_vocab", "huge_vocab"])
 def test_decode_stack_ends_validation(change):
     """The optional ends of the token step: tokens need the embedding table, a head needs a
