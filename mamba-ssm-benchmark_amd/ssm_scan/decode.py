@@ -29,7 +29,7 @@ import ctypes
 import torch
 
 from . import _abi
-from .hip_scan import METHODS
+from .hip_scan import METHODS, _require_gpu
 
 
 STACK_LIMITS = dict(d_model=512, dim=1024, dstate=(8, 16), dt_rank=(8, 16, 32), width=4)
@@ -112,7 +112,7 @@ class FastDecoder:
         the head; returns the logits."""
         m = self.layers[0]["mixer"]
         B, dm, V = tok.numel(), self.model.head.weight.shape[1], self.model.head.weight.shape[0]
-        tok = tok.reshape(-1).to(torch.long)
+        tok = tok.reshape(-1).to(torch.long).contiguous()  # a strided view of ids is copied
         u = torch.empty(B, dm, dtype=torch.float32, device=tok.device)
         logits = torch.empty(B, V, dtype=torch.float32, device=tok.device)
         n = len(self.layers)
@@ -145,6 +145,28 @@ class FastDecoder:
         _abi.check(lib.ssm_decode_stack(ctypes.byref(a), _abi.stream_handle(u.device)), "ssm_decode_stack")
         return logits
 
+    def _check(self, tok, states):
+        """Host-side checks before any launch: the kernels size every state buffer from the
+        token count and the model's dimensions."""
+        dev = self.layers[0]["w_in"].device
+        _require_gpu(self.layers[0]["w_in"], tok, *[t for s in states for t in (s.conv, s.ssm)])
+        B = tok.numel()
+        if tok.device != dev:
+            raise ValueError(f"tokens on {tok.device}, the model on {dev}")
+        if len(states) != len(self.layers):
+            raise ValueError(f"{len(states)} states for {len(self.layers)} blocks")
+        for i, (L, s) in enumerate(zip(self.layers, states)):
+            m = L["mixer"]
+            want_ssm, want_conv = (B, m.d_inner, m.d_state), (B, m.d_inner, m.d_conv - 1)
+            if tuple(s.ssm.shape) != want_ssm or tuple(s.conv.shape) != want_conv:
+                raise ValueError(f"block {i}: states {tuple(s.ssm.shape)} / {tuple(s.conv.shape)}, expected "
+                                 f"{want_ssm} / {want_conv} for {B} tokens")
+            if s.ssm.device != dev or s.conv.device != dev:
+                raise ValueError(f"block {i}: states on {s.ssm.device} / {s.conv.device}, the model on {dev}")
+            if not (s.conv.is_contiguous() and s.ssm.is_contiguous() and s.ssm.dtype == torch.float32
+                    and s.conv.dtype in (torch.float32, torch.bfloat16)):
+                raise ValueError("decode states must be contiguous: ssm float32, conv float32 or bf16")
+
     @torch.no_grad()
     def step(self, tok, states):
         """tok (B,) or (B, 1) byte ids; states from model.init_state, contiguous, updated in
@@ -157,10 +179,7 @@ class FastDecoder:
         The decode GEMMs are skinny (B rows); they are issued through rocBLAS, whose kernels
         for these shapes take a fraction of hipBLASLt's (torch's default), and torch's choice
         is restored afterwards."""
-        for s in states:
-            if not (s.conv.is_contiguous() and s.ssm.is_contiguous() and s.ssm.dtype == torch.float32
-                    and s.conv.dtype in (torch.float32, torch.bfloat16)):
-                raise ValueError("decode states must be contiguous: ssm float32, conv float32 or bf16")
+        self._check(tok, states)
         prev = torch.backends.cuda.preferred_blas_library()
         torch.backends.cuda.preferred_blas_library("cublas")   # rocBLAS on ROCm
         try:

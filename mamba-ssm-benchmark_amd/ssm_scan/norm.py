@@ -86,6 +86,8 @@ def rms_norm(x, weight, eps=1e-5):
     """models/common.py:14-16.  The kernels run for float32 x and weight and a last dimension
     <= 1024; otherwise the reference's torch expression runs on the GPU."""
     _require_gpu(x, weight)
+    if tuple(weight.shape) != (x.shape[-1],):  # the kernels read dim weights
+        raise ValueError(f"weight must be ({x.shape[-1]},), got {tuple(weight.shape)}")
     if (x.dtype == torch.float32 and weight.dtype == torch.float32 and 0 < x.shape[-1] <= MAX_DIM
             and x.numel() > 0):
         return RMSNormFn.apply(x, weight, eps)

@@ -118,6 +118,7 @@ def discretize(delta, A, Bm, x, method="zoh"):
     if method not in DISCRETIZATIONS:
         raise ValueError(f"unknown discretization {method!r}")
     _require_gpu(delta, A, Bm, x)
+    _check_shapes(x, delta, A, Bm, Bm, None, None, None, None)  # the kernels index by (B, L, D, N)
     ct = _ct(delta, A, Bm, x)
     return DiscretizeFn.apply(delta.to(ct), A.to(ct), Bm.to(ct), x.to(ct), method)
 

@@ -27,6 +27,11 @@ def ssm_step(h, x, delta, A, Bm, Cm, D=None, z=None, delta_bias=None, delta_soft
     N = A.shape[1]
     if tuple(h.shape) != (Bsz, Dm, N):
         raise ValueError(f"h must be {(Bsz, Dm, N)}, got {tuple(h.shape)}")
+    # the kernel indexes every operand by (batch, dim, dstate): their shapes are checked here
+    want = dict(delta=(Bsz, Dm), A=(Dm, N), Bm=(Bsz, N), Cm=(Bsz, N), D=(Dm,), z=(Bsz, Dm), delta_bias=(Dm,))
+    for name, t in dict(delta=delta, A=A, Bm=Bm, Cm=Cm, D=D, z=z, delta_bias=delta_bias).items():
+        if t is not None and tuple(t.shape) != want[name]:
+            raise ValueError(f"{name} must be {want[name]}, got {tuple(t.shape)}")
     io = x.dtype if all(t is None or t.dtype == x.dtype for t in (delta, Bm, Cm, z)) else ct
     if io not in _abi.DTYPE_CODE:
         io = ct
