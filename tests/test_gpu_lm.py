@@ -347,6 +347,30 @@ def test_decode_stack_matches_float64_reference(dev, shape, batch):
     _decoder_vs_oracle(dev, shape, batch, "stack")
 
 
+def _random_stack_shapes(count, seed):
+    """Seeded shapes inside the stack kernels' limits: d_model a multiple of 4 whose dt_rank
+    (ceil(d_model / 16)) is 8, 16 or 32, expand 1 or 2, dstate 8 or 16, conv width 1-4, every
+    discretization, batch 1-70, 1-3 blocks."""
+    import random
+    rng = random.Random(seed)
+    out = []
+    for _ in range(count):
+        dm = rng.choice([116, 120, 124, 128, 244, 248, 252, 256, 500, 504, 508, 512])
+        expand = rng.choice([1, 2])
+        shape = dict(n_layers=rng.randint(1, 3), d_model=dm, expand=expand, d_state=rng.choice([8, 16]),
+                     d_conv=rng.randint(1, 4), discretization=rng.choice(["zoh", "euler", "bilinear"]))
+        out.append((shape, rng.randint(1, 70)))
+    return out
+
+
+@pytest.mark.parametrize("shape,batch", _random_stack_shapes(8, 2024),
+                         ids=lambda v: "-".join(f"{k}{x}" for k, x in v.items()) if isinstance(v, dict) else f"B{v}")
+def test_decode_stack_random_shapes_match_float64_reference(dev, shape, batch):
+    """The stack path on seeded random shapes within its limits, 3 tokens each, against the
+    float64 restatement at the same bar as the fixed shapes."""
+    _decoder_vs_oracle(dev, shape, batch, "stack", T=3)
+
+
 def test_decode_stack_token_outside_vocabulary_reads_zero_row(dev):
     """A token id outside [0, vocab) reads a zero embedding row in the stack path (the reference's
     embedding raises instead): the step equals the step of a model whose row 7 is zero, given
