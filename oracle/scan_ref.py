@@ -222,7 +222,7 @@ def selective_scan_fwd(x, delta, A, Bm, Cm, h0=None, method="zoh", D=None, z=Non
 
 
 def selective_scan_bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None, z=None,
-                       dlast=None):
+                       dlast=None, mag=False):
     """Hand-written adjoint of selective_scan_fwd.
 
     Recurrence and per-method derivatives follow kernels/triton_scan.py:171-226 (reverse
@@ -231,7 +231,10 @@ def selective_scan_bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None,
     over channels, dh0 = a_0 dh_0).  Gate/skip: out = (y + D x) s z, s = sigmoid(z):
     dy = dout s z, dz = dout (y + D x) s (1 + z (1 - s)), dD = sum dy x, dx += dy D.
 
-    Returns dict with dx, ddelta, dA, dB, dC and (when present) dD, dz, dh0."""
+    Returns dict with dx, ddelta, dA, dB, dC and (when present) dD, dz, dh0.  With mag, also
+    ddelta_mag and dA_mag: per element the sum of the magnitudes of the terms it adds (over the
+    states for ddelta, over batch and time for dA), the scale of the float32 rounding a kernel
+    summing those terms can leave in it."""
     x, delta, A, Bm, Cm, dout = (np.asarray(v, np.float64) for v in (x, delta, A, Bm, Cm, dout))
     Bsz, L, Dm = x.shape
     N = A.shape[1]
@@ -251,6 +254,7 @@ def selective_scan_bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None,
         dx = dx + dy * Dv
     ddelta = np.zeros_like(delta)
     dA = np.zeros_like(A)
+    ddelta_mag, dA_mag = np.zeros_like(delta), np.zeros_like(A)
     dB = np.zeros_like(Bm)
     dC = np.zeros_like(Cm)
     dh = np.zeros((Bsz, Dm, N)) if dlast is None else np.asarray(dlast, np.float64).copy()
@@ -276,28 +280,36 @@ def selective_scan_bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None,
             zs = np.where(small, 1.0, zt)
             f = np.where(small, 0.5 + zt / 3.0 + zt * zt / 8.0 + zt ** 3 / 30.0,
                          (zs * a - e) / (zs * zs))
-            ddelta[:, t] = np.sum(da * A * a + dh * a * Bx, axis=2)
-            dA += np.sum(da * dt * a + dh * dt * dt * f * Bx, axis=0)
+            td, tA = da * A * a + dh * a * Bx, da * dt * a + dh * dt * dt * f * Bx
+            ddelta[:, t] = np.sum(td, axis=2)
+            dA += np.sum(tA, axis=0)
             dB[:, t] = np.sum(dh * coef * xt, axis=1)
             dx[:, t] += np.sum(dh * coef * Bt, axis=2)
         elif method == "euler":
             a = np.exp(zt)
-            ddelta[:, t] = np.sum(da * A * a + dh * Bx, axis=2)
-            dA += np.sum(da * dt * a, axis=0)
+            td, tA = da * A * a + dh * Bx, da * dt * a
+            ddelta[:, t] = np.sum(td, axis=2)
+            dA += np.sum(tA, axis=0)
             dB[:, t] = np.sum(dh * dt * xt, axis=1)
             dx[:, t] += np.sum(dh * dt * Bt, axis=2)
         elif method == "bilinear":
             u = 1.0 / (1.0 - 0.5 * zt)
             a = (1.0 + 0.5 * zt) * u
             u2 = u * u
-            ddelta[:, t] = np.sum(da * A * u2 + dh * u2 * Bx, axis=2)
-            dA += np.sum(da * dt * u2 + dh * 0.5 * dt * dt * u2 * Bx, axis=0)
+            td, tA = da * A * u2 + dh * u2 * Bx, da * dt * u2 + dh * 0.5 * dt * dt * u2 * Bx
+            ddelta[:, t] = np.sum(td, axis=2)
+            dA += np.sum(tA, axis=0)
             dB[:, t] = np.sum(dh * dt * u * xt, axis=1)
             dx[:, t] += np.sum(dh * dt * u * Bt, axis=2)
         else:
             raise ValueError(f"unknown discretization {method!r}")
+        if mag:
+            ddelta_mag[:, t] = np.sum(np.abs(td), axis=2)
+            dA_mag += np.sum(np.abs(tA), axis=0)
         dh = dh * a
     g.update(dx=dx, ddelta=ddelta, dA=dA, dB=dB, dC=dC)
+    if mag:
+        g.update(ddelta_mag=ddelta_mag, dA_mag=dA_mag)
     if h0 is not None:
         g["dh0"] = dh
     return g

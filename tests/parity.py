@@ -32,3 +32,21 @@ def close(got, ref, rtol=RTOL, atol=ATOL, name="", allow=0):
     print(f"parity {name or 'tensor'}: {n} of {g.size} elements outside rtol {rtol:g} / atol {atol:g}", flush=True)
     if n > allow:
         np.testing.assert_allclose(g, r, rtol=rtol, atol=atol, err_msg=f"{name}: {n} outside (allowed {allow})")
+
+
+F32_TERMS = 2.0 ** -16   # float32 resolution of a sum of terms: a few ulps of their magnitudes
+
+
+def close_or_cancelled(got, ref, mag, name="", allow=0, rtol=RTOL, atol=ATOL):
+    """The bar for a gradient summed from float32 terms that can cancel (dA over batch and
+    time, ddelta over the states): an element outside the bar passes only when its error is
+    within float32 resolution of the sum of its terms' magnitudes `mag` (the oracle's), and at
+    most `allow` elements may sit outside the bar at all."""
+    g, r, m = _np(got), _np(ref), _np(mag)
+    err = np.abs(g - r)
+    bad = ~(err <= atol + rtol * np.abs(r))
+    worst = float((err[bad] / m[bad]).max()) if bad.any() else 0.0
+    print(f"parity {name or 'tensor'}: {int(bad.sum())} of {g.size} elements outside rtol {rtol:g} / "
+          f"atol {atol:g}; largest error / term magnitude among them {worst:.2e}", flush=True)
+    assert np.all(err[bad] <= F32_TERMS * m[bad]), f"{name}: an outlier exceeds float32 resolution of its terms"
+    assert bad.sum() <= allow, f"{name}: {int(bad.sum())} outside (allowed {allow})"

@@ -12,13 +12,13 @@ pass, carry over segment summaries, main pass) -- the structure of scan_chunked
   * forced segments with 16-bit inputs, and with a strided (non-uniform) layout.
 """
 
-import numpy as np
 import pytest
 import torch
 
 import ssm_scan
 from oracle import c_oracle
 from ssm_inputs import baseline_inputs, np64, triton_test_inputs
+from parity import close_or_cancelled
 from test_gpu_fused import ATOL, ATOL_BF16, RTOL, RTOL_BF16, check_all, close, oracle
 
 pytestmark = pytest.mark.gpu
@@ -110,14 +110,8 @@ def test_long_sequence_backward_matches_c_oracle(dev):
     # ddelta_t = sum over the 16 states of float32 terms that can cancel: an element may sit
     # outside the bar only where its error is within float32 resolution (2^-16, a few ulps of
     # each term) of the sum of the terms' magnitudes, and at most 1 ppm of elements may.
-    g, r, m = np64(grads["ddelta"]), rg["ddelta"], rg["ddelta_mag"]
-    err = np.abs(g - r)
-    bad = err > ATOL + RTOL * np.abs(r)
-    print(f"parity ddelta: {int(bad.sum())} of {bad.size} elements outside rtol {RTOL:g} / atol {ATOL:g}; "
-          f"largest error / term magnitude among them {float((err / m)[bad].max()) if bad.any() else 0.0:.2e}",
-          flush=True)
-    assert np.all(err[bad] <= 2.0 ** -16 * m[bad]), "an outlier exceeds float32 resolution of its terms"
-    assert bad.sum() <= bad.size // 1_000_000, int(bad.sum())
+    close_or_cancelled(grads["ddelta"], rg["ddelta"], rg["ddelta_mag"], "ddelta",
+                       allow=rg["ddelta"].size // 1_000_000)
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float16, 4e-3)])

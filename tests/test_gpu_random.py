@@ -55,7 +55,7 @@ def build(cfg, seed):
     return x, delta, A, proj, Dv, z, bias, h0, dout, dlast
 
 
-def oracle(x, delta, A, proj, Dv, z, bias, h0, dout, dlast, N, method, softplus):
+def oracle(x, delta, A, proj, Dv, z, bias, h0, dout, dlast, N, method, softplus, mag=False):
     x, delta, A, proj = np64(x), np64(delta), np64(A), np64(proj)
     Bm, Cm = proj[..., 3:3 + N], proj[..., 3 + N:]
     raw = delta + (np64(bias) if bias is not None else 0.0)
@@ -63,9 +63,11 @@ def oracle(x, delta, A, proj, Dv, z, bias, h0, dout, dlast, N, method, softplus)
     D_, z_, h0_ = (None if t is None else np64(t) for t in (Dv, z, h0))
     out, _, last = R.selective_scan_fwd(x, d_eff, A, Bm, Cm, h0_, method, D_, z_)
     gr = R.selective_scan_bwd(x, d_eff, A, Bm, Cm, np64(dout), h0_, method, D_, z_,
-                              None if dlast is None else np64(dlast))
+                              None if dlast is None else np64(dlast), mag=mag)
     if softplus:
         gr["ddelta"] = gr["ddelta"] / (1.0 + np.exp(-raw))
+        if mag:
+            gr["ddelta_mag"] = gr["ddelta_mag"] / (1.0 + np.exp(-raw))
     if bias is not None:
         gr["ddelta_bias"] = gr["ddelta"].sum(axis=(0, 1))
     return out, last, gr
@@ -73,6 +75,24 @@ def oracle(x, delta, A, proj, Dv, z, bias, h0, dout, dlast, N, method, softplus)
 
 @pytest.mark.parametrize("seed", range(24))
 def test_random_configuration_matches_oracle(dev, seed):
+    run_case(dev, seed)
+
+
+# Seeds of a 400-configuration sweep of draw() where one or two elements of dA
+# (summed over batch and time) or of ddelta (summed over the states) sit outside the bar:
+# small values left by terms whose magnitudes add up to 24-304, an error of 0.2-1.6e-6 of
+# that magnitude.  Every other gradient element of these cases is held to the bar.
+CANCELLING_SEEDS = (74, 82, 159, 208, 218, 229, 249, 360, 370, 419)
+
+
+@pytest.mark.parametrize("seed", CANCELLING_SEEDS)
+def test_random_configuration_cancellation_within_float32_resolution(dev, seed):
+    """dA and ddelta elements outside the bar are within float32 resolution (2^-16) of the sum
+    of their terms' magnitudes, at most 2 per tensor; all else at the bar."""
+    run_case(dev, seed, cancel_allow=2)
+
+
+def run_case(dev, seed, cancel_allow=None):
     cfg = draw(seed)
     print(f"case seed={seed} {cfg}", flush=True)
     x, delta, A, proj, Dv, z, bias, h0, dout, dlast = build(cfg, 1000 + seed)
@@ -99,12 +119,17 @@ def test_random_configuration_matches_oracle(dev, seed):
     if dlast is not None:
         loss = loss + (last * dlast.to(dev)).sum()
     loss.backward()
-    rout, rlast, rg = oracle(x, delta, A, proj, Dv, z, bias, h0, dout, dlast, N, cfg["method"], cfg["softplus"])
+    rout, rlast, rg = oracle(x, delta, A, proj, Dv, z, bias, h0, dout, dlast, N, cfg["method"], cfg["softplus"],
+                             mag=cancel_allow is not None)
     close(out, rout, "out")
     close(last, rlast, "last")
     close(xg.grad, rg["dx"], "dx")
-    close(dg.grad, rg["ddelta"], "ddelta")
-    close(Ag.grad, rg["dA"], "dA")
+    if cancel_allow is None:
+        close(dg.grad, rg["ddelta"], "ddelta")
+        close(Ag.grad, rg["dA"], "dA")
+    else:
+        parity.close_or_cancelled(dg.grad, rg["ddelta"], rg["ddelta_mag"], "ddelta", allow=cancel_allow)
+        parity.close_or_cancelled(Ag.grad, rg["dA"], rg["dA_mag"], "dA", allow=cancel_allow)
     close(pg.grad[..., 3:3 + N], rg["dB"], "dB")
     close(pg.grad[..., 3 + N:], rg["dC"], "dC")
     assert float(pg.grad[..., :3].abs().max()) == 0.0

@@ -326,6 +326,32 @@ def test_c_oracle_matches_numpy_oracle(method, h0, gate):
         np.testing.assert_allclose(g2[k], g1[k], rtol=1e-11, atol=1e-12, err_msg=k)
 
 
+@pytest.mark.parametrize("method", R.DISCRETIZATIONS)
+def test_term_magnitudes_bound_values_and_add_over_rows(method):
+    """The term magnitudes that scale the float32 cancellation bound of the GPU tests:
+    ddelta_mag equals the C oracle's (its own scalar loop), every magnitude bounds its value,
+    an element of one term has magnitude |value|, and dA_mag adds over batch rows (so it is a
+    sum of |terms|, not |sum|)."""
+    ins = sel_inputs(B=3, L=40, D=7, N=6, seed=23, h0=True, gate=True)
+    g = np.random.default_rng(24)
+    dout, dl = g.standard_normal(ins[0].shape), g.standard_normal((3, 7, 6))
+    gm = R.selective_scan_bwd(*ins[:5], dout, ins[5], method, ins[6], ins[7], dl, mag=True)
+    gc = c_oracle.bwd(*ins[:5], dout, ins[5], method, ins[6], ins[7], dl, mag=True)
+    np.testing.assert_allclose(gm["ddelta_mag"], gc["ddelta_mag"], rtol=1e-11, atol=1e-12)
+    for k in ("ddelta", "dA"):
+        assert np.all(gm[k + "_mag"] >= np.abs(gm[k]) * (1 - 1e-12)), k
+        assert np.any(gm[k + "_mag"] > 1.5 * np.abs(gm[k])), k   # terms do cancel here
+    x, delta, A, Bm, Cm, hz, Dv, z = ins
+    rows = [R.selective_scan_bwd(x[b:b + 1], delta[b:b + 1], A, Bm[b:b + 1], Cm[b:b + 1], dout[b:b + 1],
+                                 hz[b:b + 1], method, Dv, z[b:b + 1], dl[b:b + 1], mag=True) for b in range(3)]
+    np.testing.assert_allclose(sum(r["dA_mag"] for r in rows), gm["dA_mag"], rtol=1e-12)
+    one = sel_inputs(B=1, L=1, D=5, N=1, seed=25, h0=True, gate=False)
+    g1 = R.selective_scan_bwd(*one[:5], g.standard_normal((1, 1, 5)), one[5], method, one[6], one[7],
+                              g.standard_normal((1, 5, 1)), mag=True)
+    for k in ("ddelta", "dA"):
+        np.testing.assert_allclose(g1[k + "_mag"], np.abs(g1[k]), rtol=1e-14, err_msg=k)
+
+
 # --------------------------------------------------------------------------- scan / discretize VJPs
 
 @pytest.mark.parametrize("with_h0", [False, True])
