@@ -134,6 +134,26 @@ def test_config1_fwd_bwd_matches_c_oracle(dev):
     check_all(got, ref)   # every element of every tensor within the bar (no exception at c1)
 
 
+@pytest.mark.parametrize("D", [1536, 5120])
+def test_wide_model_matches_oracle(dev, D):
+    """The channel widths of the larger Mamba models (d_inner 1536 and 5120): 48 / 160 channel
+    tiles whose dB / dC partials the finalize sums; gate, D skip, dt bias + softplus, h0 and
+    dlast.  Every element of every output and gradient against the float64 oracle at the bar."""
+    B, L, N = 2, 160, 16
+    print(f"case B{B} L{L} D{D} N{N}", flush=True)
+    g = torch.Generator().manual_seed(D)
+    x = torch.randn(B, L, D, generator=g)
+    delta = torch.randn(B, L, D, generator=g) * 0.5 - 1.0
+    bias = torch.randn(D, generator=g) * 0.5 - 2.0
+    A = -(torch.rand(D, N, generator=g) * 4 + 0.05)
+    Bm, Cm = torch.randn(B, L, N, generator=g), torch.randn(B, L, N, generator=g)
+    h0, Dv, z = torch.randn(B, D, N, generator=g), torch.randn(D, generator=g), torch.randn(B, L, D, generator=g)
+    dout, dlast = torch.randn(B, L, D, generator=g), torch.randn(B, D, N, generator=g)
+    ins = (x, delta, A, Bm, Cm, h0)
+    got = run_fused(ins, dev, "zoh", D=Dv, z=z, bias=bias, softplus=True, dout=dout, dlast=dlast)
+    check_all(got, oracle(ins, "zoh", D=Dv, z=z, bias=bias, softplus=True, dout=dout, dlast=dlast))
+
+
 def test_backward_is_bitwise_deterministic(dev):
     """tests/test_gpu.py:28-46: two backward passes are torch.equal (always, not only in
     torch's deterministic mode: every reduction here is fixed-order)."""
