@@ -419,7 +419,7 @@ def bench_decode(args, dev):
     is the faster of the two.  Beside it: the per-block path (in_proj GEMM, the fused
     ssm_decode_step launch, out_proj + residual GEMM per block), and the module decode path
     (models/mamba.py's structure: conv step and scan step kernels between torch ops), eager and
-    graph-replayed."""
+    graph-replayed; `--decode-path stack` times the token step alone."""
     from ssm_scan.block import MambaLM
     from ssm_scan.decode import FastDecoder
     torch.manual_seed(0)
@@ -478,13 +478,17 @@ def bench_decode(args, dev):
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) * 1e3 / args.decode_steps
 
-    eager_ms = eager_time(module_step)
-    module_graph_ms = graph_time(module_step)
+    eager_ms = module_graph_ms = block_ms = None
+    every_path = args.decode_path == "all"   # "stack": the token step alone (profiling runs)
+    if every_path:
+        eager_ms = eager_time(module_step)
+        module_graph_ms = None if args.eager else graph_time(module_step)
     fast_eager_ms = eager_time(fast_step)
-    block_ms = graph_time(block_step)
-    fast_graph_ms = graph_time(fast_step)
-    ms = min(fast_eager_ms, fast_graph_ms)   # the faster way of issuing the same token step
-    timing = "graph" if fast_graph_ms <= fast_eager_ms else "eager"
+    if every_path and not args.eager:
+        block_ms = graph_time(block_step)
+    fast_graph_ms = None if args.eager else graph_time(fast_step)
+    ms = min(fast_eager_ms, fast_graph_ms or fast_eager_ms)   # the faster way of issuing the same token step
+    timing = "graph" if fast_graph_ms is not None and fast_graph_ms <= fast_eager_ms else "eager"
     rec_cpu = None if args.no_cpu_baseline else cpu_baseline_decode(model, B)
     return {"metric": "Mamba LM decode latency per token per layer, batch 64 (10 layers)", "value": ms * 1e3 / 10,
             "unit": "us/layer", "n_gpus": 1, "steps": args.decode_steps, "warmup": 20, "ms_per_step": ms,
@@ -733,6 +737,7 @@ def c1_extras(args, dev):
                              "cpu_baseline_cores": cb.get("cores"), "cpu_baseline_kind": cb.get("kind"),
                              "gpu_time_frac_of_cpu": c2.get("gpu_time_frac_of_cpu"), "target_frac": 0.02}
     torch.cuda.empty_cache()
+    sub.decode_path = "stack"   # only the token step's time is reported here
     c4 = bench_decode(sub, dev)
     out["c4_decode_us_per_layer"] = c4["value"]
     out["c4_decode"] = {"us_per_layer": c4["value"], "ms_per_token_model": c4["ms_per_token_model"],
@@ -755,6 +760,8 @@ def main():
     ap.add_argument("--workload", default="c1", choices=["c1", "c0", "c2", "c2bf16", "c3", "c4", "long", "refdecode",
                                                                  "scans", "copy"])
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--decode-path", default="all", choices=["all", "stack"],
+                    help="c4: time every decode path, or only the token step FastDecoder runs")
     ap.add_argument("--seqlen", type=int, default=131072)
     ap.add_argument("--lengths", default="4096,16384,65536", help="long: the sequence lengths")
     ap.add_argument("--segments", type=int, default=0, help="forward time segments (0 = automatic)")
