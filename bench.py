@@ -752,7 +752,7 @@ def c1_extras(args, dev):
     return out
 
 
-def main():
+def parser():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -769,7 +769,11 @@ def main():
     ap.add_argument("--eager", action="store_true", help="report the eager step (no HIP-graph replay)")
     ap.add_argument("--no-extras", action="store_true",
                     help="c1 only: skip the c2 / c4 / long-sequence keys appended to the line")
-    args = ap.parse_args()
+    return ap
+
+
+def main():
+    args = parser().parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): the hot path here is the "
               "single-GPU scan kernel; it is not sharded across GPUs in this build.", file=sys.stderr)

@@ -3,7 +3,6 @@ the fields of the driver's contract (metric, value, unit, step counts, dtype, co
 config 1, a `roofline` whose achieved bandwidth is the algorithmic bytes over the measured
 kernel time; config 4's decode is timed and its graph replay matches its eager step."""
 
-import argparse
 import json
 import math
 import os
@@ -23,10 +22,12 @@ CONTRACT = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step
 
 
 def args(**kw):
-    base = dict(gpus=1, steps=3, warmup=1, workload="c1", decode_steps=8, seqlen=4096, segments=0,
-                no_cpu_baseline=True, eager=False)
+    ns = bench.parser().parse_args([])   # bench.py's own defaults, then the small test sizes
+    base = dict(steps=3, warmup=1, decode_steps=8, seqlen=4096, no_cpu_baseline=True)
     base.update(kw)
-    return argparse.Namespace(**base)
+    for k, v in base.items():
+        setattr(ns, k, v)
+    return ns
 
 
 def check_line(rec):
