@@ -23,10 +23,15 @@ How each function is pinned (tests/test_oracle_*.py):
                       sequential loop incl. ragged chunks and extreme decays.
   selective_scan_fwd  scalar brute-force loop with math.exp/expm1; torch fp64.
   selective_scan_bwd  torch.autograd (fp64) through an independent textbook loop;
-                      central finite differences on tiny shapes.
+                      central finite differences on tiny shapes.  Its optional term
+                      magnitudes (mag=True) equal the C oracle's for ddelta, bound
+                      their values, equal |value| for one-term elements and add over
+                      batch rows.
   ssm_step            decode step == one column of the full forward.
   conv1d_causal       torch.nn.functional.conv1d (fp64).
   plan functions      closed forms over exhaustive integer ranges; committed table.
   C oracle            equals the numpy oracle to 1e-12.
+  all of the above    reproduce the committed vectors (tests/golden/vectors.npz) from
+                      their stored inputs.
 No function of the oracle is left "parity unpinned".
 """
