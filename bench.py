@@ -120,12 +120,30 @@ def cpu_baseline_fwd(L, budget_s=20.0, label="config-2"):
                       f"independent channel tiles timed ({dt:.2f} s each), scaled to all tiles"}
 
 
+def _read_first(paths, pick):
+    for path in paths:
+        try:
+            with open(path) as f:
+                v = pick(f.read())
+            if v:
+                return v
+        except OSError:
+            continue
+    return None
+
+
 def env_record(dev):
-    """The environment the line was measured in: torch/HIP versions, the GPU and the host."""
+    """The environment the line was measured in: torch/HIP versions, the GPU, its engine-clock
+    levels (sysfs pp_dpm_sclk, the current one marked *) and the host CPU model."""
+    import glob
     props = torch.cuda.get_device_properties(dev)
+    cpu = _read_first(["/proc/cpuinfo"], lambda t: next((ln.split(":", 1)[1].strip() for ln in t.splitlines()
+                                                          if ln.startswith("model name")), None))
+    sclk = _read_first(sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")),
+                       lambda t: " | ".join(ln.strip() for ln in t.splitlines() if ln.strip()))
     return {"torch": torch.__version__, "hip": torch.version.hip, "gpu": props.name,
             "arch": getattr(props, "gcnArchName", None), "compute_units": props.multi_processor_count,
-            "host_cpus": os.cpu_count()}
+            "sclk_levels": sclk, "host_cpus": os.cpu_count(), "host_cpu_model": cpu}
 
 
 def time_stats(samples):
