@@ -154,6 +154,23 @@ def test_wide_model_matches_oracle(dev, D):
     check_all(got, oracle(ins, "zoh", D=Dv, z=z, bias=bias, softplus=True, dout=dout, dlast=dlast))
 
 
+@pytest.mark.parametrize("B", [300, 65535])
+def test_large_batch_matches_oracle(dev, B):
+    """Batch rows up to the grid's y limit (65535): one workgroup row per batch row, and the
+    finalize summing dA, dD and d_bias over every row in order.  Short rows (L 3, D 8, N 4),
+    gate, D skip, bias + softplus, h0 and dlast; every output and gradient at the bar."""
+    L, D, N = 3, 8, 4
+    print(f"case B{B} L{L} D{D} N{N}", flush=True)
+    g = torch.Generator().manual_seed(B)
+    ins = (torch.randn(B, L, D, generator=g), torch.randn(B, L, D, generator=g) * 0.5 - 1.0,
+           -(torch.rand(D, N, generator=g) * 4 + 0.05), torch.randn(B, L, N, generator=g),
+           torch.randn(B, L, N, generator=g), torch.randn(B, D, N, generator=g))
+    Dv, z, bias = torch.randn(D, generator=g), torch.randn(B, L, D, generator=g), torch.randn(D, generator=g) * 0.5
+    dout, dlast = torch.randn(B, L, D, generator=g), torch.randn(B, D, N, generator=g)
+    got = run_fused(ins, dev, "zoh", D=Dv, z=z, bias=bias, softplus=True, dout=dout, dlast=dlast)
+    check_all(got, oracle(ins, "zoh", D=Dv, z=z, bias=bias, softplus=True, dout=dout, dlast=dlast))
+
+
 def test_backward_is_bitwise_deterministic(dev):
     """tests/test_gpu.py:28-46: two backward passes are torch.equal (always, not only in
     torch's deterministic mode: every reduction here is fixed-order)."""
