@@ -371,6 +371,13 @@ def test_decode_stack_random_shapes_match_float64_reference(dev, shape, batch):
     _decoder_vs_oracle(dev, shape, batch, "stack", T=3)
 
 
+@pytest.mark.parametrize("path", ["stack", "block"])
+def test_decoders_at_a_large_batch_match_float64_reference(dev, path):
+    """Both decode paths at batch 1000 (250 row tiles of the stack kernels, 1000 workgroups of
+    the per-block kernel), 2 tokens, against the float64 restatement at the same bar."""
+    _decoder_vs_oracle(dev, dict(n_layers=2), 1000, path, T=2)
+
+
 def test_decode_stack_token_outside_vocabulary_reads_zero_row(dev):
     """A token id outside [0, vocab) reads a zero embedding row in the stack path (the reference's
     embedding raises instead): the step equals the step of a model whose row 7 is zero, given
