@@ -171,6 +171,26 @@ def test_large_batch_matches_oracle(dev, B):
     check_all(got, oracle(ins, "zoh", D=Dv, z=z, bias=bias, softplus=True, dout=dout, dlast=dlast))
 
 
+@pytest.mark.parametrize("method", ["zoh", "euler", "bilinear"])
+def test_gradcheck_float64(dev, method):
+    """tests/test_scan.py:85-88 on the engine: torch.autograd.gradcheck (central differences in
+    float64 against the float64 kernels' backward) at B1 L6 D2 N3, with the gate, D skip, dt
+    bias + softplus and h0, for the output and the last state."""
+    g = torch.Generator().manual_seed(7)
+    B, L, D, N = 1, 6, 2, 3
+    mk = lambda *s: torch.randn(*s, generator=g, dtype=torch.float64).to(dev).requires_grad_()
+    x, delta, Bm, Cm, z, h0 = mk(B, L, D), mk(B, L, D), mk(B, L, N), mk(B, L, N), mk(B, L, D), mk(B, D, N)
+    A = (-(torch.rand(D, N, generator=g, dtype=torch.float64) * 2 + 0.1)).to(dev).requires_grad_()
+    Dv, bias = mk(D), mk(D)
+
+    def fn(x, delta, A, Bm, Cm, Dv, z, bias, h0):
+        return ssm_scan.selective_scan_fn(x, delta, A, Bm, Cm, D=Dv, z=z, delta_bias=bias, delta_softplus=True,
+                                          h0=h0, method=method, return_last_state=True)
+
+    assert torch.autograd.gradcheck(fn, (x, delta, A, Bm, Cm, Dv, z, bias, h0), eps=1e-6, atol=1e-6, rtol=1e-4,
+                                    nondet_tol=0.0)
+
+
 def test_backward_is_bitwise_deterministic(dev):
     """tests/test_gpu.py:28-46: two backward passes are torch.equal (always, not only in
     torch's deterministic mode: every reduction here is fixed-order)."""

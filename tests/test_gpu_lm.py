@@ -231,6 +231,40 @@ def test_named_scan_algorithm_matches_fused(dev, scan):
         np.testing.assert_allclose(np64(outs[1][1][k]), np64(g0), rtol=1e-3, atol=1e-4 * gs, err_msg=k)
 
 
+def test_lm_is_causal(dev):
+    """tests/test_models.py:26-34: logits before position 25 do not change when later tokens do
+    (bitwise here: every kernel on the path computes a position from earlier positions only),
+    and logits from position 25 on do change."""
+    torch.manual_seed(0)
+    model = MambaLM(n_layers=2).to(dev).eval()
+    g = torch.Generator().manual_seed(5)
+    x = torch.randint(0, 256, (2, 40), generator=g)
+    x2 = x.clone()
+    x2[:, 25:] = torch.randint(0, 256, (2, 15), generator=g)
+    with torch.no_grad():
+        y, y2 = model(x.to(dev)), model(x2.to(dev))
+    assert torch.equal(y[:, :25], y2[:, :25])
+    assert not torch.allclose(y[:, 25:], y2[:, 25:])
+
+
+def test_lm_can_overfit_a_batch(dev):
+    """tests/test_models.py:96-110: 150 AdamW steps (lr 1e-2) on one batch of 4 x 33 random
+    bytes take the cross-entropy from above 5 to below 0.5, every gradient from the engine."""
+    torch.manual_seed(0)
+    model = MambaLM(n_layers=2, d_model=64).to(dev)
+    x = torch.randint(0, 256, (4, 33), generator=torch.Generator().manual_seed(0)).to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-2)
+    for step in range(150):
+        loss = torch.nn.functional.cross_entropy(model(x[:, :-1]).reshape(-1, 256), x[:, 1:].reshape(-1))
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+        if step == 0:
+            first = loss.item()
+    print(f"loss {first:.3f} -> {loss.item():.4f}", flush=True)
+    assert first > 5.0 and loss.item() < 0.5, (first, loss.item())
+
+
 def test_lti_ablation_has_constant_delta(dev):
     """selective=False freezes delta to a learned constant (tests/test_models.py:60-64)."""
     torch.manual_seed(18)
