@@ -346,8 +346,23 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   float h = 0.0f, prod = 1.0f;
   const int64_t sidx = ((b * p.nseg + seg) * p.D + d) * NP + n;  // (B, nseg, D, NP) summaries
   if (!SUM && dval && nval) {
-    if (p.nseg > 1) h = ((const float *)p.seg_hin)[sidx];
-    else if (p.has_h0) h = vload<float>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
+    if (p.nseg > kFoldSegs) {
+      h = ((const float *)p.seg_hin)[sidx];
+    } else {
+      // the state entering the segment, folded from the earlier segments' summaries with
+      // k_fwd_carry's arithmetic (h <- P h + E); their reads are issued together
+      float Pv[kFoldSegs - 1], Ev[kFoldSegs - 1];
+#pragma unroll
+      for (int s = 0; s < kFoldSegs - 1; ++s) {
+        const int64_t k = ((b * p.nseg + s) * p.D + d) * NP + n;
+        Pv[s] = s < seg ? ((const float *)p.seg_P)[k] : 0.0f;
+        Ev[s] = s < seg ? ((const float *)p.seg_E)[k] : 0.0f;
+      }
+      if (p.has_h0) h = vload<float>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
+#pragma unroll
+      for (int s = 0; s < kFoldSegs - 1; ++s)
+        if (s < seg) h = fmaf(Pv[s], h, Ev[s]);
+    }
   }
   const float biasv = p.has_bias && tval ? vload<float>(p.bias, (int64_t)(dw + tc) * p.bias.s0) : 0.0f;
   const float dskv = p.has_D && tval ? vload<float>(p.Dsk, (int64_t)(dw + tc) * p.Dsk.s0) : 0.0f;
@@ -555,9 +570,11 @@ static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
   dim3 grid((unsigned)((p.D + DT - 1) / DT), (unsigned)(p.B * p.nseg));
   if (p.nseg > 1) {
     fwd_pass<IT, NP, M, true, LR>(p, grid, dim3(WPB * kWave), s);
-    const int64_t lanes = p.B * p.D * NP;
-    hipLaunchKernelGGL((k_fwd_carry<CT, NP>), dim3((unsigned)((lanes + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                       s, p);
+    if (sizeof(IT) == 8 || p.nseg > kFoldSegs) {  // else the float main pass folds the summaries
+      const int64_t lanes = p.B * p.D * NP;
+      hipLaunchKernelGGL((k_fwd_carry<CT, NP>), dim3((unsigned)((lanes + kThreads - 1) / kThreads)), dim3(kThreads),
+                         0, s, p);
+    }
   }
   fwd_pass<IT, NP, M, false, LR>(p, grid, dim3(WPB * kWave), s);
   return hipGetLastError();

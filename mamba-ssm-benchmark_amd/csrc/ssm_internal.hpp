@@ -16,6 +16,7 @@ struct KView {
 // are staged per chunk, and the state at the end of every chunk is what the forward saves for
 // the backward.  Waves per workgroup are chosen so the per-wave LDS regions fit in 64 KiB.
 constexpr int kCK = 16;
+constexpr int kFoldSegs = 8;  // time segments the forward's main pass folds without a carry pass
 constexpr int kThreads = 256;  // threads per workgroup of the simple (non-scan) kernels
 inline int chunk_steps(int) { return kCK; }
 inline int padded_n(int64_t n) { return n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32 : 64; }
@@ -75,7 +76,9 @@ struct FwdParams {
   // Time segments: grid row blockIdx.y = b * nseg + segment; a segment spans seg_chunks chunks.
   // With nseg > 1 a summary pass writes each segment's decay product and zero-start end state
   // (seg_P, seg_E), a carry pass turns them into the state entering each segment (seg_hin),
-  // and the main pass starts every segment from seg_hin.  All three are (B, nseg, D, NP).
+  // and the main pass starts every segment from seg_hin.  All three are (B, nseg, D, NP).  With
+  // at most kFoldSegs segments the float kernels' main pass folds seg_P / seg_E itself and no
+  // carry pass runs.
   int nseg, seg_chunks;
   void *seg_P, *seg_E, *seg_hin;
   KView x, dt, A, Bm, Cm, Dsk, z, bias, h0, out, last;
