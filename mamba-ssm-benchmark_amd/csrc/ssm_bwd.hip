@@ -962,10 +962,24 @@ __global__ void __launch_bounds__(kThreads) k_bwd_carry(const BwdParams p) {
   const int64_t d = (i / NP) % p.D, b = i / (NP * p.D);
   if (n >= p.N) return;
   double mu = p.has_dlast ? (double)vload<float>(p.dlast, b * p.dlast.s0 + d * p.dlast.s1 + n * p.dlast.s2) : 0.0;
-  for (int s = p.nseg - 1; s >= 0; --s) {
-    const int64_t k = ((b * p.nseg + s) * p.D + d) * NP + n;
-    ((double *)p.seg_mu)[k] = mu;
-    if (s > 0) mu = ((const double *)p.seg_E)[k] + (double)((const float *)p.seg_P)[k] * mu;
+  // the summaries of kCarryGroup segments are read together, then folded in order
+  for (int s1 = p.nseg - 1; s1 >= 0; s1 -= kCarryGroup) {
+    double Ev[kCarryGroup];
+    float Pv[kCarryGroup];
+#pragma unroll
+    for (int j = 0; j < kCarryGroup; ++j) {  // unconditional reads (a clamped segment is never used)
+      const int64_t k = ((b * p.nseg + max(s1 - j, 0)) * p.D + d) * NP + n;
+      Ev[j] = ((const double *)p.seg_E)[k];
+      Pv[j] = ((const float *)p.seg_P)[k];
+    }
+#pragma unroll
+    for (int j = 0; j < kCarryGroup; ++j) {
+      const int s = s1 - j;
+      if (s >= 0) {
+        ((double *)p.seg_mu)[((b * p.nseg + s) * p.D + d) * NP + n] = mu;
+        if (s > 0) mu = Ev[j] + (double)Pv[j] * mu;
+      }
+    }
   }
 }
 

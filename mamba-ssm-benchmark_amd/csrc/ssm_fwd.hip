@@ -265,7 +265,9 @@ k_fwd(const FwdParams p) {
 }
 
 // State entering each time segment: h_in[0] = h0 (or 0), h_in[s+1] = P[s] h_in[s] + E[s],
-// one lane per (b, d, n), segments in order (models/scan.py:160-164 over segments).
+// one lane per (b, d, n), segments in order (models/scan.py:160-164 over segments).  The
+// summaries of kCarryGroup segments are read together, then folded in order, so the serial
+// chain waits for memory once per group instead of once per segment.
 template <typename CT, int NP>
 __global__ void __launch_bounds__(kThreads) k_fwd_carry(const FwdParams p) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
@@ -274,10 +276,21 @@ __global__ void __launch_bounds__(kThreads) k_fwd_carry(const FwdParams p) {
   const int64_t d = (i / NP) % p.D, b = i / (NP * p.D);
   if (n >= p.N) return;
   CT h = p.has_h0 ? vload<CT>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2) : (CT)0;
-  for (int s = 0; s < p.nseg; ++s) {
-    const int64_t k = ((b * p.nseg + s) * p.D + d) * NP + n;
-    ((CT *)p.seg_hin)[k] = h;
-    h = fma(((const CT *)p.seg_P)[k], h, ((const CT *)p.seg_E)[k]);
+  for (int s0 = 0; s0 < p.nseg; s0 += kCarryGroup) {
+    CT Pv[kCarryGroup], Ev[kCarryGroup];
+#pragma unroll
+    for (int j = 0; j < kCarryGroup; ++j) {  // unconditional reads (a clamped segment is never used)
+      const int64_t k = ((b * p.nseg + min(s0 + j, p.nseg - 1)) * p.D + d) * NP + n;
+      Pv[j] = ((const CT *)p.seg_P)[k];
+      Ev[j] = ((const CT *)p.seg_E)[k];
+    }
+#pragma unroll
+    for (int j = 0; j < kCarryGroup; ++j) {
+      if (s0 + j < p.nseg) {
+        ((CT *)p.seg_hin)[((b * p.nseg + s0 + j) * p.D + d) * NP + n] = h;
+        h = fma(Pv[j], h, Ev[j]);
+      }
+    }
   }
 }
 

@@ -16,7 +16,8 @@ struct KView {
 // are staged per chunk, and the state at the end of every chunk is what the forward saves for
 // the backward.  Waves per workgroup are chosen so the per-wave LDS regions fit in 64 KiB.
 constexpr int kCK = 16;
-constexpr int kFoldSegs = 8;  // time segments the forward's main pass folds without a carry pass
+constexpr int kFoldSegs = 8;     // time segments the forward's main pass folds without a carry pass
+constexpr int kCarryGroup = 16;  // segment summaries a carry kernel reads before folding them
 constexpr int kThreads = 256;  // threads per workgroup of the simple (non-scan) kernels
 inline int chunk_steps(int) { return kCK; }
 inline int padded_n(int64_t n) { return n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32 : 64; }
