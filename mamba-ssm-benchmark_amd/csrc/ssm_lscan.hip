@@ -361,10 +361,23 @@ __global__ void __launch_bounds__(256) k_lscan_chunk_carry(const LscanParams P) 
   CT *ws = (CT *)P.ws;
   const int64_t stride = P.B * P.nc * P.M;
   CT hin = ch.h0();
-  for (int cj = 0; cj < P.nc; ++cj) {
-    const int64_t k = (b * P.nc + cj) * P.M + m;
-    ws[2 * stride + k] = hin;  // state entering chunk cj
-    hin = fma(ws[k], hin, ws[stride + k]);
+  // the summaries of kCarryGroup chunks are read together (unconditionally: a clamped chunk is
+  // never used), then folded in order
+  for (int c0 = 0; c0 < P.nc; c0 += kCarryGroup) {
+    CT Pv[kCarryGroup], Ev[kCarryGroup];
+#pragma unroll
+    for (int j = 0; j < kCarryGroup; ++j) {
+      const int64_t k = (b * P.nc + min((int64_t)(c0 + j), P.nc - 1)) * P.M + m;
+      Pv[j] = ws[k];
+      Ev[j] = ws[stride + k];
+    }
+#pragma unroll
+    for (int j = 0; j < kCarryGroup; ++j) {
+      if (c0 + j < P.nc) {
+        ws[2 * stride + (b * P.nc + c0 + j) * P.M + m] = hin;  // state entering chunk c0 + j
+        hin = fma(Pv[j], hin, Ev[j]);
+      }
+    }
   }
 }
 
