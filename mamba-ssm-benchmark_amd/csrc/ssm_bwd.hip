@@ -460,17 +460,7 @@ constexpr int kFinGroup = 4;
 
 template <typename CT>
 __device__ inline CT fin_sum(const CT *src, int64_t stride, int64_t count) {
-  CT s = 0;
-  int64_t k = 0;
-  for (; k + kFinGroup <= count; k += kFinGroup) {
-    CT v[kFinGroup];
-#pragma unroll
-    for (int u = 0; u < kFinGroup; ++u) v[u] = src[(k + u) * stride];
-#pragma unroll
-    for (int u = 0; u < kFinGroup; ++u) s += v[u];
-  }
-  for (; k < count; ++k) s += src[k * stride];
-  return s;
+  return ordered_sum<kFinGroup>(src, stride, count);
 }
 
 __device__ inline float4 fin_sum4(const float4 *src, int64_t stride, int count) {

@@ -175,15 +175,11 @@ __global__ void __launch_bounds__(kThreads) k_disc_fin(const DiscParams p) {
   const int64_t nB = p.B * p.L * p.N, nA = p.D * p.N;
   if (i < nB) {
     const int64_t n = i % p.N, r = i / p.N, b = r / p.L, t = r % p.L;
-    const CT *w = (const CT *)p.ws_dB + r * p.dtiles * p.N + n;
-    CT s = 0;
-    for (int64_t k = 0; k < p.dtiles; ++k) s += w[k * p.N];
+    const CT s = ordered_sum<16>((const CT *)p.ws_dB + r * p.dtiles * p.N + n, p.N, p.dtiles);
     vstore<CT>(p.dBm, b * p.dBm.s0 + t * p.dBm.s1 + n * p.dBm.s2, s);
   } else if (i < nB + nA) {
     const int64_t j = i - nB, n = j % p.N, d = j / p.N;
-    const CT *w = (const CT *)p.ws_dA + j;
-    CT s = 0;
-    for (int64_t k = 0; k < p.ngroups; ++k) s += w[k * nA];
+    const CT s = ordered_sum<16>((const CT *)p.ws_dA + j, nA, p.ngroups);
     vstore<CT>(p.dA, d * p.dA.s0 + n * p.dA.s1, s);
   }
 }

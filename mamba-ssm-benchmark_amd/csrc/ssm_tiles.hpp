@@ -44,4 +44,22 @@ __device__ __forceinline__ float pairwise_sum(const float (&v)[N]) {
   }
 }
 
+// Sum of count values at src[0], src[stride], ... in index order (the bits of a running sum),
+// the reads of G terms issued together ahead of their adds: a sum over partials in HBM is
+// otherwise a chain of dependent memory round trips.
+template <int G, typename CT>
+__device__ inline CT ordered_sum(const CT *src, int64_t stride, int64_t count) {
+  CT s = 0;
+  int64_t k = 0;
+  for (; k + G <= count; k += G) {
+    CT v[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) v[u] = src[(k + u) * stride];
+#pragma unroll
+    for (int u = 0; u < G; ++u) s += v[u];
+  }
+  for (; k < count; ++k) s += src[k * stride];
+  return s;
+}
+
 }  // namespace ssm
