@@ -152,16 +152,19 @@ def test_lowrank_mixed_layouts(dev):
         close(t.grad, rg[name], name=name)
 
 
-def test_lowrank_bf16_inputs(dev):
-    """bf16 x, dt, B, C, z (state float32): rtol 2e-2 against the oracle on the rounded inputs."""
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float16, 4e-3)])
+def test_lowrank_half_precision_inputs(dev, dtype, tol):
+    """16-bit x, dt, B, C, z (state float32): the output, last state and dW against the oracle
+    on the rounded inputs, rtol = atol = 2e-2 (bf16) or 4e-3 (fp16), as the 16-bit tests of
+    the materialized-delta path."""
     B, L, D, N, Rk = 2, 64, 32, 16, 16
-    ins = make(B, L, D, N, Rk, seed=17, dtype=torch.bfloat16)
+    ins = make(B, L, D, N, Rk, seed=17, dtype=dtype)
     out, last, grads = run(dev, *ins, Rk, N, "zoh")
-    assert out.dtype == torch.bfloat16
+    assert out.dtype == dtype
     rout, rlast, rg = oracle(*ins, Rk, N, "zoh")
-    close(out, rout, 2e-2, 2e-2, "out")
-    close(last, rlast, 2e-2, 2e-2, "last")
-    close(grads["dW"], rg["dW"], 2e-2, 2e-2, "dW")
+    close(out, rout, tol, tol, "out")
+    close(last, rlast, tol, tol, "last")
+    close(grads["dW"], rg["dW"], tol, tol, "dW")
 
 
 def test_lowrank_with_initial_state_and_last_gradient(dev):
