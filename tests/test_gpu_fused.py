@@ -279,6 +279,36 @@ def test_decode_step_matches_forward(dev):
     torch.testing.assert_close(h, last, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("method", ["zoh", "euler", "bilinear"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64])
+def test_decode_step_dtypes_bias_softplus(dev, dtype, method):
+    """ssm_step with dt bias + softplus, D skip and gate for float32, bf16 (float32 state) and
+    float64 inputs against the oracle's step (models/mamba.py:113-118,122-124) on the same
+    (rounded) inputs: the state at the float32 bar (float64: 1e-10), the output at the bar of
+    its dtype (bf16 output rounding: rtol 2e-2)."""
+    g = torch.Generator().manual_seed(21)
+    B, D, N = 5, 40, 16
+    ct = torch.float64 if dtype == torch.float64 else torch.float32
+    mk = lambda *s, dt=dtype: torch.randn(*s, generator=g, dtype=torch.float64).to(dt)
+    h = mk(B, D, N, dt=ct)
+    x, delta, z = mk(B, D), mk(B, D) * 0.5 - 1.0, mk(B, D)
+    A = -(torch.rand(D, N, generator=g, dtype=torch.float64) * 4 + 0.05).to(ct)
+    Bm, Cm, Dv, bias = mk(B, N), mk(B, N), mk(D, dt=ct), mk(D, dt=ct) * 0.5
+    h_dev = h.to(dev)
+    out = ssm_scan.ssm_step(h_dev, x.to(dev), delta.to(dev), A.to(dev), Bm.to(dev), Cm.to(dev), D=Dv.to(dev),
+                            z=z.to(dev), delta_bias=bias.to(dev), delta_softplus=True, method=method)
+    torch.cuda.synchronize()
+    d_eff = np.log1p(np.exp(np64(delta) + np64(bias)))
+    ry, rh = R.ssm_step(np64(h), np64(x), d_eff, np64(A), np64(Bm), np64(Cm), method, np64(Dv), np64(z))
+    assert out.dtype == dtype and h_dev.dtype == ct
+    if dtype == torch.float64:
+        close(out, ry, 1e-10, 1e-10, "y")
+        close(h_dev, rh, 1e-10, 1e-10, "h")
+    else:
+        close(h_dev, rh, name="h")
+        close(out, ry, *((RTOL_BF16, ATOL_BF16) if dtype == torch.bfloat16 else (RTOL, ATOL)), "y")
+
+
 def test_cpu_tensors_are_rejected():
     x, delta, A, Bm, Cm, _ = triton_test_inputs(1, 4, 8, 16, False)
     with pytest.raises(RuntimeError, match="GPU"):
