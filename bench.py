@@ -531,9 +531,13 @@ def bench_refdecode(args, dev):
     """The reference's own decode benchmark (benchmarks/bench_decode.py:27-61, the "mamba" preset
     of models/lm.py:150-152): the 11-layer Mamba LM (d_model 256), batch 1, one token step inside
     a bf16 autocast region with a bf16 conv state and a float32 SSM state (N(0,1)).  `value` is
-    the fused token step (FastDecoder: per layer one in_proj GEMM, the fused decode layer, one
-    out_proj + residual GEMM, computed in float32, the conv state kept in bf16) replayed from a
-    HIP graph; beside it the model's own decode path under autocast (the structure of
+    the fused token step FastDecoder(model) takes by default at this shape, the stack path
+    (ssm_decode_stack: the embedding row, two launches per block with the in_proj, x_proj,
+    dt_proj and out_proj products inside, and the final norm + head; computed in float32, the
+    conv state kept in bf16) replayed from a HIP graph; `block_path_graph_ms_per_token_model`
+    holds the per-block path (an in_proj GEMM, the fused decode layer and an out_proj + residual
+    GEMM per block) replayed the same way; beside them the model's own decode path under
+    autocast (the structure of
     models/mamba.py: the engine's conv and scan step kernels between bf16 GEMMs), eager and
     replayed.  The reference's published time is on an RTX 3050 Laptop GPU (0.919 ms/token,
     graph replay)."""

@@ -4,7 +4,8 @@ and torch.nn.functional.conv1d (float64, CPU; gradients by autograd).
 Mirrors the conv of models/mamba.py:101-107 incl. its state handling (:104-106): a sequence
 processed in pieces with the carried state, and one token at a time, equals the whole
 sequence (the reference's decode == forward check, tests/test_models.py:36-48).
-Tolerances: float32 rtol 1e-5 / atol 1e-6 (a W-tap dot product); bf16 inputs 2e-2; float64 1e-12.
+Tolerances: float32 rtol 1e-5 / atol 1e-6 (a W-tap dot product); bf16 inputs rtol 2e-2 / atol
+1e-5; float64 1e-12.
 """
 
 import numpy as np
@@ -17,7 +18,7 @@ from oracle import scan_ref as R
 from ssm_inputs import np64
 
 pytestmark = pytest.mark.gpu
-TOL = {torch.float32: (1e-5, 1e-6), torch.bfloat16: (2e-2, 2e-2), torch.float64: (1e-12, 1e-12)}
+TOL = {torch.float32: (1e-5, 1e-6), torch.bfloat16: (2e-2, 1e-5), torch.float64: (1e-12, 1e-12)}
 
 
 def ref_conv(x_bld, w, bias, activation=True):

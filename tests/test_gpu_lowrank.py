@@ -16,7 +16,7 @@ import ssm_scan
 from oracle import scan_ref as R
 from ssm_inputs import np64
 
-from parity import ATOL, RTOL, close  # noqa: F401  (the north_star bar)
+from parity import ATOL, RTOL, close, close_or_cancelled  # noqa: F401  (the north_star bar)
 
 pytestmark = pytest.mark.gpu
 
@@ -67,8 +67,9 @@ def oracle(x, proj, W, A, Dv, z, bias, dout, Rk, N, method):
     draw = g["ddelta"] / (1.0 + np.exp(-raw))
     dproj = np.concatenate([draw @ W, g["dB"], g["dC"]], -1)
     dW = draw.reshape(-1, W.shape[0]).T @ dt.reshape(-1, Rk)
+    dW_mag = np.abs(draw).reshape(-1, W.shape[0]).T @ np.abs(dt).reshape(-1, Rk)   # sum of |terms|
     return out, last, {"dx": g["dx"], "dproj": dproj, "dW": dW, "dA": g["dA"], "dD": g["dD"], "dz": g["dz"],
-                       "dbias": draw.sum(axis=(0, 1))}
+                       "dbias": draw.sum(axis=(0, 1)), "dW_mag": dW_mag}
 
 
 @pytest.mark.parametrize("method", ["zoh", "euler", "bilinear"])
@@ -154,17 +155,23 @@ def test_lowrank_mixed_layouts(dev):
 
 @pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float16, 4e-3)])
 def test_lowrank_half_precision_inputs(dev, dtype, tol):
-    """16-bit x, dt, B, C, z (state float32): the output, last state and dW against the oracle
-    on the rounded inputs, rtol = atol = 2e-2 (bf16) or 4e-3 (fp16), as the 16-bit tests of
-    the materialized-delta path."""
+    """16-bit x, dt, B, C, z (state float32): the output and last state against the oracle on
+    the rounded inputs at rtol 2e-2 (bf16) or 4e-3 (fp16) with atol 1e-5, as the 16-bit tests
+    of the materialized-delta path.  dW is the GEMM of the scan's 16-bit ddelta output with dt
+    over the B x L tokens (the weight gradient of dt_proj): each of its terms carries the
+    16-bit rounding of ddelta, so an element outside the bar must be within two units of that
+    rounding (2^-7 bf16, 2^-10 fp16) of the sum of its terms' magnitudes; the count outside
+    the bar is printed."""
     B, L, D, N, Rk = 2, 64, 32, 16, 16
     ins = make(B, L, D, N, Rk, seed=17, dtype=dtype)
     out, last, grads = run(dev, *ins, Rk, N, "zoh")
     assert out.dtype == dtype
     rout, rlast, rg = oracle(*ins, Rk, N, "zoh")
-    close(out, rout, tol, tol, "out")
-    close(last, rlast, tol, tol, "last")
-    close(grads["dW"], rg["dW"], tol, tol, "dW")
+    close(out, rout, tol, 1e-5, "out")
+    close(last, rlast, tol, 1e-5, "last")
+    unit = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    close_or_cancelled(grads["dW"], rg["dW"], rg["dW_mag"], "dW", allow=rg["dW"].size, rtol=tol, atol=1e-5,
+                       unit=unit)
 
 
 def test_lowrank_with_initial_state_and_last_gradient(dev):

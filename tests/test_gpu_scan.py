@@ -4,8 +4,11 @@ Covers the materialized discretization (ssm_disc_fwd / ssm_disc_bwd), the four l
 algorithms and their adjoint (ssm_lscan / ssm_lscan_bwd), SelectiveScanFn over channel tiles,
 and the selective_scan dispatcher.  The reference's own checks are mirrored: all algorithms
 equal the sequential loop incl. ragged chunks (tests/test_scan.py:34-54), extreme decays
-(:132-142), gradients against the textbook recurrence (:67-88).  Tolerances: float32 rtol
-1e-4 / atol 1e-5; float64 rtol 1e-10.
+(:132-142), gradients against the textbook recurrence (:67-88).  Tolerances: the float32 bar
+of tests/parity.py on every element (rtol 1e-4 / atol 1e-5, no scaling by the tensor's
+magnitude), float64 rtol 1e-10 / atol 1e-12; the oracle consumes the inputs rounded to the
+dtype under test, as the reference's own float32 run would.  bf16 inputs (float32 compute):
+rtol 2e-2 / atol 1e-5.
 """
 
 import numpy as np
@@ -16,18 +19,24 @@ import ssm_scan
 from ssm_scan import scan as S
 from oracle import scan_ref as R
 from ssm_inputs import np64
+import parity
 
 pytestmark = pytest.mark.gpu
 
 ALGOS = ("sequential", "hillis_steele", "blelloch", "chunked")
-TOL = {torch.float32: (1e-4, 1e-5), torch.float64: (1e-10, 1e-12)}
+TOL = {torch.float32: (parity.RTOL, parity.ATOL), torch.float64: (1e-10, 1e-12),
+       torch.bfloat16: (parity.RTOL_BF16, parity.ATOL_BF16)}
 
 
-def close(got, ref, dtype, name="", scale_ref=True):
+def close(got, ref, dtype, name="", allow=0):
+    """Every element within atol + rtol |ref| of the oracle (no magnitude scaling)."""
     rtol, atol = TOL[dtype]
-    ref = np.asarray(ref)
-    scale = max(1.0, float(np.sqrt(np.mean(np.square(ref))))) if scale_ref and ref.size else 1.0
-    np.testing.assert_allclose(np64(got), ref, rtol=rtol, atol=atol * scale, err_msg=name)
+    parity.close(got, ref, rtol=rtol, atol=atol, name=f"{name} {str(dtype)[6:]}", allow=allow)
+
+
+def rnd(t, dtype):
+    """The float64 oracle's view of an input the kernels receive in `dtype`."""
+    return None if t is None else np64(t.to(dtype))
 
 
 def sel_inputs(B=2, L=33, D=20, N=8, seed=0, h0=True):
@@ -60,11 +69,12 @@ def test_discretize_forward_and_vjp(dev, method, dtype):
     leaves = [t.to(dev, dtype).requires_grad_() for t in (delta, A, Bm, x)]
     a, b = S.discretize(*leaves, method=method)
     assert a.shape == (2, 37, 21, 5) and a.dtype == dtype
-    ra, rb = R.discretize(*(np64(t) for t in (delta, A, Bm, x)), method)
+    ins = [rnd(t, dtype) for t in (delta, A, Bm, x)]
+    ra, rb = R.discretize(*ins, method)
     close(a.detach(), ra, dtype, "a")
     close(b.detach(), rb, dtype, "b")
     torch.autograd.backward((a, b), (ga.to(dev, dtype), gb.to(dev, dtype)))
-    ref = R.discretize_vjp(*(np64(t) for t in (delta, A, Bm, x)), np64(ga), np64(gb), method)
+    ref = R.discretize_vjp(*ins, rnd(ga, dtype), rnd(gb, dtype), method)
     for name, t, r in zip(("ddelta", "dA", "dBm", "dx"), leaves, ref):
         close(t.grad, r, dtype, name)
 
@@ -76,7 +86,8 @@ def test_discretize_strided_views_and_errors(dev):
     big[..., 2:6] = Bm
     Bv = big[..., 2:6].to(dev, torch.float32)                                  # strided split view
     a, b = S.discretize(delta.to(dev, torch.float32), A.to(dev, torch.float32), Bv, xs, "zoh")
-    ra, rb = R.discretize(np64(delta), np64(A), np64(Bm), np64(x), "zoh")
+    f32 = torch.float32
+    ra, rb = R.discretize(rnd(delta, f32), rnd(A, f32), rnd(Bm, f32), rnd(x, f32), "zoh")
     close(a, ra, torch.float32)
     close(b, rb, torch.float32)
     with pytest.raises(ValueError):
@@ -100,7 +111,8 @@ def test_discretize_backward_long_groups_and_strided_views(dev):
         t.requires_grad_()
     a, b = S.discretize(*leaves, method="zoh")
     torch.autograd.backward((a, b), (ga.to(dev, torch.float32), gb.to(dev, torch.float32)))
-    ref = R.discretize_vjp(*(np64(t) for t in (delta, A, Bm, x)), np64(ga), np64(gb), "zoh")
+    f32 = torch.float32
+    ref = R.discretize_vjp(*(rnd(t, f32) for t in (delta, A, Bm, x)), rnd(ga, f32), rnd(gb, f32), "zoh")
     for name, t, r in zip(("ddelta", "dA", "dBm", "dx"), leaves, ref):
         close(t.grad, r, torch.float32, name)
 
@@ -122,11 +134,11 @@ def test_zoh_matrix_matches_diagonal_discretize(dev):
 def test_scans_match_sequential_oracle(dev, name, L, with_h0):
     a, b, h0 = ab_inputs((2, L, 3, 5), seed=L)
     h0 = h0 if with_h0 else None
-    ref = R.scan_sequential(np64(a), np64(b), None if h0 is None else np64(h0))
     for dtype in (torch.float64, torch.float32):
+        ref = R.scan_sequential(rnd(a, dtype), rnd(b, dtype), rnd(h0, dtype))
         got = S.SCANS[name](a.to(dev, dtype), b.to(dev, dtype), None if h0 is None else h0.to(dev, dtype))
         assert got.shape == a.shape and got.dtype == dtype
-        close(got, ref, dtype, f"{name} {dtype}")
+        close(got, ref, dtype, name)
 
 
 @pytest.mark.parametrize("chunk", [1, 3, 4, 5, 16, 64, 100, 700])
@@ -163,8 +175,9 @@ def test_scan_adjoint_matches_oracle(dev, name, with_h0):
         hz = h0.to(dev, dtype).requires_grad_() if with_h0 else None
         h = S.SCANS[name](leaves[0], leaves[1], hz)
         h.backward(dh.to(dev, dtype))
-        href = R.scan_sequential(np64(a), np64(b), np64(h0) if with_h0 else None)
-        da, db, dh0 = R.scan_vjp(np64(a), np64(h0) if with_h0 else None, href, np64(dh))
+        ra, rh0 = rnd(a, dtype), rnd(h0, dtype) if with_h0 else None
+        href = R.scan_sequential(ra, rnd(b, dtype), rh0)
+        da, db, dh0 = R.scan_vjp(ra, rh0, href, rnd(dh, dtype))
         close(leaves[0].grad, da, dtype, "da")
         close(leaves[1].grad, db, dtype, "db")
         if with_h0:
@@ -184,10 +197,10 @@ def test_reverse_scan_and_errors(dev):
 
 
 # ------------------------------------------------------------------ composed selective scan
-def _oracle_sel(ins, method, dy, dlast):
-    x, delta, A, Bm, Cm, h0 = (np64(t) for t in ins)
+def _oracle_sel(ins, method, dy, dlast, dtype=torch.float64):
+    x, delta, A, Bm, Cm, h0 = (rnd(t, dtype) for t in ins)
     _, y, last = R.selective_scan_fwd(x, delta, A, Bm, Cm, h0, method)
-    g = R.selective_scan_bwd(x, delta, A, Bm, Cm, np64(dy), h0, method, dlast=np64(dlast))
+    g = R.selective_scan_bwd(x, delta, A, Bm, Cm, rnd(dy, dtype), h0, method, dlast=rnd(dlast, dtype))
     return y, last, g
 
 
@@ -204,7 +217,7 @@ def test_selective_scan_composed_matches_oracle(dev, scan, method, dtype):
                                chunk_size=5 if scan == "chunked" else None)
     assert y.dtype == dtype and last.dtype == dtype and last.shape == (2, 20, 8)
     ((y * dy.to(dev, dtype)).sum() + (last * dlast.to(dev, dtype)).sum()).backward()
-    ry, rlast, rg = _oracle_sel(ins, method, dy, dlast)
+    ry, rlast, rg = _oracle_sel(ins, method, dy, dlast, dtype)
     close(y.detach(), ry, dtype, "y")
     close(last.detach(), rlast, dtype, "last")
     for name, t in zip(("dx", "ddelta", "dA", "dB", "dC", "dh0"), leaves):
@@ -218,7 +231,7 @@ def test_selective_scan_dispatch_names(dev, scan):
     y, last = S.selective_scan(*leaves, method="zoh", scan=scan)
     dy = torch.ones_like(y)
     y.backward(dy)
-    ry, rlast, rg = _oracle_sel(ins, "zoh", dy.cpu().double(), None)
+    ry, rlast, rg = _oracle_sel(ins, "zoh", dy.cpu().double(), None, torch.float32)
     close(y.detach(), ry, torch.float32, "y")
     close(last.detach(), rlast, torch.float32, "last")
     for name, t in zip(("dx", "ddelta", "dA", "dB", "dC", "dh0"), leaves):
@@ -229,7 +242,7 @@ def test_selective_scan_auto_non_power_of_two_uses_chunked(dev):
     ins = sel_inputs(B=1, L=20, D=8, N=6, seed=9, h0=False)
     assert ssm_scan.plan.resolve_scan("auto", True, "zoh", 6) == "chunked"
     y, last = S.selective_scan(*(None if t is None else t.to(dev, torch.float32) for t in ins), scan="auto")
-    ry, rlast, _ = _oracle_sel(ins, "zoh", torch.zeros(1, 20, 8, dtype=torch.float64), None)
+    ry, rlast, _ = _oracle_sel(ins, "zoh", torch.zeros(1, 20, 8, dtype=torch.float64), None, torch.float32)
     close(y, ry, torch.float32)
     close(last, rlast, torch.float32)
 
@@ -242,10 +255,28 @@ def test_selective_scan_errors_and_dtypes(dev):
         S.selective_scan(*ins, method="rk4", scan="chunked")
     with pytest.raises(ValueError):
         S.selective_scan(*ins, method="rk4", scan="triton")
-    bf = [t.to(torch.bfloat16) if t is not None else None for t in ins]
-    for scan in ("chunked", "triton", "reference"):
-        y, last = S.selective_scan(*bf, scan=scan)
-        assert y.dtype == torch.bfloat16 and last.dtype == torch.float32
+
+
+@pytest.mark.parametrize("scan", ["chunked", "blelloch", "triton", "reference"])
+def test_selective_scan_bf16_inputs_match_oracle(dev, scan):
+    """bf16 inputs compute in float32 (models/scan.py:289-299): y returns in bf16 and `last` in
+    float32, gradients in the inputs' dtype.  y, last and the six gradients against the float64
+    oracle on the bf16-rounded inputs at the bf16 bar (rtol 2e-2 / atol 1e-5)."""
+    bf = torch.bfloat16
+    ins = sel_inputs(B=2, L=40, D=16, N=16, seed=14, h0=True)
+    g = torch.Generator().manual_seed(15)
+    dy = torch.randn(2, 40, 16, generator=g, dtype=torch.float64)
+    dlast = torch.randn(2, 16, 16, generator=g, dtype=torch.float64)
+    leaves = [t.to(dev, bf).requires_grad_() for t in ins]
+    y, last = S.selective_scan(*leaves, method="zoh", scan=scan, d_block=5)
+    assert y.dtype == bf and last.dtype == torch.float32
+    ((y.float() * dy.to(dev, bf).float()).sum() + (last * dlast.to(dev, bf).float()).sum()).backward()
+    ry, rlast, rg = _oracle_sel(ins, "zoh", dy, dlast, bf)
+    close(y.detach(), ry, bf, "y")
+    close(last.detach(), rlast, bf, "last")
+    for name, t in zip(("dx", "ddelta", "dA", "dB", "dC", "dh0"), leaves):
+        assert t.grad.dtype == bf, name
+        close(t.grad, rg[name], bf, name)
 
 
 def test_composed_backward_is_deterministic(dev):

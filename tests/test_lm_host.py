@@ -115,3 +115,27 @@ def test_dense_embedding_gradient_on_the_cpu():
     torch.testing.assert_close(got, emb.weight.grad, rtol=1e-5, atol=1e-5)
     with torch.no_grad():                         # not training: torch's own embedding
         assert torch.equal(embedding(emb, idx), emb(idx))
+
+
+@pytest.mark.parametrize("method", ["zoh", "bilinear"])
+def test_lm_ref_c_oracle_scan_node_matches_time_loop(method):
+    """oracle/lm_ref's scan="c" node (each layer's scan, D skip and gate on the C oracle's float64
+    forward and adjoint) equals the autograd time loop of the same restatement: the logits and
+    every parameter gradient of a 2-layer LM, float64, to 1e-10."""
+    from oracle import lm_ref
+    torch.manual_seed(3)
+    m = MambaLM(n_layers=2, d_model=32, d_state=8)
+    sd = m.state_dict()
+    g = torch.Generator().manual_seed(4)
+    idx = torch.randint(0, 256, (2, 24), generator=g)
+    w = torch.randn(2, 24, 256, generator=g, dtype=torch.float64)
+    res = []
+    for scan in ("loop", "c"):
+        p = {k: v.detach().double().requires_grad_() for k, v in sd.items()}
+        logits = lm_ref.lm_forward(p, idx, 2, d_state=8, dt_rank=2, method=method, scan=scan)
+        (logits * w).sum().backward()
+        res.append((logits.detach(), {k: t.grad for k, t in p.items() if t.grad is not None}))
+    torch.testing.assert_close(res[1][0], res[0][0], rtol=1e-10, atol=1e-12)
+    assert res[0][1].keys() == res[1][1].keys() and len(res[0][1]) == 2 + 2 * 10
+    for k, g0 in res[0][1].items():
+        torch.testing.assert_close(res[1][1][k], g0, rtol=1e-10, atol=1e-12, msg=k)

@@ -455,3 +455,31 @@ def test_lm_ref_rmsnorm_matches_torch_rms_norm(shape, eps):
     torch.testing.assert_close(lm_ref.rmsnorm(x, w, eps), ref, rtol=1e-13, atol=1e-13)
     # a plausible slip (eps outside the root, or a sum instead of the mean) fails this check
     assert not torch.allclose(x / (x.pow(2).mean(-1, keepdim=True).sqrt() + eps) * w, ref, rtol=1e-13, atol=0) or eps < 1e-12
+
+
+@pytest.mark.parametrize("ragged", [False, True])
+def test_cpu_baseline_restatement_matches_oracle(monkeypatch, ragged):
+    """oracle/cpu_chunked (the torch-CPU restatement timed as bench.py's cpu_baseline) against
+    the numpy oracle in float64: the output (y + D x) * silu(z) and all seven gradients of one
+    fwd + bwd, to 1e-10.  Channel tiles of 3 (d_block forced below D, models/scan.py:185-190)
+    and, ragged, a length that is not a multiple of the chunk (padding of scan_chunked)."""
+    from oracle import cpu_chunked
+    monkeypatch.setattr(cpu_chunked, "_blocks", lambda B, L, D, N: [(i, min(i + 3, D)) for i in range(0, D, 3)])
+    B, L, D, N = 2, 37 if ragged else 32, 8, 4
+    g = torch.Generator().manual_seed(71)
+    x = torch.randn(B, L, D, generator=g, dtype=torch.float64)
+    delta = torch.rand(B, L, D, generator=g, dtype=torch.float64) * 0.3 + 1e-3
+    A = -torch.rand(D, N, generator=g, dtype=torch.float64) * 4 - 0.05
+    Bm, Cm = (torch.randn(B, L, N, generator=g, dtype=torch.float64) for _ in range(2))
+    Dv = torch.randn(D, generator=g, dtype=torch.float64)
+    z, dy = (torch.randn(B, L, D, generator=g, dtype=torch.float64) for _ in range(2))
+    f = [t.numpy() for t in (x, delta, A, Bm, Cm)]
+    out, y, _ = R.selective_scan_fwd(*f, None, "zoh", Dv.numpy(), z.numpy())
+    np.testing.assert_allclose(cpu_chunked.fwd(x, delta, A, Bm, Cm).numpy(), y, rtol=1e-10, atol=1e-12)
+    ref = R.selective_scan_bwd(*f, dy.numpy(), None, "zoh", Dv.numpy(), z.numpy())
+    got = cpu_chunked.fwd_bwd(x, delta, A, Bm, Cm, Dv, z, dy)
+    for name, gv in zip(("dx", "ddelta", "dA", "dB", "dC", "dD", "dz"), got):
+        np.testing.assert_allclose(gv.numpy(), ref[name], rtol=1e-10, atol=1e-12, err_msg=name)
+    # a planted slip (a dropped D skip in the restatement's output) is caught by this check
+    bad = (torch.from_numpy(y) * torch.nn.functional.silu(z)).numpy()
+    assert not np.allclose(bad, out, rtol=1e-10, atol=1e-12)
