@@ -746,7 +746,8 @@ def bench_copy(args, dev):
 def c1_extras(args, dev):
     """The other north_star targets and the long-sequence fwd+bwd, measured in the default run
     beside the c1 line: c2's L = 131072 fp32 forward against the CPU baseline, c4's decode
-    latency per layer at batch 64 (graph replay), and B1 D512 N16 fwd+bwd at L 4096..65536."""
+    latency per layer at batch 64 (graph replay), config 3's 10-layer LM training step (B16
+    L512, eager), and B1 D512 N16 fwd+bwd at L 4096..65536."""
     sub = argparse.Namespace(**vars(args))
     sub.steps, sub.warmup = min(args.steps, 20), min(args.warmup, 5)
     sub.segments = 0
@@ -765,6 +766,14 @@ def c1_extras(args, dev):
     out["c4_decode"] = {"us_per_layer": c4["value"], "ms_per_token_model": c4["ms_per_token_model"],
                         "step_mode": c4["timing"], "path": "ssm_decode_stack", "batch": 64, "target_us_per_layer": 20.0,
                         "cpu_baseline_us_per_layer": c4.get("cpu_baseline", {}).get("value")}
+    torch.cuda.empty_cache()
+    sub3 = argparse.Namespace(**vars(sub))
+    sub3.steps, sub3.warmup = min(args.steps, 10), min(args.warmup, 3)
+    c3 = bench_lm(sub3, dev)
+    out["c3_lm"] = {"ms_per_step": c3["ms_per_step"], "tokens_per_s": c3["value"], "step_mode": c3["step_mode"],
+                    "steps": sub3.steps, "engine_ms_per_step": c3["engine_ms_per_step"],
+                    "workload": "config 3: 10-layer Mamba LM fwd+bwd, B16 L512 fp32, next-byte cross-entropy"}
+    del c3
     torch.cuda.empty_cache()
     lg = bench_long(sub, dev)
     out["long_fwd_bwd"] = {"Mtok_s_L65536": lg["value"], "vs_reference_published": lg["vs_baseline"],

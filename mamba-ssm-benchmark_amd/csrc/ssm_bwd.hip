@@ -552,12 +552,15 @@ __global__ void __launch_bounds__(256) k_bwd_finalize(const FinParams p) {
 // adjoint carried into it.  A summary pass (SUM) gives each segment's zero-start adjoint at its
 // first step times that step's decay (E) and the product of its decays (P); k_bwd_carry turns
 // them into the adjoint entering every segment, the reverse of the forward's segment carry.
+// (dx, ddelta) terms of half a chunk at [c * PCS + (t * 2 + q) * NPP + n]: the 16 lanes of a
+// 16-byte read phase (one channel's 8 steps x 2 quantities) read 16 consecutive rows, and a
+// channel block is padded by 16 floats so the state lanes' writes fall on 64 distinct banks.
 template <int NP, bool LR>
 struct BwdwLds {
-  static constexpr int CW = kWave / NP, CKP = ck_pad(4), NPP = np_pad(4, NP), RH = 8;
+  static constexpr int CW = kWave / NP, CKP = ck_pad(4), NPP = np_pad(4, NP), RH = 8, PCS = 2 * RH * NPP + 16;
   float B[NP][CKP];
   float C[NP][CKP];
-  float pn[RH][CW][2][NPP];  // (dx, ddelta) terms of half a chunk, per state
+  float pn[CW * PCS];
   float lr[LR ? kCK : 1][lr_pad(4)];
   float wr[LR ? CW : 1][lr_pad(4)];
 };
@@ -569,14 +572,18 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   typedef RowTile<IT, NP, UL> RT;
   constexpr int CW = G::CW, CK = kCK, RH = WL::RH, WPB = bwdw_waves(NP), NT = WPB * kWave;
   constexpr bool M1 = METHOD == 0;
-  // (dB, dC) terms of half a chunk for every channel of the workgroup, by half: rows of CH
-  // channels padded to CHP (16-byte reads; the lanes of one write hit distinct banks).  After
-  // a barrier TPI threads sum each (step, quantity, state) row, IPT rows per thread.
+  // (dB, dC) of half a chunk for every channel of the workgroup, by half: rows of CH channels
+  // padded to CHP (16-byte reads; the lanes of one write hit distinct banks).  The state lanes
+  // write their factors -- dB_t[n] = sum_c (lambda cf)_t[c][n] x_t[c] and dC_t[n] = sum_c
+  // h_t[c][n] dy_t[c] -- and after a barrier TPI threads form each (step, quantity, state)
+  // row's dot product with the step's x or dy row (staged per chunk, by chunk parity), IPT
+  // rows per thread: one FMA per term where a product per state lane and an add were two.
   constexpr int CH = WPB * CW, CHP = CH + 4, NITEM = RH * 2 * NP;
   constexpr int TPI = NT >= NITEM ? NT / NITEM : 1, IPT = NITEM > NT ? NITEM / NT : 1, CPT = CH / TPI;
   static_assert(TPI <= 2 && CPT % 4 == 0 && NITEM == IPT * (NT / TPI), "reduction layout");
   __shared__ __align__(16) WL lds_all[WPB];
   __shared__ __align__(16) float pdw[2][RH][2][NP][CHP];
+  __shared__ __align__(16) float xdy[2][2][kCK][CHP];  // [chunk parity][x, dy][step][channel]
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave, wv = tid / kWave;
@@ -708,19 +715,33 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   // whose work hides their latency (the two wavefronts of a SIMD belong to one workgroup and
   // reach the barrier together, so nothing else would).  dq_t: first step of the pending half;
   // dq_L: the sequence length, 0 when nothing is pending (every store masked).
-  float dq[IPT][CPT];
+  float dq[IPT][CPT], dqw[IPT][CPT];
 #pragma unroll
   for (int i = 0; i < IPT; ++i)
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) dq[i][j] = 0.0f;
+    for (int j = 0; j < CPT; ++j) dq[i][j] = dqw[i][j] = 0.0f;
   int dq_t = 0, dq_L = 0;
+  // Reducer thread -> (row item, part of its channels).  With two threads per item the 16 lanes
+  // of a 16-byte read phase take 16 consecutive items of one part (16 distinct rows, distinct
+  // banks); a thread's partner is the lane 16 apart in its 32-lane half.
+  auto red_item = [&](int i, int &item, int &part) {
+    if constexpr (TPI == 2) {
+      part = (tid >> 4) & 1;
+      item = (tid >> 5) * 16 + (tid & 15) + i * (NT / TPI);
+    } else {
+      part = 0;
+      item = tid + i * NT;
+    }
+  };
   auto dq_flush = [&]() {
 #pragma unroll
     for (int i = 0; i < IPT; ++i) {
-      const int item = tid / TPI + i * (NT / TPI), part = tid % TPI;
+      int item, part;
+      red_item(i, item, part);
       const int st = item / (2 * NP), q = (item / NP) % 2, nn = item % NP;
-      float sum = pairwise_sum(dq[i]);
-      if constexpr (TPI == 2) sum += dpp_f<0xB1>(sum);  // the partner lane's channels (same bits in both)
+      float sum = dot_sum(dq[i], dqw[i]);
+      if constexpr (TPI == 2)  // the partner's channels (lane ^ 16; the same bits in both lanes)
+        sum += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, sum), 0x401F));
       const int tg = dq_t + st;
       if constexpr (UL) {  // two masked stores: q differs between the lanes of a wavefront
         const uint32_t ow = (uint32_t)((st * NP + nn) * 4), tw = (uint32_t)(dq_t * NP * 4);
@@ -778,6 +799,10 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
       }
     }
     const float hstart = k <= 0 ? h0v : T.ck;
+    if constexpr (!SUM) {  // the chunk's x and dy rows for the (dB, dC) sums of every wavefront
+      xdy[par][0][tj][wv * CW + tc] = xv;
+      xdy[par][1][tj][wv * CW + tc] = dyv;
+    }
     wave_lds_sync();
     load(T, k - 1);
     // the chunk's B and C rows of this lane's state, read once: the recompute and the walk use
@@ -807,11 +832,10 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
 
     float dA_acc = 0.0f;
     // ------------------------------------------------------------ walk back, half a chunk at a time
-    // The walk broadcasts delta and x again rather than keeping the recompute's 2 x 16 values
-    // live (tied to the adjoint: the compiler cannot reuse them).
-    float dvw = dv, xvw = xv;
+    // The walk broadcasts delta again rather than keeping the recompute's 16 values live (tied
+    // to the adjoint: the compiler cannot reuse them).
+    float dvw = dv;
     order_after(dvw, lamf);
-    order_after(xvw, lamf);
     static_for_down<0, CK / RH>([&](auto hcst) {
       constexpr int half = decltype(hcst)::value;
       const float *rC = rCa + half * RH, *rB = rBa + half * RH;
@@ -856,10 +880,10 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
             if constexpr (METHOD == 1) dA_acc = fmaf(lamf * dtb, a_ * hh[t], dA_acc);
             else dA_acc = fmaf(lamf * dtb * (u_ * u_), fmaf(0.5f * dtb, bx[t], hh[t]), dA_acc);
           }
-          S.pn[tt][c][0][n] = dhc * rB[tt];
-          S.pn[tt][c][1][n] = pD;
-          pdw[half][tt][0][n][wv * CW + c] = dhc * row_bcast<t>(xvw);
-          pdw[half][tt][1][n][wv * CW + c] = dyb * hh[t + 1];
+          S.pn[c * WL::PCS + (tt * 2) * WL::NPP + n] = dhc * rB[tt];
+          S.pn[c * WL::PCS + (tt * 2 + 1) * WL::NPP + n] = pD;
+          pdw[half][tt][0][n][wv * CW + c] = dhc;
+          pdw[half][tt][1][n][wv * CW + c] = hh[t + 1];
         }
       });
       if constexpr (!SUM) {
@@ -868,7 +892,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
         // the previous half's (dB, dC) sums (read during this walk) are formed meanwhile
         {
           float part[NP];
-          lds_row(&S.pn[tj % RH][tc][tj / RH][0], part);
+          lds_row(&S.pn[tc * WL::PCS + ((tj % RH) * 2 + tj / RH) * WL::NPP], part);
           dq_flush();
           Rh[half] = pairwise_sum(part);
         }
@@ -876,15 +900,16 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
         lds_barrier();
 #pragma unroll
         for (int i = 0; i < IPT; ++i) {
-          const int item = tid / TPI + i * (NT / TPI), part = tid % TPI;
+          int item, part;
+          red_item(i, item, part);
           const int st = item / (2 * NP), q = (item / NP) % 2, nn = item % NP;
           lds_row(&pdw[half][st][q][nn][part * CPT], dq[i]);
+          lds_row(&xdy[par][q][half * RH + st][part * CPT], dqw[i]);
         }
         dq_t = t0 + half * RH;
         dq_L = Lc;
       }
     });
-    (void)par;
     dA64 += (double)dA_acc;
     if constexpr (SUM) {
       wave_lds_sync();

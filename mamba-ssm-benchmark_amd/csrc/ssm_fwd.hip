@@ -305,13 +305,20 @@ __global__ void __launch_bounds__(kThreads) k_fwd_carry(const FwdParams p) {
 //   * the chunk loop is software-pipelined: iteration k runs the serial state updates of chunk
 //     k - 1 interleaved step by step with the independent per-step work of chunk k (exp,
 //     expm1, B x), so most instructions have their operands ready when they issue.
+// The output y_t = sum_n C_t[n] h_t[n] is formed by the lanes that store it: the state lanes
+// put h_t itself into LDS and the (step, channel) lane takes the dot product with the step's C
+// row (C staged step-major), one FMA per state where a product per state lane and an add
+// would be two instructions.
 // NP >= 16 (a smaller dstate is padded to 16).
+// The states go in channel-major ([c][t][n], rows of NPP): the 16 lanes of one 16-byte read
+// phase (the steps of one channel) read 16 consecutive rows, and a channel block is padded by
+// 16 floats so the state lanes' writes (4 channels x 16 states) fall on 64 distinct banks.
 template <int NP>
 struct FwdwLds {
-  static constexpr int CW = kWave / NP, CKP = ck_pad(4), NPP = np_pad(4, NP);
+  static constexpr int CW = kWave / NP, CKP = ck_pad(4), NPP = np_pad(4, NP), YCS = kCK * NPP + 16;
   float B[NP][CKP];
-  float C[NP][CKP];
-  float y[kCK][CW][NPP];
+  float Ct[2][kCK][NPP];  // C of the chunk, step-major, by chunk parity
+  float y[CW * YCS];      // the chunk's states h_t at [c * YCS + t * NPP + n]
   float lr[kCK][lr_pad(4)];  // low-rank delta input rows of the chunk
   float wr[CW][lr_pad(4)];   // low-rank weight rows of the wavefront's channels
 };
@@ -322,7 +329,6 @@ template <bool SUM>
 struct FwdwStage {
   float m[kCK];  // ZOH: a - 1 (expm1); other methods: a
   float u[kCK];  // ZOH: B x / A; other methods: b
-  float C[SUM ? 1 : kCK];
   float x, z;    // the lane's row-tile element of x and the gate
 };
 
@@ -448,7 +454,6 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     const int Lc = k < k1 ? L : 0;
     const bool ev = t0 + tj < Lc && tval;  // the row-tile element is a real (step, channel)
     T.B.store(S.B, bt, lane, t0, Lc, 0, N);
-    if (!SUM) T.C.store(S.C, ctt, lane, t0, Lc, 0, N);
     nx.x = ev ? T.x.v : 0.0f;
     nx.z = T.z.v;
     float dv;
@@ -469,20 +474,23 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     dv = ev ? dv : 0.0f;  // padded steps: delta 0 is the identity step
     const float xv = nx.x;
     wave_lds_sync();
+    // chunk k's C (read by the next iteration's output phase) beside chunk k - 1's (read by
+    // this one's), before the tile registers are refilled
+    if (!SUM) T.C.store_t(S.Ct[k & 1], ctt, lane, t0, Lc, 0, N);
     load(T, k + 2);
     float rB[CK];
     lds_row(&S.B[n][0], rB);
-    if constexpr (!SUM) lds_row(&S.C[n][0], nx.C);
 
     // Scheduling window: step t's independent work follows the update of step t - 2, and the
-    // update of step t follows the independent work of step t - 2 (ties, no instructions).
+    // update of step t follows the independent work of step t - 2 (ties, no instructions: the
+    // tie on the update rewrites pv.u[t], which no later step reads, so no copy is needed).
     float dvs = dv, xvs = xv, hl1 = h, hl2 = h;
     static_for<0, CK>([&](auto tcst) {
       constexpr int t = decltype(tcst)::value;
       if constexpr (t >= 2) {
         order_after(dvs, hl2);
         order_after(xvs, hl2);
-        order_after(h, nx.m[t - 2], nx.u[t - 2]);
+        order_after(pv.u[t], nx.m[t - 2], nx.u[t - 2]);
       }
       // serial update of chunk k - 1 (ZOH: h <- h + (a - 1)(h + B x / A))
       if constexpr (METHOD == 0) {
@@ -492,7 +500,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
         h = fmaf(pv.m[t], h, pv.u[t]);
         if constexpr (SUM) prod *= pv.m[t];
       }
-      if constexpr (!SUM) S.y[t][c][n] = pv.C[t] * h;
+      if constexpr (!SUM) S.y[c * WL::YCS + t * WL::NPP + n] = h;
       // independent values of chunk k
       const float dtb = row_bcast<t>(dvs);
       const float bxr = rB[t] * row_bcast<t>(xvs);
@@ -514,10 +522,12 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     const int kp = k - 1;  // the chunk whose outputs are now complete
     const bool live = kp >= k0 && kp < k1;
     wave_lds_sync();
-    // outputs of chunk k - 1: the lane of (step tj, channel tc) sums the partials over the states
-    float part[NP];
-    lds_row(&S.y[tj][tc][0], part);
-    const float y = pairwise_sum(part);
+    // outputs of chunk k - 1: the lane of (step tj, channel tc) forms sum_n C[tj][n] h[tj][tc][n]
+    // (four interleaved FMA chains, added pairwise)
+    float part[NP], cw[NP];
+    lds_row(&S.y[tc * WL::YCS + tj * WL::NPP], part);
+    lds_row(&S.Ct[kp & 1][tj][0], cw);
+    const float y = dot_sum(part, cw);
     const int tg = kp * CK + tj, dd = dw + tc;
     const bool st = live && G::lead(lane) && tg < L && tval;
     const float o0 = y + dskv * pv.x;
@@ -543,7 +553,6 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   for (int t = 0; t < CK; ++t) {  // inert chunk k0 - 1: a - 1 = 0 (ZOH) / a = 1, b = 0
     P1.m[t] = METHOD == 0 ? 0.0f : 1.0f;
     P1.u[t] = 0.0f;
-    if constexpr (!SUM) P1.C[t] = 0.0f;
   }
   P1.x = P1.z = 0.0f;
   load(T0, k0);

@@ -60,8 +60,9 @@ __host__ __device__ constexpr int bwd_fits(int s, int np, int w) {
 __host__ __device__ constexpr int bwd_waves(int s, int np) {
   return bwd_fits(s, np, 8) ? 8 : bwd_fits(s, np, 4) ? 4 : bwd_fits(s, np, 2) ? 2 : 1;
 }
-// Wavefronts per workgroup of the float-compute backward (row tiles, NP >= 16).
-__host__ __device__ constexpr int bwdw_waves(int np) { return np <= 32 ? 8 : 4; }
+// Wavefronts per workgroup of the float-compute backward (row tiles, NP >= 16): as many as fit
+// in the 160 KiB of LDS (8 at 16 states, 4 at 32 and 64).
+__host__ __device__ constexpr int bwdw_waves(int np) { return np <= 16 ? 8 : 4; }
 // Channels per backward workgroup (= the channel tile of the dB / dC partial sums).
 inline int bwd_channels_per_block(int dtype, int np) {
   if (dtype == 3) return bwd_waves(8, np) * (64 / np);

@@ -44,6 +44,21 @@ __device__ __forceinline__ float pairwise_sum(const float (&v)[N]) {
   }
 }
 
+// Dot product of two N-vectors (N a multiple of 4) as four interleaved FMA chains over
+// j = i mod 4, added pairwise at the end: one instruction per term, four independent chains.
+template <int N>
+__device__ __forceinline__ float dot_sum(const float (&a)[N], const float (&w)[N]) {
+  static_assert(N % 4 == 0 && N >= 4, "dot_sum length");
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = a[i] * w[i];
+#pragma unroll
+  for (int j = 4; j < N; j += 4)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = fmaf(a[j + i], w[j + i], s[i]);
+  return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
 // Sum of count values at src[0], src[stride], ... in index order (the bits of a running sum),
 // the reads of G terms issued together ahead of their adds: a sum over partials in HBM is
 // otherwise a chain of dependent memory round trips.

@@ -230,6 +230,19 @@ struct WaveTile {
       S[c][t] = (t0 + t < L && c0 + c < C) ? v[i] : (CT)0;
     }
   }
+  // The same elements stored step-major ([t][c]): a lane reads one step's values of every
+  // column with 16-byte loads.
+  template <int RP>
+  __device__ __forceinline__ void store_t(CT (*S)[RP], bool tfast, int lane, int t0, int L, int c0, int C) const {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const int e = lane + i * kWave;
+      if (e >= ROWS * COLS) break;
+      int t, c;
+      tc_of<ROWS, COLS>(e, tfast, t, c);
+      S[t][c] = (t0 + t < L && c0 + c < C) ? v[i] : (CT)0;
+    }
+  }
 };
 
 // Per-lane delta bias of the tile elements a lane stages (the channel of element i of a lane is
