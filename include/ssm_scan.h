@@ -237,7 +237,8 @@ typedef struct ssm_decode_stack_args {
   float *u;                /* (B, d_model) residual stream, replaced in place */
   void *workspace;         /* device memory of ssm_decode_stack_workspace_bytes() */
   int64_t workspace_bytes;
-  const int64_t *tokens;   /* (B,) token ids on the device, or NULL */
+  const int64_t *tokens;   /* (B,) token ids on the device, or NULL; an id outside [0, vocab)
+                              reads a zero embedding row and sets the status word (below) */
   const float *embed;      /* (vocab, d_model) embedding table, read when tokens is set */
   const float *head_w4;    /* (d_model/4, vocab, 4): element [g][v][j] = W[v][4g + j] for
                               W = W_head diag(norm_f_w), or NULL (no head) */
@@ -371,6 +372,13 @@ int64_t ssm_disc_workspace_bytes(const ssm_disc_args *args);
 int64_t ssm_conv_workspace_bytes(const ssm_conv_args *args);
 int64_t ssm_norm_workspace_bytes(const ssm_norm_args *args);
 int64_t ssm_decode_stack_workspace_bytes(const ssm_decode_stack_args *args);
+/* Byte offset inside the decode-stack workspace of an int32 status word: ssm_decode_stack sets
+ * it to 1 when a token id lies outside [0, vocab) (the reference's nn.Embedding,
+ * models/lm.py:125, raises on such ids; the step itself reads a zero row and goes on).  The
+ * library never clears it: the caller zeroes it (e.g. when it allocates the workspace) and
+ * reads it when it wants to check, so the step stays free of host synchronization and can be
+ * captured in a graph.  No counterpart in the reference.  -1 for invalid dimensions. */
+int64_t ssm_decode_stack_status_offset(const ssm_decode_stack_args *args);
 
 /* Launches (asynchronous on `stream`). */
 int ssm_fwd(const ssm_fwd_args *args, void *stream);

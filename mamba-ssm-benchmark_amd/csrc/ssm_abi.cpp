@@ -709,7 +709,7 @@ int ssm_decode_step(const ssm_decode_args *a, void *stream) {
 namespace {
 struct StackLayout {
   int64_t nct, ndu, P;
-  int64_t off_ua, off_ub, off_du, off_xc, off_gate, off_part, total;
+  int64_t off_ua, off_ub, off_du, off_xc, off_gate, off_part, off_status, total;
 };
 StackLayout stack_layout(const ssm_decode_stack_args *a) {
   StackLayout l;
@@ -724,6 +724,7 @@ StackLayout stack_layout(const ssm_decode_stack_args *a) {
   l.off_xc = o; o += align256(B * Dm * 4);
   l.off_gate = o; o += align256(B * Dm * 4);
   l.off_part = o; o += align256(B * l.nct * l.P * 4);
+  l.off_status = o; o += 256;
   l.total = o;
   return l;
 }
@@ -782,6 +783,11 @@ int64_t ssm_decode_stack_workspace_bytes(const ssm_decode_stack_args *a) {
   return stack_layout(a).total;
 }
 
+int64_t ssm_decode_stack_status_offset(const ssm_decode_stack_args *a) {
+  if (!a || a->batch < 1 || a->dim < 1 || a->d_model < 1) return -1;
+  return stack_layout(a).off_status;
+}
+
 int ssm_decode_stack(const ssm_decode_stack_args *a, void *stream) {
   int rc = ssm_decode_stack_check(a);
   if (rc) return rc;
@@ -814,6 +820,7 @@ int ssm_decode_stack(const ssm_decode_stack_args *a, void *stream) {
     pi.w_in4 = k.w_in4; pi.conv_w = k.conv_w; pi.conv_b = k.conv_b; pi.x_proj_wt = k.x_proj_wt;
     pi.conv_state = k.conv_state;
     pi.xc = xc; pi.gate = gate; pi.part = part;
+    pi.bad_token = (int *)(ws + l.off_status);
     hipError_t e = launch_dec_in(pi, (int)a->width, s);
     if (e != hipSuccess) return hip_fail(e, "ssm_decode_stack in-stage launch");
     DecScanParams ps;

@@ -108,6 +108,9 @@ __global__ void __launch_bounds__(kStThreads) k_dec_in(const DecInParams p) {
     int64_t row = b;
     if (emb) row = b < B ? p.tokens[b] : -1;
     const bool rok = row >= 0 && row < (emb ? p.V : B);
+    // an id outside the vocabulary reads a zero row and raises the call's status word (a vector
+    // store from one lane of the row's wavefront; every workgroup of the row stores the same 1)
+    if (emb && b < B && !rok && lane == 0) *(volatile int *)p.bad_token = 1;
 #pragma unroll
     for (int q = 0; q < KQ; ++q) {
       const int k4 = 4 * lane + q * kStThreads;

@@ -234,6 +234,7 @@ struct DecInParams {
   const float *conv_w, *conv_b, *x_proj_wt;
   void *conv_state;
   float *xc, *gate, *part;  // (B, Dm), (B, Dm), (B, nct, P)
+  int *bad_token;           // status word: set to 1 when a token id lies outside [0, V)
 };
 struct DecScanParams {
   int B, dm, Dm, N, R, P, nrt, nct, ndu;

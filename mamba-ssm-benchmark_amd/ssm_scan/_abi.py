@@ -154,6 +154,7 @@ _SIGS = {
     "ssm_conv_workspace_bytes": (c_i64, [ctypes.POINTER(ConvArgs)]),
     "ssm_norm_workspace_bytes": (c_i64, [ctypes.POINTER(NormArgs)]),
     "ssm_decode_stack_workspace_bytes": (c_i64, [ctypes.POINTER(DecodeStackArgs)]),
+    "ssm_decode_stack_status_offset": (c_i64, [ctypes.POINTER(DecodeStackArgs)]),
     "ssm_fwd": (c_i32, [ctypes.POINTER(FwdArgs), c_vp]),
     "ssm_fwd_noalloc": (c_i32, [ctypes.POINTER(FwdArgs), c_vp]),
     "ssm_bwd": (c_i32, [ctypes.POINTER(BwdArgs), c_vp]),

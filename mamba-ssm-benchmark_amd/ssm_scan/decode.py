@@ -140,8 +140,13 @@ class FastDecoder:
         need = lib.ssm_decode_stack_workspace_bytes(ctypes.byref(a))
         key = (u.device, need)
         if key not in self._ws:
-            self._ws[key] = torch.empty(need, dtype=torch.uint8, device=u.device)
-        a.workspace, a.workspace_bytes = self._ws[key].data_ptr(), need
+            ws = torch.empty(need, dtype=torch.uint8, device=u.device)
+            off = lib.ssm_decode_stack_status_offset(ctypes.byref(a))
+            status = ws[off:off + 4].view(torch.int32)
+            status.zero_()            # the library sets it, never clears it
+            self._ws[key] = (ws, status)
+        ws = self._ws[key][0]
+        a.workspace, a.workspace_bytes = ws.data_ptr(), need
         _abi.check(lib.ssm_decode_stack(ctypes.byref(a), _abi.stream_handle(u.device)), "ssm_decode_stack")
         return logits
 
@@ -167,19 +172,43 @@ class FastDecoder:
                     and s.conv.dtype in (torch.float32, torch.bfloat16)):
                 raise ValueError("decode states must be contiguous: ssm float32, conv float32 or bf16")
 
+    def _check_ids(self, tok):
+        """The reference's nn.Embedding raises on ids outside the vocabulary (models/lm.py:125).
+        Both paths check the ids on the host before any launch (a host read of the ids)."""
+        V = self.model.embed.weight.shape[0]
+        bad = (tok < 0) | (tok >= V)
+        if bool(bad.any()):
+            raise IndexError(f"token id outside the vocabulary [0, {V}): {tok[bad].reshape(-1)[:8].tolist()}")
+
+    def bad_tokens_seen(self, clear=True):
+        """Whether a stack-path step since the last clear read a token id outside the vocabulary
+        (its embedding row read as zeros): the status word ssm_decode_stack raises on the device,
+        read here with one host synchronization; `clear` zeroes it again."""
+        seen = False
+        for _, status in self._ws.values():
+            if bool(status.item()):
+                seen = True
+                if clear:
+                    status.zero_()
+        return seen
+
     @torch.no_grad()
-    def step(self, tok, states):
+    def step(self, tok, states, check_ids=False):
         """tok (B,) or (B, 1) byte ids; states from model.init_state, contiguous, updated in
         place: the SSM state float32, the conv state float32 or bf16 (the states of a model run
         under bf16 autocast, models/mamba.py:86-91; the new conv inputs are stored rounded to
         bf16).  Returns float32 logits (B, V).  The step computes in float32 also inside a bf16
         autocast region (its results then differ from the autocast path's by the latter's bf16
-        rounding).
+        rounding).  With check_ids, ids outside the vocabulary raise IndexError before any launch
+        (one host read of the ids); without it the stack path reads a zero embedding row for
+        them and raises the status word that bad_tokens_seen() reports.
 
         The decode GEMMs are skinny (B rows); they are issued through rocBLAS, whose kernels
         for these shapes take a fraction of hipBLASLt's (torch's default), and torch's choice
         is restored afterwards."""
         self._check(tok, states)
+        if check_ids:
+            self._check_ids(tok)
         prev = torch.backends.cuda.preferred_blas_library()
         torch.backends.cuda.preferred_blas_library("cublas")   # rocBLAS on ROCm
         try:

@@ -241,13 +241,17 @@ def _stack_args(n_blocks=2):
 def test_decode_stack_workspace_layout():
     """Workspace of the stack step: two residual-stream buffers, the out_proj partial sums over
     64-channel tiles, the conv output and gate, the x_proj partial sums over 32-channel tiles,
-    each region rounded up to 256 bytes."""
+    each region rounded up to 256 bytes, then the 256-byte region of the status word (bad token
+    ids), whose offset ssm_decode_stack_status_offset reports."""
     a = _stack_args()
     r = lambda v: -(-v // 256) * 256
     B, dm, D, P = 64, 256, 512, 16 + 32
     want = 2 * r(B * dm * 4) + r(B * (D // 64) * dm * 4) + 2 * r(B * D * 4) + r(B * (D // 32) * P * 4)
-    assert a.workspace_bytes == want
+    assert a.workspace_bytes == want + 256
+    assert _abi.lib().ssm_decode_stack_status_offset(ctypes.byref(a)) == want
     assert _abi.lib().ssm_decode_stack_check(ctypes.byref(a)) == 0
+    a.batch = 0
+    assert _abi.lib().ssm_decode_stack_status_offset(ctypes.byref(a)) == -1
 
 
 @pytest.mark.parametrize("field,value", [("d_model", 513), ("dim", 1025), ("dstate", 12), ("dt_rank", 24),

@@ -563,7 +563,9 @@ def test_decode_stack_token_outside_vocabulary_reads_zero_row(dev):
     """A token id outside [0, vocab) reads a zero embedding row in the stack path (the reference's
     embedding raises instead): the step equals the step of a model whose row 7 is zero, given
     token 7 there: states, and the logits of every other vocabulary entry (the head is tied to the
-    embedding)."""
+    embedding).  Such a step raises the device status word that bad_tokens_seen() reports (a step
+    with valid ids does not), and step(check_ids=True) raises IndexError before any launch on
+    both paths, as the reference's nn.Embedding does (models/lm.py:125)."""
     from ssm_scan.decode import FastDecoder
     torch.manual_seed(31)
     model = MambaLM(n_layers=2).to(dev).eval()
@@ -574,12 +576,23 @@ def test_decode_stack_token_outside_vocabulary_reads_zero_row(dev):
     s1 = _random_states(model, 6, dev, 32)
     s2 = _clone(s1)
     tok = torch.tensor([3, 300, -1, 5, 255, 1 << 40], device=dev)
-    got = FastDecoder(model, path="stack").step(tok, s1)
-    ref = FastDecoder(zeroed, path="stack").step(torch.tensor([3, 7, 7, 5, 255, 7], device=dev), s2)
+    fast, fast_zeroed = FastDecoder(model, path="stack"), FastDecoder(zeroed, path="stack")
+    got = fast.step(tok, s1)
+    ref = fast_zeroed.step(torch.tensor([3, 7, 7, 5, 255, 7], device=dev), s2)
     keep = torch.arange(got.shape[1], device=dev) != 7
     assert torch.equal(got[:, keep], ref[:, keep])
     for a, b_ in zip(s1, s2):
         assert torch.equal(a.ssm, b_.ssm) and torch.equal(a.conv, b_.conv)
+    assert fast.bad_tokens_seen() and not fast.bad_tokens_seen()    # reported once, then cleared
+    assert not fast_zeroed.bad_tokens_seen()
+    fast.step(torch.tensor([3, 7, 0, 5, 255, 9], device=dev), s1)
+    assert not fast.bad_tokens_seen()
+    for path in ("stack", "block"):
+        before = _clone(s1)
+        with pytest.raises(IndexError):
+            FastDecoder(model, path=path).step(tok, s1, check_ids=True)
+        for a, b_ in zip(s1, before):                                # nothing ran
+            assert torch.equal(a.ssm, b_.ssm) and torch.equal(a.conv, b_.conv)
 
 
 def test_decode_stack_limits_fall_back_to_blocks(dev):
@@ -605,8 +618,10 @@ def test_fast_decoder_bf16_conv_state(dev, shape):
     float64 restatement whose conv state is rounded to bf16 after every update the same way.
 
     The rounding of a conv input to bf16 may fall on the other side of a rounding boundary in
-    float64 than in float32 (rarely); the tolerance is the north_star's bf16 bar (rtol 2e-2,
-    atol 2e-2 x max|.|), and the count of elements outside the float32 bar is printed."""
+    float64 than in float32 (rarely): a flipped input moves the logits by ~1e-5 absolute, which
+    is outside the bf16 bar (rtol 2e-2 / atol 1e-5) only for logits near zero -- measured 0-2 of
+    4,096 per token, so up to 4 per token may sit outside it; the states are held to the bar
+    with none outside, and the count outside the float32 bar is printed."""
     from ssm_scan.decode import FastDecoder
     from parity import close, outside
     torch.manual_seed(21)
@@ -634,7 +649,7 @@ def test_fast_decoder_bf16_conv_state(dev, shape):
             r["conv"] = r["conv"].to(torch.bfloat16).double()
         scale = float(ref.abs().max())
         print(f"token {t}: logits outside the float32 bar: {outside(got, ref, 1e-4, 1e-5 * scale)}", flush=True)
-        close(got, ref, rtol=2e-2, atol=2e-2 * scale, name=f"logits token {t}")
+        close(got, ref, rtol=2e-2, atol=1e-5, name=f"logits token {t}", allow=4)
     for i, (s_, r) in enumerate(zip(states, rstates)):
-        close(s_.ssm, r["ssm"], rtol=2e-2, atol=2e-2, name=f"layer {i} ssm state")
-        close(s_.conv.float(), r["conv"], rtol=2e-2, atol=2e-2, name=f"layer {i} conv state")
+        close(s_.ssm, r["ssm"], rtol=2e-2, atol=1e-5, name=f"layer {i} ssm state")
+        close(s_.conv.float(), r["conv"], rtol=2e-2, atol=1e-5, name=f"layer {i} conv state")
