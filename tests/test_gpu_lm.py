@@ -51,7 +51,10 @@ def lm_close(got, ref, name, rtol=1e-4, atol_rel=1e-5, allow_literal=0):
     return lit
 
 
-def check_lm_grads(model, p, allow_literal=None):
+def check_lm_grads(model, p, allow_literal=0):
+    """Every parameter gradient against the float64 reference: the literal bar with no element
+    outside it, and the LM bar (rtol 1e-3, atol 1e-4 x max|grad|), the stricter one for
+    gradients whose largest element is below 0.1."""
     named = dict(model.named_parameters())
     assert len(named) == len([k for k in p if k != "head.weight"])
     for name, prm in named.items():
@@ -82,7 +85,8 @@ def test_config3_lm_train_step_matches_reference(dev):
     this size the mixer node (ssm_scan.mixer) and the split-K weight gradients
     (ssm_scan.linear, from 2,048 tokens) run, as in the benchmark.  Against oracle/lm_ref in
     float64 with each layer's scan on the C oracle's forward and adjoint: logits, loss and
-    every parameter gradient at the LM bar, with per-tensor literal-bar counts printed."""
+    every parameter gradient at the literal bar with none outside (and at the LM bar); the
+    per-tensor counts are printed."""
     model = build(0).to(dev)
     g = torch.Generator().manual_seed(41)
     data = torch.randint(0, 256, (16, 513), generator=g)
