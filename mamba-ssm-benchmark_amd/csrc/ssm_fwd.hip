@@ -448,12 +448,15 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
 
   // Iteration k: stage chunk k (inert past k1: zero inputs, a = 1, b = 0) and compute its
   // independent per-step values into `nx`, interleaved with the serial updates of chunk k - 1
-  // from `pv` (inert before k0); then the outputs of chunk k - 1.
-  auto iter = [&](Tiles &T, int k, ST &pv, ST &nx) {
+  // from `pv` (inert before k0); then the outputs of chunk k - 1.  FULL iterations (the
+  // caller checks: k0 < k < k1, chunk k wholly inside the sequence, N = NP, every channel of
+  // the wavefront real) drop the range selects of the staging and of the stores.
+  auto iter = [&](auto full, Tiles &T, int k, ST &pv, ST &nx) {
+    constexpr bool F = decltype(full)::value;
     const int t0 = k * CK;
-    const int Lc = k < k1 ? L : 0;
-    const bool ev = t0 + tj < Lc && tval;  // the row-tile element is a real (step, channel)
-    T.B.store(S.B, bt, lane, t0, Lc, 0, N);
+    const int Lc = F || k < k1 ? L : 0;
+    const bool ev = F || (t0 + tj < Lc && tval);  // the row-tile element is a real (step, channel)
+    T.B.template store<!F>(S.B, bt, lane, t0, Lc, 0, N);
     nx.x = ev ? T.x.v : 0.0f;
     nx.z = T.z.v;
     float dv;
@@ -476,7 +479,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     wave_lds_sync();
     // chunk k's C (read by the next iteration's output phase) beside chunk k - 1's (read by
     // this one's), before the tile registers are refilled
-    if (!SUM) T.C.store_t(S.Ct[k & 1], ctt, lane, t0, Lc, 0, N);
+    if (!SUM) T.C.template store_t<!F>(S.Ct[k & 1], ctt, lane, t0, Lc, 0, N);
     load(T, k + 2);
     float rB[CK];
     lds_row(&S.B[n][0], rB);
@@ -520,7 +523,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
       return;
     }
     const int kp = k - 1;  // the chunk whose outputs are now complete
-    const bool live = kp >= k0 && kp < k1;
+    const bool live = F || (kp >= k0 && kp < k1);
     wave_lds_sync();
     // outputs of chunk k - 1: the lane of (step tj, channel tc) forms sum_n C[tj][n] h[tj][tc][n]
     // (four interleaved FMA chains, added pairwise)
@@ -529,12 +532,12 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     lds_row(&S.Ct[kp & 1][tj][0], cw);
     const float y = dot_sum(part, cw);
     const int tg = kp * CK + tj, dd = dw + tc;
-    const bool st = live && G::lead(lane) && tg < L && tval;
+    const bool st = F ? G::lead(lane) : live && G::lead(lane) && tg < L && tval;
     const float o0 = y + dskv * pv.x;
     const float o = p.has_z ? o0 * (pv.z * sigmoidf(pv.z)) : o0;
     if constexpr (UL) {  // branch-free: masked lanes store out of range (dropped)
-      const uint32_t kpc = (uint32_t)(kp < 0 ? 0 : kp);
-      buf_store<float>(rbk, offK + kpc * (uint32_t)(p.D * NP * 4), dval && live, h);
+      const uint32_t kpc = (uint32_t)(F || kp >= 0 ? kp : 0);
+      buf_store<float>(rbk, offK + kpc * (uint32_t)(p.D * NP * 4), F || (dval && live), h);
       buf_store<float>(rby, offY + kpc * tstepY, st, o0);
       buf_store<IT>(rbo, offO + kpc * (uint32_t)(CK * (int)vout.s1 * ES), st, o);
     } else {
@@ -557,9 +560,22 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   P1.x = P1.z = 0.0f;
   load(T0, k0);
   load(T1, k0 + 1);
-  for (int k = k0; k <= k1; k += 2) {
-    iter(T0, k, P1, P0);
-    iter(T1, k + 1, P0, P1);
+  const std::integral_constant<bool, false> ranged;
+  const std::integral_constant<bool, true> full;
+  iter(ranged, T0, k0, P1, P0);
+  int k = k0 + 1;
+  if constexpr (UL) {
+    // pairs of whole chunks strictly inside the segment, every lane's state and channel real
+    const int kf = min(k1, L / CK);
+    if (p.N == NP && p.D % (WPB * CW) == 0)
+      for (; k + 1 < kf; k += 2) {
+        iter(full, T1, k, P0, P1);
+        iter(full, T0, k + 1, P1, P0);
+      }
+  }
+  for (; k <= k1; k += 2) {
+    iter(ranged, T1, k, P0, P1);
+    iter(ranged, T0, k + 1, P1, P0);
   }
 
   if constexpr (SUM) {

@@ -219,7 +219,9 @@ struct WaveTile {
     for (int i = 0; i < E; ++i) v[i] = buf_load<IT>(r, off[i] + toff);
   }
 
-  template <int RP>
+  // Elements past the row's extent (t0 + t >= L or c0 + c >= C) are stored as 0; with RANGE
+  // false the caller guarantees the whole tile lies inside (no range selects).
+  template <bool RANGE = true, int RP>
   __device__ __forceinline__ void store(CT (*S)[RP], bool tfast, int lane, int t0, int L, int c0, int C) const {
 #pragma unroll
     for (int i = 0; i < E; ++i) {
@@ -227,12 +229,12 @@ struct WaveTile {
       if (e >= ROWS * COLS) break;
       int t, c;
       tc_of<ROWS, COLS>(e, tfast, t, c);
-      S[c][t] = (t0 + t < L && c0 + c < C) ? v[i] : (CT)0;
+      S[c][t] = (!RANGE || (t0 + t < L && c0 + c < C)) ? v[i] : (CT)0;
     }
   }
   // The same elements stored step-major ([t][c]): a lane reads one step's values of every
   // column with 16-byte loads.
-  template <int RP>
+  template <bool RANGE = true, int RP>
   __device__ __forceinline__ void store_t(CT (*S)[RP], bool tfast, int lane, int t0, int L, int c0, int C) const {
 #pragma unroll
     for (int i = 0; i < E; ++i) {
@@ -240,7 +242,7 @@ struct WaveTile {
       if (e >= ROWS * COLS) break;
       int t, c;
       tc_of<ROWS, COLS>(e, tfast, t, c);
-      S[t][c] = (t0 + t < L && c0 + c < C) ? v[i] : (CT)0;
+      S[t][c] = (!RANGE || (t0 + t < L && c0 + c < C)) ? v[i] : (CT)0;
     }
   }
 };
