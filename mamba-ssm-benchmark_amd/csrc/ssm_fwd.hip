@@ -401,10 +401,9 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   uint32_t offB[EB];
   tile_offsets<CK, NP>(offB, vB, 0, bt, lane, ES);
   const __amdgpu_buffer_rsrc_t empty = __builtin_amdgcn_make_buffer_rsrc((void *)p.x.p, (short)0, 0, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rbx = row_buffer(vx, b, L, D, ES);
-  const __amdgpu_buffer_rsrc_t rbdt = LR ? empty : row_buffer(vdt, b, L, D, ES);
-  const __amdgpu_buffer_rsrc_t rbz = row_buffer(vzl, b, L, D, ES);
-  const __amdgpu_buffer_rsrc_t rbB = row_buffer(vB, b, L, N, ES), rbC = row_buffer(vC, b, L, N, ES);
+  // the input rows, read through a window at each chunk (the chunk's offset in scalar registers)
+  const RowWin rwx = row_win(vx, b, L, D, ES), rwdt = row_win(LR ? vx : vdt, b, L, D, ES);
+  const RowWin rwz = row_win(vzl, b, L, D, ES), rwB = row_win(vB, b, L, N, ES), rwC = row_win(vC, b, L, N, ES);
   __amdgpu_buffer_rsrc_t rblr = empty;
   uint32_t offLR = 0, tstepLR = 0;
   bool rvLR = false;
@@ -432,11 +431,11 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     if constexpr (LR) T.lr.load(rblr, offLR + (uint32_t)(t0 * (int)p.dtl.s1 * ES), tstepLR, rvLR);
     if constexpr (UL) {
       const uint32_t tx_ = (uint32_t)(t0 * (int)vx.s1 * ES), tb_ = (uint32_t)(t0 * (int)vB.s1 * ES);
-      T.x.load_buf(rbx, offX, tx_);
-      if constexpr (!LR) T.dt.load_buf(rbdt, offX, tx_);
-      T.B.load_buf(rbB, offB, tb_);
-      if (!SUM) T.C.load_buf(rbC, offB, tb_);
-      if (!SUM) T.z.load_buf(rbz, offZ, (uint32_t)(t0 * (int)vzl.s1 * ES));
+      T.x.load_buf(rwx.at(tx_), offX, 0u);
+      if constexpr (!LR) T.dt.load_buf(rwdt.at(tx_), offX, 0u);
+      T.B.load_buf(rwB.at(tb_), offB, 0u);
+      if (!SUM) T.C.load_buf(rwC.at(tb_), offB, 0u);
+      if (!SUM) T.z.load_buf(rwz.at((uint32_t)(t0 * (int)vzl.s1 * ES)), offZ, 0u);
     } else {
       T.x.load(vx, b, t0, L, dw, D, lane);
       if constexpr (!LR) T.dt.load(vdt, b, t0, L, dw, D, lane);
@@ -451,8 +450,9 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   // from `pv` (inert before k0); then the outputs of chunk k - 1.  FULL iterations (the
   // caller checks: k0 < k < k1, chunk k wholly inside the sequence, N = NP, every channel of
   // the wavefront real) drop the range selects of the staging and of the stores.
-  auto iter = [&](auto full, Tiles &T, int k, ST &pv, ST &nx) {
+  auto iter = [&](auto full, auto slot, Tiles &T, int k, ST &pv, ST &nx) {
     constexpr bool F = decltype(full)::value;
+    constexpr int SL = decltype(slot)::value;  // the tiles' slot: chunks alternate between the two
     const int t0 = k * CK;
     const int Lc = F || k < k1 ? L : 0;
     const bool ev = F || (t0 + tj < Lc && tval);  // the row-tile element is a real (step, channel)
@@ -478,8 +478,8 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     const float xv = nx.x;
     wave_lds_sync();
     // chunk k's C (read by the next iteration's output phase) beside chunk k - 1's (read by
-    // this one's), before the tile registers are refilled
-    if (!SUM) T.C.template store_t<!F>(S.Ct[k & 1], ctt, lane, t0, Lc, 0, N);
+    // this one's, in the other tiles' slot), before the tile registers are refilled
+    if (!SUM) T.C.template store_t<!F>(S.Ct[SL], ctt, lane, t0, Lc, 0, N);
     load(T, k + 2);
     float rB[CK];
     lds_row(&S.B[n][0], rB);
@@ -529,17 +529,19 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     // (four interleaved FMA chains, added pairwise)
     float part[NP], cw[NP];
     lds_row(&S.y[tc * WL::YCS + tj * WL::NPP], part);
-    lds_row(&S.Ct[kp & 1][tj][0], cw);
+    lds_row(&S.Ct[1 - SL][tj][0], cw);
     const float y = dot_sum(part, cw);
     const int tg = kp * CK + tj, dd = dw + tc;
     const bool st = F ? G::lead(lane) : live && G::lead(lane) && tg < L && tval;
     const float o0 = y + dskv * pv.x;
     const float o = p.has_z ? o0 * (pv.z * sigmoidf(pv.z)) : o0;
     if constexpr (UL) {  // branch-free: masked lanes store out of range (dropped)
+      // the chunk's offset is the stores' scalar offset: a masked lane's vector offset lies
+      // past every buffer, and the stores of the other lanes lie inside their rows
       const uint32_t kpc = (uint32_t)(F || kp >= 0 ? kp : 0);
-      buf_store<float>(rbk, offK + kpc * (uint32_t)(p.D * NP * 4), F || (dval && live), h);
-      buf_store<float>(rby, offY + kpc * tstepY, st, o0);
-      buf_store<IT>(rbo, offO + kpc * (uint32_t)(CK * (int)vout.s1 * ES), st, o);
+      buf_store_s<float>(rbk, offK, kpc * (uint32_t)(p.D * NP * 4), F || (dval && live), h);
+      buf_store_s<float>(rby, offY, kpc * tstepY, st, o0);
+      buf_store_s<IT>(rbo, offO, kpc * (uint32_t)(CK * (int)vout.s1 * ES), st, o);
     } else {
       if (p.ckpt && dval && live) ((float *)p.ckpt)[((b * p.nchunks + kp) * p.D + d) * NP + n] = h;
       if (st) {
@@ -562,20 +564,22 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   load(T1, k0 + 1);
   const std::integral_constant<bool, false> ranged;
   const std::integral_constant<bool, true> full;
-  iter(ranged, T0, k0, P1, P0);
+  const std::integral_constant<int, 0> s0;
+  const std::integral_constant<int, 1> s1;
+  iter(ranged, s0, T0, k0, P1, P0);
   int k = k0 + 1;
   if constexpr (UL) {
     // pairs of whole chunks strictly inside the segment, every lane's state and channel real
     const int kf = min(k1, L / CK);
     if (p.N == NP && p.D % (WPB * CW) == 0)
       for (; k + 1 < kf; k += 2) {
-        iter(full, T1, k, P0, P1);
-        iter(full, T0, k + 1, P1, P0);
+        iter(full, s1, T1, k, P0, P1);
+        iter(full, s0, T0, k + 1, P1, P0);
       }
   }
   for (; k <= k1; k += 2) {
-    iter(ranged, T1, k, P0, P1);
-    iter(ranged, T0, k + 1, P1, P0);
+    iter(ranged, s1, T1, k, P0, P1);
+    iter(ranged, s0, T0, k + 1, P1, P0);
   }
 
   if constexpr (SUM) {

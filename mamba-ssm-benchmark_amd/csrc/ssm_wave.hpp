@@ -169,6 +169,22 @@ struct RowRef {
     return __builtin_amdgcn_make_buffer_rsrc((void *)b, (short)0, ext, kBufferFlags);
   }
 };
+// A row buffer read through windows that start a uniform byte offset into the row: a read at
+// offset o of the window at `off` lands at row offset off + o and returns 0 past the row's extent,
+// as through the whole row's buffer, while the chunk's offset costs a few scalar instructions
+// (the window's base and extent) instead of a vector add per read.
+struct RowWin {
+  const char *base;
+  int ext;
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t at(uint32_t off) const {
+    const int rem = ext - (int)off;
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + off), (short)0, rem > 0 ? rem : 0, kBufferFlags);
+  }
+};
+__device__ __forceinline__ RowWin row_win(const KView &V, int64_t b, int L, int C, int esize) {
+  const int64_t ext = ((int64_t)(L - 1) * V.s1 + (int64_t)(C - 1) * V.s2 + 1) * esize;
+  return RowWin{(const char *)V.p + b * V.s0 * esize, (int)ext};
+}
 __device__ __forceinline__ RowRef row_ref(const KView &V, int64_t b, int L, int C, int esize) {
   const int64_t ext = ((int64_t)(L - 1) * V.s1 + (int64_t)(C - 1) * V.s2 + 1) * esize;
   return RowRef{(const char *)V.p + b * V.s0 * esize, (int)ext};
