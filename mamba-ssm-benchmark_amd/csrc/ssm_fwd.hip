@@ -450,9 +450,17 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   // from `pv` (inert before k0); then the outputs of chunk k - 1.  FULL iterations (the
   // caller checks: k0 < k < k1, chunk k wholly inside the sequence, N = NP, every channel of
   // the wavefront real) drop the range selects of the staging and of the stores.
+  // Issue priority.  Two wavefronts that share a SIMD would run oldest-first: the older ends
+  // several microseconds before the younger, which then runs alone to the end of the launch with
+  // its latencies exposed.  Each wavefront instead takes the higher priority in alternate windows
+  // of 512 ticks (5.12 us) of the 100 MHz real-time counter, by the parity of its wave slot on the
+  // SIMD (HW_ID bits 3:0), so a pair progresses evenly and ends together.
+  const unsigned slot_par = __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 4) & 1u;
   auto iter = [&](auto full, auto slot, Tiles &T, int k, ST &pv, ST &nx) {
     constexpr bool F = decltype(full)::value;
     constexpr int SL = decltype(slot)::value;  // the tiles' slot: chunks alternate between the two
+    if (((((unsigned)__builtin_amdgcn_s_memrealtime()) >> 9) ^ slot_par) & 1u) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
     const int t0 = k * CK;
     const int Lc = F || k < k1 ? L : 0;
     const bool ev = F || (t0 + tj < Lc && tval);  // the row-tile element is a real (step, channel)
