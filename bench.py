@@ -744,14 +744,24 @@ def cpu_baseline_scans(B, L, M, gpu_ms, budget_s=10.0, m_sample=2048):
 
 
 def bench_copy(args, dev):
-    """A plain device copy of 256 MiB (reads 256 MiB, writes 256 MiB): PMC calibration."""
+    """A plain device copy of 256 MiB (reads 256 MiB, writes 256 MiB): PMC calibration, and the
+    read + write bandwidth a plain copy reaches (the practical ceiling of the HBM-bound kernels)."""
     src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
-    for _ in range(args.warmup + args.steps):
+    for _ in range(args.warmup):
         dst.copy_(src)
     torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    gbs = 2 * src.numel() * 4 / (ms * 1e-3) / 1e9
     return {"metric": "device copy 256 MiB (PMC calibration)", "value": 256.0, "unit": "MiB",
-            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup}
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_copy": ms,
+            "read_write_GBps": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS}
 
 
 def c1_extras(args, dev):

@@ -27,8 +27,10 @@
 // by the adjoint) the multiplier at a step is the a of the previous step in processing order
 // and 1 for the first step: lambda_t = g_t + a_{t+1} lambda_{t+1} (models/scan.py:239-240).
 #include "ssm_device.hpp"
+#include "ssm_dpp.hpp"
 #include "ssm_internal.hpp"
 #include "ssm_tiles.hpp"
+#include "ssm_wave.hpp"
 
 namespace ssm {
 
@@ -105,6 +107,84 @@ __global__ void __launch_bounds__(kSeqThreads) k_lscan_seq(const LscanParams P) 
     run(a0, b0, pos, L - pos);
     run(a1, b1, pos + K, L - pos - K);
   }
+}
+
+// Sequential, float, unit stride along m: the same walk with the reads and writes moved through
+// LDS tiles.  A wavefront owns 64 consecutive recurrences m of one batch row and walks 16-step
+// blocks.  A block's a and b tiles (16 steps x 64 recurrences) are read with 16-byte loads -- a
+// lane reads 4 recurrences of one step, so one load instruction carries 4 steps where a read per
+// recurrence carries one -- and transposed through LDS so that each lane walks its own
+// recurrence; the block's states go back through LDS and leave as 16-byte stores.  With at most
+// 63 memory instructions outstanding per wavefront, that puts ~4x the bytes of the one-lane-per-
+// recurrence walk in flight.  Reads run kSeqTAhead blocks ahead, at clamped positions (past the
+// end: re-reads of the last step, never used).
+constexpr int kSeqTB = 16, kSeqTAhead = 3;
+typedef float f32x4 __attribute__((ext_vector_type(4)));  // a native vector (HIP's float4 is a struct)
+
+__global__ void __launch_bounds__(64) k_lscan_seqt(const LscanParams P) {
+  __shared__ __align__(16) float sA[kSeqTB][64], sB[kSeqTB][64], sH[kSeqTB][64];
+  const int lane = threadIdx.x;
+  const int64_t b = blockIdx.y, m0 = (int64_t)blockIdx.x * 64;
+  const int L = (int)P.L;
+  const int rl = lane / 16, cl = (lane % 16) * 4;  // the lane's row in a group of 4 steps, its column
+  Chain<float> ch{P, b, m0 + lane};
+  float h = ch.h0();
+  const float *pa = (const float *)P.a.p + b * P.a.s0 + m0 + cl;
+  const float *pb = (const float *)P.b.p + b * P.b.s0 + m0 + cl;
+  float *ph = (float *)P.h.p + b * P.h.s0 + m0 + cl;
+  struct Blk {
+    f32x4 a[kSeqTB / 4], b[kSeqTB / 4];
+  };
+  auto fetch = [&](Blk &k, int pos0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kSeqTB / 4; ++j) {
+      const int pos = min(pos0 + rl + 4 * j, L - 1);
+      const int apos = P.shift ? max(pos - 1, 0) : pos;  // the shifted multiplier (the adjoint's)
+      k.a[j] = *(const f32x4 *)(pa + (int64_t)ch.t_of(apos) * P.a.s1);
+      k.b[j] = *(const f32x4 *)(pb + (int64_t)ch.t_of(pos) * P.b.s1);
+    }
+  };
+  auto run = [&](const Blk &k, int pos0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kSeqTB / 4; ++j) {
+      *(f32x4 *)&sA[rl + 4 * j][cl] = k.a[j];
+      *(f32x4 *)&sB[rl + 4 * j][cl] = k.b[j];
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int r = 0; r < kSeqTB; ++r) {
+      const float a = (P.shift && pos0 + r == 0) ? 1.0f : sA[r][lane];
+      h = fmaf(a, h, sB[r][lane]);
+      sH[r][lane] = h;
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int j = 0; j < kSeqTB / 4; ++j) {
+      const int pos = pos0 + rl + 4 * j;
+      const f32x4 v = *(const f32x4 *)&sH[rl + 4 * j][cl];
+      if (pos < L) *(f32x4 *)(ph + (int64_t)ch.t_of(pos) * P.h.s1) = v;
+    }
+    wave_lds_sync();  // the next block's tiles reuse the LDS
+  };
+  Blk k[kSeqTAhead];
+  static_for<0, kSeqTAhead>([&](auto icst) { fetch(k[decltype(icst)::value], decltype(icst)::value * kSeqTB); });
+  for (int pos = 0; pos < L; pos += kSeqTAhead * kSeqTB) {
+    // blocks past the end are skipped (their reads, clamped, are never used)
+    static_for<0, kSeqTAhead>([&](auto icst) {
+      constexpr int i = decltype(icst)::value;
+      if (pos + i * kSeqTB < L) run(k[i], pos + i * kSeqTB);
+      fetch(k[i], pos + (i + kSeqTAhead) * kSeqTB);
+    });
+  }
+}
+
+// The tiled walk's conditions: float, every view with unit stride along m and 16-byte aligned
+// rows, M a multiple of 64.
+static bool seqt_ok(const LscanParams &P) {
+  auto ok = [](const KView &v) {
+    return v.s2 == 1 && v.s1 % 4 == 0 && v.s0 % 4 == 0 && ((uintptr_t)v.p % 16) == 0;
+  };
+  return P.M % 64 == 0 && ok(P.a) && ok(P.b) && ok(P.h);
 }
 
 // Tiled parallel scans: a workgroup of 256 lanes owns kScanMC recurrences m (lane % 64) of one
@@ -424,6 +504,10 @@ static hipError_t launch_lscan_t(const LscanParams &P, int algo, hipStream_t s) 
   const int64_t chains = P.B * P.M;
   switch (algo) {
     case 1:
+      if (sizeof(CT) == 4 && seqt_ok(P)) {
+        hipLaunchKernelGGL(k_lscan_seqt, dim3((unsigned)(P.M / 64), (unsigned)P.B), dim3(64), 0, s, P);
+        break;
+      }
       hipLaunchKernelGGL((k_lscan_seq<CT>), dim3((unsigned)((chains + kSeqThreads - 1) / kSeqThreads)),
                          dim3(kSeqThreads), 0, s, P);
       break;

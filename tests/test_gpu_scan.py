@@ -184,6 +184,53 @@ def test_scan_adjoint_matches_oracle(dev, name, with_h0):
             close(hz.grad, dh0, dtype, "dh0")
 
 
+@pytest.mark.parametrize("L", [1, 7, 16, 47, 48, 49, 300, 1031])
+@pytest.mark.parametrize("with_h0", [False, True])
+def test_sequential_tiled_walk_matches_oracle(dev, L, with_h0):
+    """float32 with M a multiple of 64 takes the tiled sequential walk (16-step blocks of 64
+    recurrences read with 16-byte loads and transposed through LDS, three blocks of reads
+    ahead): forward and reverse against the oracle at every L around the block and read-ahead
+    boundaries; the same values in a view whose rows are not 16-byte aligned take the
+    one-lane-per-recurrence walk and agree with it bit for bit."""
+    f = torch.float32
+    a, b, h0 = ab_inputs((2, L, 128), seed=L + 7)
+    h0 = h0 if with_h0 else None
+    ra, rb, rh = rnd(a, f), rnd(b, f), rnd(h0, f)
+    hz = None if h0 is None else h0.to(dev, f)
+    got = S.scan_sequential(a.to(dev, f), b.to(dev, f), hz)
+    close(got, R.scan_sequential(ra, rb, rh), f, "tiled")
+    refr = np.flip(R.scan_sequential(np.flip(ra, 1), np.flip(rb, 1), rh), 1)
+    gotr = S.LinearScanFn.apply(a.to(dev, f), b.to(dev, f), hz, 1, None, True)
+    close(gotr, refr, f, "tiled reverse")
+    aw = torch.zeros(2, L, 129, dtype=f, device=dev)
+    bw = torch.zeros(2, L, 129, dtype=f, device=dev)
+    aw[..., 1:] = a.to(dev, f)
+    bw[..., 1:] = b.to(dev, f)
+    assert aw[..., 1:].stride(1) % 4 != 0
+    assert torch.equal(S.scan_sequential(aw[..., 1:], bw[..., 1:], hz), got)
+
+
+@pytest.mark.parametrize("with_h0", [False, True])
+def test_sequential_tiled_adjoint_matches_oracle(dev, with_h0):
+    """The adjoint scan (shifted multipliers, reverse direction) through the tiled walk: float32
+    at M = 64."""
+    f = torch.float32
+    a, b, h0 = ab_inputs((2, 301, 64), seed=19)
+    g = torch.Generator().manual_seed(20)
+    dh = torch.randn(2, 301, 64, generator=g, dtype=torch.float64)
+    leaves = [a.to(dev, f).requires_grad_(), b.to(dev, f).requires_grad_()]
+    hz = h0.to(dev, f).requires_grad_() if with_h0 else None
+    h = S.scan_sequential(leaves[0], leaves[1], hz)
+    h.backward(dh.to(dev, f))
+    ra, rh0 = rnd(a, f), rnd(h0, f) if with_h0 else None
+    href = R.scan_sequential(ra, rnd(b, f), rh0)
+    da, db, dh0 = R.scan_vjp(ra, rh0, href, rnd(dh, f))
+    close(leaves[0].grad, da, f, "da")
+    close(leaves[1].grad, db, f, "db")
+    if with_h0:
+        close(hz.grad, dh0, f, "dh0")
+
+
 def test_reverse_scan_and_errors(dev):
     a, b, h0 = ab_inputs((2, 50, 3), seed=13)
     ref = np.flip(R.scan_sequential(np.flip(np64(a), 1), np.flip(np64(b), 1), np64(h0)), 1)
