@@ -58,6 +58,53 @@ __global__ void __launch_bounds__(kThreads) k_disc_fwd(const DiscParams p) {
   }
 }
 
+// The float forward with 16-byte stores: a lane owns 4 consecutive states (n .. n+3) of one
+// channel (N a multiple of 4), so a store instruction writes 1 KB of an output row where a lane
+// per element wrote 256 B: 4x the bytes behind each outstanding memory instruction of the
+// write-dominated pass.  B's 4 values of a row arrive as one 16-byte read.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kDiscQuadGroups = 64;  // row groups in the grid's y dimension (each walks L / (64 x 8))
+
+template <int METHOD>
+__global__ void __launch_bounds__(kThreads) k_disc_fwd4(const DiscParams p) {
+  const int e4 = blockIdx.x * kThreads + threadIdx.x;  // the lane's quad within a (b, t) row
+  const int DN4 = (int)(p.D * p.N / 4), N4 = (int)(p.N / 4);
+  if (e4 >= DN4) return;
+  const int n0 = (e4 % N4) * 4, d = e4 / N4;
+  const int L = (int)p.L;
+  AConst<float> ac[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ac[j] = make_aconst(vload<float>(p.A, d * p.A.s0 + (n0 + j) * p.A.s1));
+  for (int64_t b = blockIdx.z; b < p.B; b += gridDim.z) {
+    for (int t0 = blockIdx.y * kDiscRows; t0 < L; t0 += gridDim.y * kDiscRows) {
+      float dt[kDiscRows], xv[kDiscRows];
+      f32x4 Bv[kDiscRows];
+#pragma unroll
+      for (int k = 0; k < kDiscRows; ++k) {  // clamped rows past the end are read, not stored
+        const int64_t t = min(t0 + k, L - 1);
+        dt[k] = vload<float>(p.delta, b * p.delta.s0 + t * p.delta.s1 + d * p.delta.s2);
+        xv[k] = vload<float>(p.x, b * p.x.s0 + t * p.x.s1 + d * p.x.s2);
+        Bv[k] = *(const f32x4 *)((const float *)p.Bm.p + b * p.Bm.s0 + t * p.Bm.s1 + n0);
+      }
+#pragma unroll
+      for (int k = 0; k < kDiscRows; ++k) {
+        if (t0 + k >= L) break;
+        f32x4 av, bv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float a, coef;
+          disc<METHOD>(dt[k], ac[j], a, coef);
+          av[j] = a;
+          bv[j] = bcoef<METHOD>(dt[k], coef) * (Bv[k][j] * xv[k]);
+        }
+        const int64_t i = (b * p.L + t0 + k) * DN4 + e4;
+        ((f32x4 *)p.a)[i] = av;
+        ((f32x4 *)p.b)[i] = bv;
+      }
+    }
+  }
+}
+
 template <typename CT, int NP, int METHOD>
 __global__ void __launch_bounds__(kThreads) k_disc_bwd(const DiscParams p) {
   constexpr int DT = kThreads / NP;
@@ -187,9 +234,16 @@ __global__ void __launch_bounds__(kThreads) k_disc_fin(const DiscParams p) {
 template <typename CT, int M>
 static hipError_t disc_fwd_t(const DiscParams &p, hipStream_t s) {
   const int64_t ty = (p.L + kDiscRows - 1) / kDiscRows;
-  const dim3 grid((unsigned)((p.D * p.N + kThreads - 1) / kThreads), (unsigned)(ty < 65535 ? ty : 65535),
+  // 16-byte stores: float, N a multiple of 4, B contiguous along n with 16-byte aligned rows
+  const bool quads = sizeof(CT) == 4 && p.N % 4 == 0 && p.Bm.s2 == 1 && p.Bm.s1 % 4 == 0 && p.Bm.s0 % 4 == 0 &&
+                     (uintptr_t)p.Bm.p % 16 == 0 && (uintptr_t)p.a % 16 == 0 && (uintptr_t)p.b % 16 == 0;
+  const int64_t lanes = quads ? p.D * p.N / 4 : p.D * p.N;
+  // the 16-byte kernel walks several row groups per workgroup (fewer, longer wavefronts)
+  const int64_t tymax = quads ? kDiscQuadGroups : 65535;
+  const dim3 grid((unsigned)((lanes + kThreads - 1) / kThreads), (unsigned)(ty < tymax ? ty : tymax),
                   (unsigned)(p.B < 65535 ? p.B : 65535));
-  hipLaunchKernelGGL((k_disc_fwd<CT, M>), grid, dim3(kThreads), 0, s, p);
+  if (quads) hipLaunchKernelGGL((k_disc_fwd4<M>), grid, dim3(kThreads), 0, s, p);
+  else hipLaunchKernelGGL((k_disc_fwd<CT, M>), grid, dim3(kThreads), 0, s, p);
   return hipGetLastError();
 }
 

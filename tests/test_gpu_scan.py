@@ -61,14 +61,16 @@ def ab_inputs(shape, seed=0, lo=0.05, hi=0.95):
 # ------------------------------------------------------------------ discretization
 @pytest.mark.parametrize("method", R.DISCRETIZATIONS)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_discretize_forward_and_vjp(dev, method, dtype):
-    x, delta, A, Bm, _, _ = sel_inputs(B=2, L=37, D=21, N=5, seed=1, h0=False)
+@pytest.mark.parametrize("N", [5, 16])
+def test_discretize_forward_and_vjp(dev, method, dtype, N):
+    """N = 16 in float32 takes the forward with 16-byte stores (a lane per 4 states)."""
+    x, delta, A, Bm, _, _ = sel_inputs(B=2, L=37, D=21, N=N, seed=1, h0=False)
     g = torch.Generator().manual_seed(2)
-    ga = torch.randn(2, 37, 21, 5, generator=g, dtype=torch.float64)
-    gb = torch.randn(2, 37, 21, 5, generator=g, dtype=torch.float64)
+    ga = torch.randn(2, 37, 21, N, generator=g, dtype=torch.float64)
+    gb = torch.randn(2, 37, 21, N, generator=g, dtype=torch.float64)
     leaves = [t.to(dev, dtype).requires_grad_() for t in (delta, A, Bm, x)]
     a, b = S.discretize(*leaves, method=method)
-    assert a.shape == (2, 37, 21, 5) and a.dtype == dtype
+    assert a.shape == (2, 37, 21, N) and a.dtype == dtype
     ins = [rnd(t, dtype) for t in (delta, A, Bm, x)]
     ra, rb = R.discretize(*ins, method)
     close(a.detach(), ra, dtype, "a")
