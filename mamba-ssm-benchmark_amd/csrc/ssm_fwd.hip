@@ -304,7 +304,10 @@ __global__ void __launch_bounds__(kThreads) k_fwd_carry(const FwdParams p) {
 //     and the C h partials pass through LDS;
 //   * the chunk loop is software-pipelined: iteration k runs the serial state updates of chunk
 //     k - 1 interleaved step by step with the independent per-step work of chunk k (exp,
-//     expm1, B x), so most instructions have their operands ready when they issue.
+//     expm1, B x), so most instructions have their operands ready when they issue;
+//   * chunks wholly inside the sequence run a copy of the loop body without range selects, and
+//     the chunk's inputs are read through windows of the row buffers that start at the chunk
+//     (its offset in scalar registers, not one vector add per read).
 // The output y_t = sum_n C_t[n] h_t[n] is formed by the lanes that store it: the state lanes
 // put h_t itself into LDS and the (step, channel) lane takes the dot product with the step's C
 // row (C staged step-major), one FMA per state where a product per state lane and an add
@@ -317,7 +320,7 @@ template <int NP>
 struct FwdwLds {
   static constexpr int CW = kWave / NP, CKP = ck_pad(4), NPP = np_pad(4, NP), YCS = kCK * NPP + 16;
   float B[NP][CKP];
-  float Ct[2][kCK][NPP];  // C of the chunk, step-major, by chunk parity
+  float Ct[2][kCK][NPP];  // C of the chunk, step-major, one per register set of the pipeline
   float y[CW * YCS];      // the chunk's states h_t at [c * YCS + t * NPP + n]
   float lr[kCK][lr_pad(4)];  // low-rank delta input rows of the chunk
   float wr[CW][lr_pad(4)];   // low-rank weight rows of the wavefront's channels
