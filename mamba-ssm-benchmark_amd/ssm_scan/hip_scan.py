@@ -19,7 +19,7 @@ import ctypes
 import torch
 
 from . import _abi
-from .linear import weight_grad
+from .linear import rocblas, weight_grad
 from .profiling import timed_launch
 
 ZOH, EULER, BILINEAR = 0, 1, 2
@@ -218,8 +218,9 @@ class FusedSelectiveScanFn(torch.autograd.Function):
             # the projection's gradients: the two small GEMMs of F.linear's backward, in torch
             ct = ctx.settings[3]
             ddc = dd.to(ct)
-            dW = weight_grad(ddc.reshape(-1, ddc.shape[-1]), ds.to(ct).reshape(-1, Wv.shape[1]))
-            dd = torch.matmul(ddc, Wv)
+            with rocblas():
+                dW = weight_grad(ddc.reshape(-1, ddc.shape[-1]), ds.to(ct).reshape(-1, Wv.shape[1]))
+                dd = torch.matmul(ddc, Wv)
         grads = [dx, dd, dA, dB, dC, dD, dz, db, dh0]
         out = []
         for g, dt in zip(grads, ctx.in_dtypes):

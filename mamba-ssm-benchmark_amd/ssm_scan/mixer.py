@@ -16,7 +16,7 @@ import torch.nn.functional as F
 
 from .conv import conv_backward, conv_forward
 from .hip_scan import LOWRANK_MAX, METHODS, scan_backward, scan_forward
-from .linear import weight_grad
+from .linear import rocblas, weight_grad
 
 
 class MixerFn(torch.autograd.Function):
@@ -28,7 +28,8 @@ class MixerFn(torch.autograd.Function):
         x, z = xz[..., :Dm], xz[..., Dm:]
         w2 = conv_w.reshape(conv_w.shape[0], conv_w.shape[-1])
         xc = conv_forward(x, w2, conv_b, True)
-        proj = F.linear(xc, xproj_w)
+        with rocblas():
+            proj = F.linear(xc, xproj_w)
         dt, Bm, Cm = proj[..., :R], proj[..., R:R + N], proj[..., R + N:]
         need = any(ctx.needs_input_grad)
         y, _, (tensors, settings) = scan_forward(xc, dt, A_log, Bm, Cm, Dv, z, dt_bias, None, method, True, 0,
@@ -53,11 +54,12 @@ class MixerFn(torch.autograd.Function):
                                                         dB=dproj[..., R:R + N], dC=dproj[..., R + N:])
         dd2 = dd.reshape(-1, Dm)
         dt2 = proj.reshape(-1, P)[:, :R]
-        dW_dt = weight_grad(dd2, dt2)                       # dt_proj weight (D, R)
-        dproj[..., :R] = (dd2 @ Wdt).view(dd.shape[:-1] + (R,))
-        dproj2 = dproj.view(-1, P)
-        dxc2 = torch.addmm(dxc.reshape(-1, Dm), dproj2, xproj_w).view(xc.shape)
-        dW_x = weight_grad(dproj2, xc.reshape(-1, Dm))      # x_proj weight (P, D)
+        with rocblas():
+            dW_dt = weight_grad(dd2, dt2)                       # dt_proj weight (D, R)
+            dproj[..., :R] = (dd2 @ Wdt).view(dd.shape[:-1] + (R,))
+            dproj2 = dproj.view(-1, P)
+            dxc2 = torch.addmm(dxc.reshape(-1, Dm), dproj2, xproj_w).view(xc.shape)
+            dW_x = weight_grad(dproj2, xc.reshape(-1, Dm))      # x_proj weight (P, D)
         _, dwc, dbc = conv_backward(xz[..., :Dm], w2, conv_b, dxc2, True, dx=dxz[..., :Dm])
         return dxz, dwc.view(ctx.conv_shape), dbc, dW_x, dW_dt, db, dA, dD, None
 
