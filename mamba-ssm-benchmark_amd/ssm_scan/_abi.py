@@ -223,5 +223,34 @@ def view(t):
     return v
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device):
+    """The raw handle of torch's current stream on `device`, which the launches are enqueued on
+    (read without building a torch.cuda.Stream object: this is on every launch's host path)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
+
+
+class on_device:
+    """The engine launches on the current device: make `device` current for the block, and
+    skip torch.cuda.device's two device exchanges when it already is (the usual case)."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, device):
+        self.idx = device.index
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        self.prev = cur if self.idx is not None and self.idx != cur else None
+        if self.prev is not None:
+            torch.cuda.set_device(self.idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False

@@ -31,7 +31,7 @@ def _args(x, weight, bias, activation):
 
 
 def _launch(name, fn, args, dev):
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         rc = fn(ctypes.byref(args), _abi.stream_handle(dev))
     _abi.check(rc, name)
 

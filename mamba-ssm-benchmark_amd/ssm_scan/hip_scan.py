@@ -132,7 +132,7 @@ def scan_forward(x, delta, A, Bm, Cm, D, z, delta_bias, h0, method, delta_softpl
         _abi.check(0 if nbytes >= 0 else 1, "ssm_fwd_saved_bytes")
         saved = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
         args.saved = saved.data_ptr()
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         stream = _abi.stream_handle(dev)
         rc = timed_launch("ssm_fwd", stream, lambda: lib.ssm_fwd(ctypes.byref(args), stream))
     _abi.check(rc, "ssm_fwd")
@@ -182,7 +182,7 @@ def scan_backward(tensors, settings, dout, dlast, dz=None, dB=None, dC=None):
         _abi.check(lib.ssm_bwd_check(ctypes.byref(args)), "ssm_bwd")
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         stream = _abi.stream_handle(dev)
         rc = timed_launch("ssm_bwd", stream, lambda: lib.ssm_bwd(ctypes.byref(args), stream))
     _abi.check(rc, "ssm_bwd")

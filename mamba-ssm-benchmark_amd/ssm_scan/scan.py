@@ -52,7 +52,7 @@ def _ct(*ts):
 
 
 def _launch(name, fn, args, dev):
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         stream = _abi.stream_handle(dev)
         rc = timed_launch(name, stream, lambda: fn(ctypes.byref(args), stream))
     _abi.check(rc, name)

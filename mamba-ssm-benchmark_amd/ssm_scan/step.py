@@ -47,7 +47,7 @@ def ssm_step(h, x, delta, A, Bm, Cm, D=None, z=None, delta_bias=None, delta_soft
     args.delta_softplus = 1 if delta_softplus else 0
     args.h, args.out = _abi.view(h), _abi.view(out)
     lib = _abi.lib()
-    with torch.cuda.device(x.device):
+    with _abi.on_device(x.device):
         rc = lib.ssm_step(ctypes.byref(args), _abi.stream_handle(x.device))
     _abi.check(rc, "ssm_step")
     return out if out.dtype == x.dtype else out.to(x.dtype)
