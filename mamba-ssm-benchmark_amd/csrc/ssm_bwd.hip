@@ -552,9 +552,10 @@ __global__ void __launch_bounds__(256) k_bwd_finalize(const FinParams p) {
 // adjoint carried into it.  A summary pass (SUM) gives each segment's zero-start adjoint at its
 // first step times that step's decay (E) and the product of its decays (P); k_bwd_carry turns
 // them into the adjoint entering every segment, the reverse of the forward's segment carry.
-// (dx, ddelta) terms of half a chunk at [c * PCS + (t * 2 + q) * NPP + n]: the 16 lanes of a
-// 16-byte read phase (one channel's 8 steps x 2 quantities) read 16 consecutive rows, and a
-// channel block is padded by 16 floats so the state lanes' writes fall on 64 distinct banks.
+// (dx, ddelta) terms of half a chunk at [c * PCS + (t * 2 + q) * NPP + n]: a channel block is
+// padded by 16 floats, so the two channels of a half-wavefront write 32 distinct banks.  (Reads
+// of the rows in the forward's conflict-free order, with the reducers remapped to match, took
+// 4 extra cycles fewer per 16-byte read and no less time: this kernel is not bound by LDS.)
 template <int NP, bool LR>
 struct BwdwLds {
   static constexpr int CW = kWave / NP, CKP = ck_pad(4), NPP = np_pad(4, NP), RH = 8, PCS = 2 * RH * NPP + 16;
@@ -573,7 +574,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   constexpr int CW = G::CW, CK = kCK, RH = WL::RH, WPB = bwdw_waves(NP), NT = WPB * kWave;
   constexpr bool M1 = METHOD == 0;
   // (dB, dC) of half a chunk for every channel of the workgroup, by half: rows of CH channels
-  // padded to CHP (16-byte reads; the lanes of one write hit distinct banks).  The state lanes
+  // padded to CHP (rows 16-byte aligned for the reducers' reads).  The state lanes
   // write their factors -- dB_t[n] = sum_c (lambda cf)_t[c][n] x_t[c] and dC_t[n] = sum_c
   // h_t[c][n] dy_t[c] -- and after a barrier TPI threads form each (step, quantity, state)
   // row's dot product with the step's x or dy row (staged per chunk, by chunk parity), IPT

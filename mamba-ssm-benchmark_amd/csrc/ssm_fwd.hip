@@ -313,15 +313,15 @@ __global__ void __launch_bounds__(kThreads) k_fwd_carry(const FwdParams p) {
 // row (C staged step-major), one FMA per state where a product per state lane and an add
 // would be two instructions.
 // NP >= 16 (a smaller dstate is padded to 16).
-// The states go in channel-major ([c][t][n], rows of NPP): the 16 lanes of one 16-byte read
-// phase (the steps of one channel) read 16 consecutive rows, and a channel block is padded by
-// 16 floats so the state lanes' writes (4 channels x 16 states) fall on 64 distinct banks.
+// The states go in channel-major ([c][step_row(t)][n], rows of NPP): a channel block is padded
+// by 16 floats, so the two channels of a half-wavefront write 32 distinct banks, and step_row
+// orders the rows so that a 16-byte read phase (steps of two channels) hits distinct banks.
 template <int NP>
 struct FwdwLds {
   static constexpr int CW = kWave / NP, CKP = ck_pad(4), NPP = np_pad(4, NP), YCS = kCK * NPP + 16;
   float B[NP][CKP];
   float Ct[2][kCK][NPP];  // C of the chunk, step-major, one per register set of the pipeline
-  float y[CW * YCS];      // the chunk's states h_t at [c * YCS + t * NPP + n]
+  float y[CW * YCS];      // the chunk's states h_t at [c * YCS + step_row(t) * NPP + n]
   float lr[kCK][lr_pad(4)];  // low-rank delta input rows of the chunk
   float wr[CW][lr_pad(4)];   // low-rank weight rows of the wavefront's channels
 };
@@ -514,7 +514,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
         h = fmaf(pv.m[t], h, pv.u[t]);
         if constexpr (SUM) prod *= pv.m[t];
       }
-      if constexpr (!SUM) S.y[c * WL::YCS + t * WL::NPP + n] = h;
+      if constexpr (!SUM) S.y[c * WL::YCS + step_row(t) * WL::NPP + n] = h;
       // independent values of chunk k
       const float dtb = row_bcast<t>(dvs);
       const float bxr = rB[t] * row_bcast<t>(xvs);
@@ -539,7 +539,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     // outputs of chunk k - 1: the lane of (step tj, channel tc) forms sum_n C[tj][n] h[tj][tc][n]
     // (four interleaved FMA chains, added pairwise)
     float part[NP], cw[NP];
-    lds_row(&S.y[tc * WL::YCS + tj * WL::NPP], part);
+    lds_row(&S.y[tc * WL::YCS + step_row(tj) * WL::NPP], part);
     lds_row(&S.Ct[1 - SL][tj][0], cw);
     const float y = dot_sum(part, cw);
     const int tg = kp * CK + tj, dd = dw + tc;

@@ -31,6 +31,14 @@ inline int fused_np(int64_t n, int dtype) {
 // which spreads the lanes of a read over distinct banks.
 __host__ __device__ constexpr int ck_pad(int s) { return kCK + 16 / s; }
 __host__ __device__ constexpr int np_pad(int s, int np) { return np + 16 / s; }
+// gfx950 LDS (measured): a wavefront's 32-bit accesses go in 32-lane halves over 32 banks; its
+// 16-byte reads go in 16-lane phases over 64 banks, a phase being lanes {0-3, 12-15, 20-23,
+// 24-27} or {4-11, 16-19, 28-31} of a half (the same 32 higher).  When the two channels of a
+// half-wavefront each read 16 step rows of np_pad floats at a channel-block stride of 16 rows +
+// 16 floats, a phase reads steps {0-3, 12-15} of one channel and {4-11} of the other; this row
+// order puts those 16 rows on 16 distinct 16-byte bank groups (the natural order puts 4 pairs on
+// one group: 4 extra cycles per read).  Row of step t among a chunk's 16 step rows:
+__host__ __device__ constexpr int step_row(int t) { return 4 * (t % 4) + (t < 4 ? 2 : t < 8 ? 0 : t < 12 ? 1 : 3); }
 // Low-rank delta (the dt_proj GEMM fused into the staging): a chunk's (CK, R <= kLR) input
 // rows and the wavefront's channels' weight rows, padded like the other LDS rows.
 constexpr int kLR = 16;
