@@ -92,6 +92,19 @@ def test_random_configuration_cancellation_within_float32_resolution(dev, seed):
     run_case(dev, seed, cancel_allow=2)
 
 
+# A wider sweep, 2,000 draws (seeds 2000-3999): 17 draws with one or two such elements and one,
+# seed 3086 (N = 64, bilinear, B2 L333: 64-term state sums), with four ddelta elements at
+# 0.07-0.37e-6 of their terms' magnitudes (100-200); none outside the rule otherwise.
+WIDE_SWEEP_CANCELLING = tuple((s, 2) for s in (2008, 2077, 2215, 2237, 2555, 2572, 2724, 2752, 2812, 2897, 3045,
+                                              3556, 3562, 3599, 3769, 3926, 3961)) + ((3086, 4),)
+
+
+@pytest.mark.parametrize("seed,allow", WIDE_SWEEP_CANCELLING)
+def test_random_configuration_wide_sweep_cancellation(dev, seed, allow):
+    """The wide sweep's draws that need the cancellation rule, each at its own count."""
+    run_case(dev, seed, cancel_allow=allow)
+
+
 def run_case(dev, seed, cancel_allow=None):
     cfg = draw(seed)
     print(f"case seed={seed} {cfg}", flush=True)
