@@ -164,7 +164,11 @@ __global__ void __launch_bounds__(kThreads) k_disc_bwd(const DiscParams p) {
   CT *const dds = (CT *)p.ddelta.p, *const dxs = (CT *)p.dx.p;
   CT *wsB = (CT *)p.ws_dB + (r0 * p.dtiles + tile) * p.N;
   const int64_t wstep = p.dtiles * p.N;
-  CT gA = 0;
+  // dA sums one term per row over the group's rows (hundreds): each read-ahead group of rows is
+  // summed in CT and folded into a float64 running sum, so the rounding does not grow with the
+  // number of rows
+  double gA = 0;
+  CT gA4 = 0;
   auto row = [&](const Row &cur, int buf) {
     CT gd = 0, gx = 0, gB = 0;
     if (valid) {
@@ -173,7 +177,7 @@ __global__ void __launch_bounds__(kThreads) k_disc_bwd(const DiscParams p) {
       dfactors<METHOD>(cur.dt, ac, a, coef, dadz, dbdd, d2f);
       const CT bx = cur.B * cur.x, gz = cur.ga * dadz, gbc = cur.gb * bcoef<METHOD>(cur.dt, coef);
       gd = fma(ac.A, gz, cur.gb * dbdd * bx);
-      gA += fma(cur.dt, gz, cur.gb * d2f * bx);
+      gA4 += fma(cur.dt, gz, cur.gb * d2f * bx);
       gx = gbc * cur.B;
       gB = gbc * cur.x;
     }
@@ -212,8 +216,10 @@ __global__ void __launch_bounds__(kThreads) k_disc_bwd(const DiscParams p) {
       q[k] = fetch_next();
       row(cur, k & 1);
     }
+    gA += (double)gA4;
+    gA4 = 0;
   }
-  if (valid) ((CT *)p.ws_dA)[(g * p.D + d) * p.N + n] = gA;
+  if (valid) ((CT *)p.ws_dA)[(g * p.D + d) * p.N + n] = (CT)gA;
 }
 
 template <typename CT>
@@ -226,8 +232,8 @@ __global__ void __launch_bounds__(kThreads) k_disc_fin(const DiscParams p) {
     vstore<CT>(p.dBm, b * p.dBm.s0 + t * p.dBm.s1 + n * p.dBm.s2, s);
   } else if (i < nB + nA) {
     const int64_t j = i - nB, n = j % p.N, d = j / p.N;
-    const CT s = ordered_sum<16>((const CT *)p.ws_dA + j, nA, p.ngroups);
-    vstore<CT>(p.dA, d * p.dA.s0 + n * p.dA.s1, s);
+    const double s = ordered_sum<16, CT, double>((const CT *)p.ws_dA + j, nA, p.ngroups);  // float64 sum
+    vstore<CT>(p.dA, d * p.dA.s0 + n * p.dA.s1, (CT)s);
   }
 }
 

@@ -176,7 +176,7 @@ struct DiscParams {
   void *a, *b;
   const void *da, *db;
   void *ws_dB;  // (B*L, dtiles, N) partial sums over each channel tile
-  void *ws_dA;  // (ngroups, D, N) partial sums over each group of rows
+  void *ws_dA;  // (ngroups, D, N) partial sums over each group of rows (float64 running sums)
 };
 
 // Causal depthwise conv over (B, L, D) views; a lane owns (b, d, one block of TB steps).

@@ -62,18 +62,20 @@ __device__ __forceinline__ float dot_sum(const float (&a)[N], const float (&w)[N
 // Sum of count values at src[0], src[stride], ... in index order (the bits of a running sum),
 // the reads of G terms issued together ahead of their adds: a sum over partials in HBM is
 // otherwise a chain of dependent memory round trips.
-template <int G, typename CT>
-__device__ inline CT ordered_sum(const CT *src, int64_t stride, int64_t count) {
-  CT s = 0;
+// ST: the running sum's type (a float64 sum of float32 partials keeps a long sum's rounding from
+// growing with the count).
+template <int G, typename CT, typename ST = CT>
+__device__ inline ST ordered_sum(const CT *src, int64_t stride, int64_t count) {
+  ST s = 0;
   int64_t k = 0;
   for (; k + G <= count; k += G) {
     CT v[G];
 #pragma unroll
     for (int u = 0; u < G; ++u) v[u] = src[(k + u) * stride];
 #pragma unroll
-    for (int u = 0; u < G; ++u) s += v[u];
+    for (int u = 0; u < G; ++u) s += (ST)v[u];
   }
-  for (; k < count; ++k) s += src[k * stride];
+  for (; k < count; ++k) s += (ST)src[k * stride];
   return s;
 }
 

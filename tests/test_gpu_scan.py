@@ -338,3 +338,56 @@ def test_composed_backward_is_deterministic(dev):
         runs.append([t.grad.clone() for t in leaves])
     for g1, g2 in zip(*runs):
         assert torch.equal(g1, g2)
+
+
+def run_composed_case(dev, seed, cancel_allow=None):
+    """A random draw of the composed path: shape, algorithm, discretization, dtype, h0, dlast,
+    channel tile and chunk size, against the float64 oracle (every output and gradient)."""
+    rng = np.random.default_rng(seed)
+    B, L, D = int(rng.integers(1, 4)), int(rng.integers(1, 400)), int(rng.integers(1, 40))
+    N = int(rng.integers(1, 20))
+    algo = ALGOS[int(rng.integers(0, 4))]
+    method = R.DISCRETIZATIONS[int(rng.integers(0, 3))]
+    dtype = (torch.float32, torch.float64)[int(rng.integers(0, 2))]
+    with_h0, with_dlast = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+    d_block = int(rng.integers(1, D + 1)) if rng.integers(0, 2) else None
+    chunk = int(rng.integers(1, 80)) if algo == "chunked" and rng.integers(0, 2) else None
+    print(f"case seed={seed} B{B} L{L} D{D} N{N} {algo} {method} {dtype} h0={with_h0} dlast={with_dlast} "
+          f"d_block={d_block} chunk={chunk}", flush=True)
+    ins = sel_inputs(B=B, L=L, D=D, N=N, seed=seed, h0=with_h0)
+    g = torch.Generator().manual_seed(seed + 1)
+    dy = torch.randn(B, L, D, generator=g, dtype=torch.float64)
+    dlast = torch.randn(B, D, N, generator=g, dtype=torch.float64) if with_dlast else None
+    leaves = [None if t is None else t.to(dev, dtype).requires_grad_() for t in ins]
+    y, last = S.selective_scan(*leaves, method=method, scan=algo, d_block=d_block, chunk_size=chunk)
+    loss = (y * dy.to(dev, dtype)).sum()
+    if dlast is not None:
+        loss = loss + (last * dlast.to(dev, dtype)).sum()
+    loss.backward()
+    ry, rlast, rg = _oracle_sel(ins, method, dy, dlast, dtype)
+    close(y.detach(), ry, dtype, "y")
+    close(last.detach(), rlast, dtype, "last")
+    for name, t in zip(("dx", "ddelta", "dA", "dB", "dC", "dh0"), leaves):
+        if t is None:
+            continue
+        if name == "dA" and cancel_allow is not None:
+            x, delta, A, Bm, Cm, h0 = (rnd(v, dtype) for v in ins)
+            mag = R.selective_scan_bwd(x, delta, A, Bm, Cm, rnd(dy, dtype), h0, method, dlast=rnd(dlast, dtype),
+                                       mag=True)["dA_mag"]
+            parity.close_or_cancelled(t.grad, rg["dA"], mag, "dA", allow=cancel_allow)
+        else:
+            close(t.grad, rg[name], dtype, name)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_composed_matches_oracle(dev, seed):
+    run_composed_case(dev, seed)
+
+
+# A 500-draw sweep (seeds 0-499) left one or two float32 dA elements outside the bar in these
+# three draws (errors 1e-7 - 4e-7 of their terms' magnitudes; the sequential algorithm leaves the
+# same ones); three more did while dA's per-workgroup row sums ran in float32, none since they
+# run in float64.
+@pytest.mark.parametrize("seed", (104, 135, 267))
+def test_random_composed_cancellation_within_float32_resolution(dev, seed):
+    run_composed_case(dev, seed, cancel_allow=2)
