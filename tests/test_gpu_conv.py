@@ -133,3 +133,33 @@ def test_conv_errors(dev):
         causal_conv1d(x, torch.zeros(7, 4, device=dev))
     with pytest.raises(RuntimeError):
         causal_conv1d(x.cpu(), torch.zeros(8, 4))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shapes_forward_backward_match_torch(dev, seed):
+    """Seeded random shapes (B 1-4, L 1-599, D 1-299, W 1-8), activation, bias and the split
+    in_proj view, float32 against torch float64 autograd: y and dx at the float32 conv bar, the
+    weight and bias gradients (sums over B x L tokens) at rtol 1e-4 / atol 1e-5.  A 300-draw
+    sweep of the same draws had none outside."""
+    rng = np.random.default_rng(seed)
+    B, L, D, W = int(rng.integers(1, 5)), int(rng.integers(1, 600)), int(rng.integers(1, 300)), int(rng.integers(1, 9))
+    act, with_bias, split = bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+    print(f"case seed={seed} B={B} L={L} D={D} W={W} activation={act} bias={with_bias} split={split}", flush=True)
+    x, w, bias = inputs(B, L, D, W, seed=seed, split_view=split)
+    if not with_bias:
+        bias = None
+    xg, wg = x.to(dev, torch.float32).requires_grad_(), w.to(dev, torch.float32).requires_grad_()
+    bg = None if bias is None else bias.to(dev, torch.float32).requires_grad_()
+    y = causal_conv1d(xg, wg, bg, activation=act)
+    dy = torch.randn(B, L, D, generator=torch.Generator().manual_seed(seed + 1), dtype=torch.float64)
+    (y * dy.to(dev, torch.float32)).sum().backward()
+    xr, wr = x.clone().requires_grad_(), w.clone().requires_grad_()
+    br = None if bias is None else bias.clone().requires_grad_()
+    (ref_conv(xr, wr, br, activation=act) * dy).sum().backward()
+    rt, at = TOL[torch.float32]
+    yr = ref_conv(x, w, bias, activation=act)
+    np.testing.assert_allclose(np64(y), yr.numpy(), rtol=rt, atol=at, err_msg="y")
+    np.testing.assert_allclose(np64(xg.grad), xr.grad.numpy(), rtol=rt, atol=at, err_msg="dx")
+    np.testing.assert_allclose(np64(wg.grad), wr.grad.numpy(), rtol=1e-4, atol=1e-5, err_msg="dw")
+    if bg is not None:
+        np.testing.assert_allclose(np64(bg.grad), br.grad.numpy(), rtol=1e-4, atol=1e-5, err_msg="dbias")
