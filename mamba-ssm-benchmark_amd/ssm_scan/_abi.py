@@ -208,19 +208,17 @@ def check(rc, what):
         raise _ERRORS.get(rc, RuntimeError)(f"{what}: {msg}")
 
 
+_ABSENT = Tensor()  # null data, zero strides; an argument struct copies it on assignment
+
+
 def view(t):
     """ssm_tensor for a torch tensor (None -> absent); strides in elements, padded to 3."""
-    v = Tensor()
     if t is None:
-        v.data = None
-        return v
-    if t.dim() > 3:
+        return _ABSENT
+    st = t.stride()
+    if len(st) > 3:
         raise ValueError(f"expected a tensor of at most 3 dims, got shape {tuple(t.shape)}")
-    v.data = t.data_ptr()
-    st = list(t.stride()) + [0, 0, 0]
-    for i in range(3):
-        v.stride[i] = st[i]
-    return v
+    return Tensor(t.data_ptr(), st + (0,) * (3 - len(st)))
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
