@@ -619,6 +619,10 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   float lamf = (float)lam;
   float m_next = M1 ? 0.0f : 1.0f;  // a - 1 (ZOH) or a of the step after the current one
   float prod = 1.0f;                // summary: product of the segment's decays
+  // summary, ZOH and Euler: that product is exp(A sum_t delta_t), from the lanes' row-tile
+  // deltas added once per chunk (float64) and summed over the row at the end
+  constexpr bool PSUM = SUM && METHOD != 2;
+  double dsum = 0.0;
   float h0v = 0.0f;
   if (!SUM && p.has_h0 && dval && nval) h0v = vload<float>(p.h0, b * p.h0.s0 + d * p.h0.s1 + n * p.h0.s2);
   // dA sums every step of the sequence: each chunk's 16 terms in float32, the chunk sums in
@@ -784,6 +788,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
       dv = softplusf(dv);
     }
     dv = ev ? dv : 0.0f;
+    if constexpr (PSUM) dsum += (double)dv;
     // dy = dout silu(z); dz = dout (y + D x) silu'(z) from the saved pre-gate output
     const float g0 = ev ? T.g.v : 0.0f;
     float dyv = g0;
@@ -854,8 +859,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
         lamf = (float)lam;
         m_next = am[t];
         if constexpr (SUM) {
-          if constexpr (M1) prod = fmaf(am[t], prod, prod);
-          else prod *= am[t];
+          if constexpr (!PSUM) prod *= am[t];
         } else {
           const float dtb = row_bcast<t>(dvw);
           float cf, pD;
@@ -950,6 +954,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   const double lam_a = M1 ? lam + (double)m_next * lam : lam * (double)m_next;
   const BwdParams &q = params_here<BwdParams>();  // fields read after the loop are loaded here
   if constexpr (SUM) {
+    if constexpr (PSUM) prod = fast_exp2((float)((double)ac.A2 * row_sum_f64(dsum)));
     if (dval && nval) {
       ((double *)q.seg_E)[sidx] = lam_a;
       ((float *)q.seg_P)[sidx] = prod;

@@ -45,6 +45,22 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
+// The same row sum in float64 (the two halves of each value move by the same DPP pattern).
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, 0xF, 0xF, false);
+  const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ double row_sum_f64(double v) {
+  v += dpp_d<0xB1>(v);
+  v += dpp_d<0x4E>(v);
+  v += dpp_d<0x141>(v);
+  v += dpp_d<0x140>(v);
+  return v;
+}
+
 // Scheduling ties (no instructions): `order_after(a, b)` makes the compiler treat `a` as
 // rewritten from `b`, so every later use of `a` is scheduled after `b` is computed.  The
 // software-pipelined kernels use them to keep a serial recurrence interleaved step by step

@@ -366,6 +366,11 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   }
   const AConst<float> ac = make_aconst(Av);
   float h = 0.0f, prod = 1.0f;
+  // Summary pass, ZOH and Euler: the decay product is exp(A sum_t delta_t) -- the lane adds its
+  // row-tile delta once per chunk (float64) and the row's 16 lanes are summed at the end,
+  // instead of one product per step and state (bilinear keeps the product)
+  constexpr bool PSUM = SUM && METHOD != 2;
+  double dsum = 0.0;
   const int64_t sidx = ((b * p.nseg + seg) * p.D + d) * NP + n;  // (B, nseg, D, NP) summaries
   if (!SUM && dval && nval) {
     if (p.nseg > kFoldSegs) {
@@ -486,6 +491,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     dv += biasv;
     if (p.softplus) dv = softplusf(dv);
     dv = ev ? dv : 0.0f;  // padded steps: delta 0 is the identity step
+    if constexpr (PSUM) dsum += (double)dv;
     const float xv = nx.x;
     wave_lds_sync();
     // chunk k's C (read by the next iteration's output phase) beside chunk k - 1's (read by
@@ -509,10 +515,9 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
       // serial update of chunk k - 1 (ZOH: h <- h + (a - 1)(h + B x / A))
       if constexpr (METHOD == 0) {
         h = fmaf(pv.m[t], h + pv.u[t], h);
-        if constexpr (SUM) prod = fmaf(pv.m[t], prod, prod);
       } else {
         h = fmaf(pv.m[t], h, pv.u[t]);
-        if constexpr (SUM) prod *= pv.m[t];
+        if constexpr (SUM && !PSUM) prod *= pv.m[t];
       }
       if constexpr (!SUM) S.y[c * WL::YCS + step_row(t) * WL::NPP + n] = h;
       // independent values of chunk k
@@ -594,6 +599,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   }
 
   if constexpr (SUM) {
+    if constexpr (PSUM) prod = fast_exp2((float)((double)ac.A2 * row_sum_f64(dsum)));
     if (dval && nval) {
       ((float *)p.seg_P)[sidx] = prod;
       ((float *)p.seg_E)[sidx] = h;
