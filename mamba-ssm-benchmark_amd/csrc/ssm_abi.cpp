@@ -111,22 +111,75 @@ bool saved_rows_fit(const FwdLayout &f, int64_t L, int64_t D, int dtype) {
   return (int64_t)f.nchunks * D * f.np * state_size(dtype) < lim && L * D * state_size(dtype) < lim;
 }
 
-// Time segments, shared by the forward and the backward: one unless the B x ceil(D /
-// channels-per-wavefront) wavefronts leave the GPU short of work (fewer than kSegEnough); then
-// enough segments for about kSegTarget wavefronts, each at least kSegMinChunks chunks long.  A
-// positive `requested` overrides the choice (clamped to the valid range).
-constexpr int64_t kSegEnough = 2048, kSegTarget = 6144, kSegMinChunks = 4;
+// Time segments.  A pass launches W = B x ceil(D / channels-per-wavefront) wavefronts per
+// segment; each segment after the first also costs a summary pass over its chunks, so segments
+// pay only while they supply wavefronts the GPU would otherwise lack.  The automatic count
+// minimises a cost model of MI355X's 1,024 SIMDs: the busiest SIMD holds ceil(W x nseg / 1,024)
+// wavefronts, `cap` at a time, and runs them in rounds, each round as long as one wavefront's walk
+// over its segment at that round's occupancy.  The constants are fitted to kernel times of the
+// float32 N = 16 kernels at D 512 over forced counts (B 1-16 at L 512, B1 at L 4,096-131,072,
+// B2-8 at L 1,024-65,536; at each shape the model's pick is within 2 % of the fastest count
+// measured): the backward's wavefronts walk nearly as fast two to a SIMD as alone
+// (latency-bound), so a partly filled extra round costs a whole walk (B1 L65536: 16, 32 and 48
+// segments 1.16-1.18 ms, 24 segments 1.52 ms); the forward keeps its SIMDs busy from 2
+// wavefronts on, so it segments less at short lengths (B8 L512: one segment 39 us, 2 segments
+// 45 us, 6 segments 53 us).  Segments are at least kSegMinChunks chunks long; a positive
+// `requested` overrides the choice (clamped to the valid range).
+constexpr int64_t kSimds = 1024, kSegMinChunks = 4;
+
+struct PassModel {
+  int cap;             // wavefronts per SIMD that the kernel's registers and LDS allow
+  double lat[3];       // a wavefront's time per chunk with 1..cap wavefronts on its SIMD
+  double summary;      // the summary pass's time per chunk relative to the main pass's
+  double per_wave;     // a wavefront's start and end, in chunks
+  double fixed;        // a segmented pass's extra launches and carry, in chunks
+  double per_segment;  // folding one more segment's summary, in chunks
+};
+
+constexpr PassModel kFwdModel{3, {1.0, 1.2, 1.63}, 0.5, 1.0, 8.0, 1.0};
+constexpr PassModel kBwdModel{2, {1.0, 1.04, 0.0}, 0.37, 0.0, 4.0, 0.0};
+
+double walk_cost(const PassModel &m, int64_t waves, int64_t chunks) {
+  const int64_t w = cdiv(waves, kSimds), full = w / m.cap, rest = w % m.cap;
+  return ((double)full * m.lat[m.cap - 1] + (rest ? m.lat[rest - 1] : 0.0)) * ((double)chunks + m.per_wave);
+}
+
+double plan_cost(const PassModel &m, int64_t waves, int64_t nchunks, int64_t n) {
+  const int64_t sc = cdiv(nchunks, n), ns = cdiv(nchunks, sc);
+  double c = walk_cost(m, waves * ns, sc);
+  if (ns > 1) c += m.summary * walk_cost(m, waves * (ns - 1), sc) + m.fixed + m.per_segment * (double)ns;
+  return c;
+}
 
 struct SegPlan {
   int nseg, seg_chunks;
 };
 
-SegPlan seg_plan(int64_t B, int64_t D, const FwdLayout &f, int requested) {
+SegPlan seg_plan(int64_t B, int64_t D, const FwdLayout &f, int requested, bool backward) {
   SegPlan s;
   const int64_t waves = B * cdiv(D, 64 / f.np);
   int64_t n = 1;
-  if (requested > 0) n = requested;
-  else if (waves < kSegEnough) n = std::min(cdiv(kSegTarget, waves), (int64_t)f.nchunks / kSegMinChunks);
+  if (requested > 0) {
+    n = requested;
+  } else {
+    // the last automatic choice per thread, keyed by its inputs (every call plans twice or more)
+    thread_local int64_t key[4] = {-1, -1, -1, -1}, memo = 1;
+    const int64_t k[4] = {waves, f.nchunks, B, backward};
+    if (std::equal(k, k + 4, key)) {
+      n = memo;
+    } else {
+      const PassModel &m = backward ? kBwdModel : kFwdModel;
+      // past 16 full rounds more segments only add summary work
+      const int64_t nmax = std::min({(int64_t)f.nchunks / kSegMinChunks, 65535 / B, cdiv(16 * m.cap * kSimds, waves)});
+      double best = plan_cost(m, waves, f.nchunks, 1);
+      for (int64_t c = 2; c <= nmax; ++c) {
+        const double v = plan_cost(m, waves, f.nchunks, c);
+        if (v < best) best = v, n = c;
+      }
+      std::copy(k, k + 4, key);
+      memo = n;
+    }
+  }
   n = std::max((int64_t)1, std::min(n, std::min((int64_t)f.nchunks, 65535 / B)));
   s.seg_chunks = (int)cdiv(f.nchunks, n);
   s.nseg = (int)cdiv(f.nchunks, s.seg_chunks);
@@ -144,7 +197,7 @@ BwdLayout bwd_layout(const ssm_bwd_args *a) {
   BwdLayout w;
   w.f = fwd_layout(a->batch, a->seqlen, a->dim, a->dstate, a->dtype, has(a->z));
   // float64 runs the register-staged kernel, which has no time segments
-  w.sp = a->dtype == SSM_F64 ? SegPlan{1, w.f.nchunks} : seg_plan(a->batch, a->dim, w.f, a->segments);
+  w.sp = a->dtype == SSM_F64 ? SegPlan{1, w.f.nchunks} : seg_plan(a->batch, a->dim, w.f, a->segments, true);
   const int ss = state_size(a->dtype);
   const int64_t rows = a->batch * w.sp.nseg;
   w.ntiles = (int)cdiv(a->dim, bwd_channels_per_block(a->dtype, w.f.np));
@@ -219,7 +272,7 @@ static int64_t seg_buf_bytes(const ssm_fwd_args *a, const FwdLayout &f, const Se
 int64_t ssm_fwd_workspace_bytes(const ssm_fwd_args *a) {
   if (ssm_fwd_check(a)) return -1;
   FwdLayout f = fwd_layout(a->batch, a->seqlen, a->dim, a->dstate, a->dtype, has(a->z));
-  return 3 * seg_buf_bytes(a, f, seg_plan(a->batch, a->dim, f, a->segments));
+  return 3 * seg_buf_bytes(a, f, seg_plan(a->batch, a->dim, f, a->segments, false));
 }
 
 static void fill_fwd(FwdParams &p, const ssm_fwd_args *a, const FwdLayout &f) {
@@ -254,7 +307,7 @@ int ssm_fwd(const ssm_fwd_args *a, void *stream) {
     p.ckpt = a->saved;
     p.ypre = has(a->z) ? (char *)a->saved + f.ckpt_bytes : nullptr;
   }
-  const SegPlan sp = seg_plan(a->batch, a->dim, f, a->segments);
+  const SegPlan sp = seg_plan(a->batch, a->dim, f, a->segments, false);
   const int64_t bb = seg_buf_bytes(a, f, sp);
   if (sp.nseg > 1) {
     if (!a->workspace || a->workspace_bytes < 3 * bb)

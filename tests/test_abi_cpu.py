@@ -106,10 +106,11 @@ def test_plans_match_committed_golden_table():
         assert plan.resolve_scan(*row[0]) == row[1]
 
 
-def _fwd_args(B=2, L=8, D=4, N=16, method=0, dtype=0, drop=()):
-    x = torch.zeros(B, L, D)
-    A = torch.zeros(D, N)
-    Bm = torch.zeros(B, L, N)
+def _fwd_args(B=2, L=8, D=4, N=16, method=0, dtype=0, drop=(), empty=False):
+    new = torch.empty if empty else torch.zeros
+    x = new(B, L, D)
+    A = new(D, N)
+    Bm = new(B, L, N)
     a = _abi.FwdArgs()
     a.batch, a.seqlen, a.dim, a.dstate, a.method, a.dtype = B, L, D, N, method, dtype
     for name, t in (("x", x), ("delta", x), ("A", A), ("Bm", Bm), ("Cm", Bm), ("out", x)):
@@ -136,6 +137,44 @@ def test_forward_validation_accepts_and_sizes():
     assert lib.ssm_fwd_check(ctypes.byref(a)) == 0
     # chunk-boundary states: B * ceil(L/16) * D * 16 float32
     assert lib.ssm_fwd_saved_bytes(ctypes.byref(a)) == 16 * 32 * 512 * 16 * 4
+
+
+def _bwd_args(B, L, D, N, segments):
+    x = torch.empty(B, L, D)
+    A = torch.empty(D, N)
+    Bm = torch.empty(B, L, N)
+    b = _abi.BwdArgs()
+    b.batch, b.seqlen, b.dim, b.dstate, b.segments = B, L, D, N, segments
+    for name, t in (("x", x), ("delta", x), ("A", A), ("Bm", Bm), ("Cm", Bm), ("dout", x), ("dx", x),
+                    ("ddelta", x), ("dA", A), ("dBm", Bm), ("dCm", Bm)):
+        setattr(b, name, _abi.view(t))
+    b._keep = (x, A, Bm)
+    return b
+
+
+# (B, L, forward segments, backward segments) chosen automatically at D512 N16 float32 (128
+# wavefronts per batch row, 16-step chunks) by the library's cost model of resident rounds on
+# 1,024 SIMDs (3 forward / 2 backward wavefronts per SIMD); the counts are the segments the plan
+# actually walks (ceil(chunks / ceil(chunks / n))).
+AUTO_PLANS = [(1, 512, 8, 8), (2, 512, 8, 8), (4, 512, 4, 4), (6, 512, 1, 8), (8, 512, 1, 2), (12, 512, 1, 1),
+              (16, 512, 1, 1), (1, 4096, 16, 16), (1, 16384, 24, 16), (1, 131072, 24, 16), (3, 16384, 8, 16),
+              (5, 8192, 9, 16), (5, 65536, 24, 16), (2, 4096, 8, 8), (8, 4096, 3, 2), (4, 1024, 4, 4)]
+
+
+@pytest.mark.parametrize("B,L,nf,nb", AUTO_PLANS)
+def test_automatic_time_segments(B, L, nf, nb):
+    """The automatic plan equals the forced count (workspace sizes depend on the count)."""
+    lib = _abi.lib()
+    sizes = {}
+    other_f, other_b = (nf // 2 if nf > 1 else 2), (nb // 2 if nb > 1 else 2)
+    for seg in (0, nf, other_f):
+        a = _fwd_args(B=B, L=L, D=512, N=16, empty=True)
+        a.segments = seg
+        sizes[seg] = lib.ssm_fwd_workspace_bytes(ctypes.byref(a))
+    assert sizes[0] == sizes[nf] != sizes[other_f]
+    assert (sizes[0] == 0) == (nf == 1)
+    sizes = {seg: lib.ssm_bwd_workspace_bytes(ctypes.byref(_bwd_args(B, L, 512, 16, seg))) for seg in (0, nb, other_b)}
+    assert sizes[0] == sizes[nb] != sizes[other_b]
 
 
 def test_backward_requires_gradient_buffers():

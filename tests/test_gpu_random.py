@@ -73,7 +73,7 @@ def oracle(x, delta, A, proj, Dv, z, bias, h0, dout, dlast, N, method, softplus,
     return out, last, gr
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", [s for s in range(25) if s != 13])
 def test_random_configuration_matches_oracle(dev, seed):
     run_case(dev, seed)
 
@@ -82,7 +82,7 @@ def test_random_configuration_matches_oracle(dev, seed):
 # (summed over batch and time) or of ddelta (summed over the states) sit outside the bar:
 # small values left by terms whose magnitudes add up to 24-304, an error of 0.2-1.6e-6 of
 # that magnitude.  Every other gradient element of these cases is held to the bar.
-CANCELLING_SEEDS = (74, 82, 159, 208, 218, 229, 249, 360, 370, 419)
+CANCELLING_SEEDS = (13, 74, 82, 153, 159, 208, 229, 249, 360)
 
 
 @pytest.mark.parametrize("seed", CANCELLING_SEEDS)
@@ -95,7 +95,7 @@ def test_random_configuration_cancellation_within_float32_resolution(dev, seed):
 # A wider sweep, 2,000 draws (seeds 2000-3999): 17 draws with one or two such elements and one,
 # seed 3086 (N = 64, bilinear, B2 L333: 64-term state sums), with four ddelta elements at
 # 0.07-0.37e-6 of their terms' magnitudes (100-200); none outside the rule otherwise.
-WIDE_SWEEP_CANCELLING = tuple((s, 2) for s in (2008, 2077, 2215, 2237, 2555, 2572, 2724, 2752, 2812, 2897, 3045,
+WIDE_SWEEP_CANCELLING = tuple((s, 2) for s in (2008, 2077, 2215, 2555, 2572, 2724, 2752, 2798, 2812, 2897, 3045,
                                               3556, 3562, 3599, 3769, 3926, 3961)) + ((3086, 4),)
 
 
@@ -163,9 +163,10 @@ def test_random_lowrank_configuration_matches_oracle(dev, seed):
     run_lowrank(dev, seed)
 
 
-# A 1,000-draw sweep of the low-rank draws (seeds 100-1099) found 4 with one element of dA (a sum
+# A 1,000-draw sweep of the low-rank draws (seeds 100-1099) found 3 with one element of dA (a sum
 # over batch and time) or dW (a sum over the tokens) outside the bar, all bilinear at L = 257:
-# errors of 1.6e-8 - 4.1e-7 of their terms' magnitudes.
+# errors of 1.6e-8 - 4.1e-7 of their terms' magnitudes.  Seed 320 was a fourth under an earlier
+# time-segment plan (another order of the segment sums) and stays here as a check at the rule.
 LOWRANK_CANCELLING = (268, 320, 780, 1094)
 
 
@@ -389,15 +390,16 @@ def run_large(dev, seed, use_c, cancel_allow=None):
             close(v, rg[GRAD_MAP[k]], k)
 
 
-# A 40-draw sweep of large_draw (seeds 0-39) against the C oracle: these 11 draws have every
+# A 40-draw sweep of large_draw (seeds 0-39) against the C oracle: these 10 draws have every
 # element of every output and gradient at the bar.  In the others every element outside it was
 # a dA or ddelta sum within the cancellation rule (1 to 37 per tensor of up to 3.75 M elements,
 # at most 3e-6 of the terms' magnitudes), or, once, a near-zero output (the 16-state C.h sum,
-# 1.08e-5 off against atol 1e-5).
-LARGE_AT_BAR = (2, 5, 16, 17, 18, 22, 24, 26, 35, 36, 37)
-# ZOH draws with one dA element outside the bar (a sum over up to 2 x 1,500 steps), checked with
-# the numpy oracle's magnitudes: 4e-8 - 2.5e-7 of them.
-LARGE_CANCELLING = (0, 20, 30, 33, 39)
+# 1.08e-5 off against atol 1e-5).  Which draws sit at the bar depends on the time-segment plan,
+# which sets the order of the segment sums.
+LARGE_AT_BAR = (2, 5, 16, 17, 18, 22, 24, 26, 35, 37)
+# Draws with one or two dA elements outside the bar (sums over up to 3,000 steps),
+# checked with the numpy oracle's magnitudes: 3.4e-8 - 2.5e-7 of them.
+LARGE_CANCELLING = ((0, 1), (20, 1), (30, 1), (33, 1), (36, 2), (39, 1))
 
 
 @pytest.mark.parametrize("seed", LARGE_AT_BAR)
@@ -405,6 +407,6 @@ def test_random_large_shapes_match_c_oracle(dev, seed):
     run_large(dev, seed, use_c=True)
 
 
-@pytest.mark.parametrize("seed", LARGE_CANCELLING)
-def test_random_large_shapes_cancellation_within_float32_resolution(dev, seed):
-    run_large(dev, seed, use_c=False, cancel_allow=1)
+@pytest.mark.parametrize("seed,allow", LARGE_CANCELLING)
+def test_random_large_shapes_cancellation_within_float32_resolution(dev, seed, allow):
+    run_large(dev, seed, use_c=False, cancel_allow=allow)
