@@ -596,7 +596,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   if (SUM && seg == 0) return;  // the first segment's summary is never used
   const int k0 = seg * p.seg_chunks;
   const int k1 = k0 + p.seg_chunks < p.nchunks ? k0 + p.seg_chunks : p.nchunks;
-  const int tile = blockIdx.x;
+  const int tile = xcd_tile();
   const int dw = (tile * WPB + wv) * CW;
   const int d = dw + c;
   const bool dval = d < p.D, nval = n < p.N;

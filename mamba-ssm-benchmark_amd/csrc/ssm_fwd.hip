@@ -353,7 +353,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   if (SUM && seg == p.nseg - 1) return;  // the last segment's summary is never used
   const int k0 = seg * p.seg_chunks;
   const int k1 = k0 + p.seg_chunks < p.nchunks ? k0 + p.seg_chunks : p.nchunks;
-  const int dw = (blockIdx.x * WPB + wv) * CW;  // first channel of this wavefront
+  const int dw = (xcd_tile() * WPB + wv) * CW;  // first channel of this wavefront
   const int d = dw + c;
   const bool dval = d < p.D, nval = n < p.N;
   const int L = (int)p.L, D = (int)p.D, N = (int)p.N;

@@ -39,6 +39,15 @@ __host__ __device__ constexpr int np_pad(int s, int np) { return np + 16 / s; }
 // order puts those 16 rows on 16 distinct 16-byte bank groups (the natural order puts 4 pairs on
 // one group: 4 extra cycles per read).  Row of step t among a chunk's 16 step rows:
 __host__ __device__ constexpr int step_row(int t) { return 4 * (t % 4) + (t < 4 ? 2 : t < 8 ? 0 : t < 12 ? 1 : 3); }
+// Channel tile of a fused-kernel workgroup.  MI355X hands workgroup l (linear id x + y *
+// gridDim.x) to XCD l % 8, each XCD with its own L2.  Tiles next to each other share 128-byte
+// lines of (B, L, D) rows (a 16-channel float32 tile reads 64 bytes of a row per step), so with
+// tile = blockIdx.x the two halves of every line went to two XCDs, each fetching the whole
+// line.  When gridDim.x is a multiple of 8, XCD k gets tiles [k, k + 1) * gridDim.x / 8 instead.
+__device__ __forceinline__ int xcd_tile() {
+  const int nx = (int)gridDim.x, x = (int)blockIdx.x;
+  return nx % 8 ? x : (x % 8) * (nx / 8) + x / 8;
+}
 // Low-rank delta (the dt_proj GEMM fused into the staging): a chunk's (CK, R <= kLR) input
 // rows and the wavefront's channels' weight rows, padded like the other LDS rows.
 constexpr int kLR = 16;
