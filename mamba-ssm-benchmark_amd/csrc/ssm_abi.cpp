@@ -123,9 +123,15 @@ bool saved_rows_fit(const FwdLayout &f, int64_t L, int64_t D, int dtype) {
 // (latency-bound), so a partly filled extra round costs a whole walk (B1 L65536: 16, 32 and 48
 // segments 1.16-1.18 ms, 24 segments 1.52 ms); the forward keeps its SIMDs busy from 2
 // wavefronts on, so it segments less at short lengths (B8 L512: one segment 39 us, 2 segments
-// 45 us, 6 segments 53 us).  Segments are at least kSegMinChunks chunks long; a positive
-// `requested` overrides the choice (clamped to the valid range).
-constexpr int64_t kSimds = 1024, kSegMinChunks = 4;
+// 45 us, 6 segments 53 us).  With fewer than 512 wavefronts per segment (one to three rows at
+// D 512), walks over kSegLongChunks chunks end unevenly, which the rounds do not capture: there the
+// plan takes the best count with segments of at most kSegLongChunks chunks when the model prices
+// it within kSegLongSlack of the best (B1 D512 L131072 forward: 64 segments 0.857 ms, 24 segments
+// 0.874 ms; L65536 with (B, L, D) inputs: 48-64 segments 0.60-0.62 ms, 24 segments 0.66 ms;
+// backward 32 segments 1.168 ms, 16 segments 1.183 ms).  Segments are at least kSegMinChunks
+// chunks long; a positive `requested` overrides the choice (clamped to the valid range).
+constexpr int64_t kSimds = 1024, kSegMinChunks = 4, kSegLongChunks = 128;
+constexpr double kSegLongSlack = 1.1;
 
 struct PassModel {
   int cap;             // wavefronts per SIMD that the kernel's registers and LDS allow
@@ -171,11 +177,14 @@ SegPlan seg_plan(int64_t B, int64_t D, const FwdLayout &f, int requested, bool b
       const PassModel &m = backward ? kBwdModel : kFwdModel;
       // past 16 full rounds more segments only add summary work
       const int64_t nmax = std::min({(int64_t)f.nchunks / kSegMinChunks, 65535 / B, cdiv(16 * m.cap * kSimds, waves)});
-      double best = plan_cost(m, waves, f.nchunks, 1);
-      for (int64_t c = 2; c <= nmax; ++c) {
-        const double v = plan_cost(m, waves, f.nchunks, c);
+      double best = plan_cost(m, waves, f.nchunks, 1), best_short = -1.0;
+      int64_t n_short = 0;
+      for (int64_t c = 1; c <= nmax; ++c) {
+        const double v = c == 1 ? best : plan_cost(m, waves, f.nchunks, c);
         if (v < best) best = v, n = c;
+        if (cdiv(f.nchunks, c) <= kSegLongChunks && (n_short == 0 || v < best_short)) best_short = v, n_short = c;
       }
+      if (2 * waves < kSimds && n_short && best_short <= kSegLongSlack * best) n = n_short;
       std::copy(k, k + 4, key);
       memo = n;
     }

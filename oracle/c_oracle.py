@@ -28,7 +28,7 @@ def _load():
         P = ctypes.c_void_p
         I64 = ctypes.c_int64
         _lib.ssm_oracle_fwd.argtypes = [I64, I64, I64, I64, ctypes.c_int] + [P] * 11 + [ctypes.c_int]
-        _lib.ssm_oracle_bwd.argtypes = [I64, I64, I64, I64, ctypes.c_int] + [P] * 19 + [ctypes.c_int]
+        _lib.ssm_oracle_bwd.argtypes = [I64, I64, I64, I64, ctypes.c_int] + [P] * 22 + [ctypes.c_int]
         _lib.ssm_oracle_fwd.restype = ctypes.c_int
         _lib.ssm_oracle_bwd.restype = ctypes.c_int
     return _lib
@@ -61,7 +61,10 @@ def fwd(x, delta, A, Bm, Cm, h0=None, method="zoh", D=None, z=None, nthreads=0):
 def bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None, z=None, dlast=None,
         nthreads=0, mag=False):
     """Returns the gradient dict of scan_ref.selective_scan_bwd, in float64.  With mag=True it
-    also holds "ddelta_mag": per ddelta element, the sum over states of the |terms| it adds."""
+    also holds "ddelta_mag", "dA_mag", "dB_mag" and "dC_mag": per element the sum of the |terms|
+    it adds (over the states for ddelta, over batch and time for dA, over the channels for dB and
+    dC), as
+    scan_ref.selective_scan_bwd(mag=True)."""
     lib = _load()
     x, delta, A, Bm, Cm, dout, h0, D, z, dlast = (
         _c(v) for v in (x, delta, A, Bm, Cm, dout, h0, D, z, dlast))
@@ -73,10 +76,13 @@ def bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None, z=None, dlast=
     g_dz = np.empty_like(z) if z is not None else None
     g_dh0 = np.empty_like(h0) if h0 is not None else None
     g_mag = np.empty_like(delta) if mag else None
+    g_amag = np.empty_like(A) if mag else None
+    g_bmag = np.empty_like(Bm) if mag else None
+    g_cmag = np.empty_like(Cm) if mag else None
     rc = lib.ssm_oracle_bwd(Bsz, L, Dm, N, METHODS[method], _p(x), _p(delta), _p(A), _p(Bm),
                             _p(Cm), _p(h0), _p(D), _p(z), _p(dout), _p(dlast), _p(g["dx"]),
                             _p(g["ddelta"]), _p(g["dA"]), _p(g["dB"]), _p(g["dC"]), _p(g_dD),
-                            _p(g_dz), _p(g_dh0), _p(g_mag), nthreads)
+                            _p(g_dz), _p(g_dh0), _p(g_mag), _p(g_amag), _p(g_bmag), _p(g_cmag), nthreads)
     if rc:
         raise RuntimeError(f"ssm_oracle_bwd failed: {rc}")
     if g_dD is not None:
@@ -87,4 +93,7 @@ def bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None, z=None, dlast=
         g["dh0"] = g_dh0
     if g_mag is not None:
         g["ddelta_mag"] = g_mag
+        g["dA_mag"] = g_amag
+        g["dB_mag"] = g_bmag
+        g["dC_mag"] = g_cmag
     return g

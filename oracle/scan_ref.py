@@ -232,9 +232,10 @@ def selective_scan_bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None,
     dy = dout s z, dz = dout (y + D x) s (1 + z (1 - s)), dD = sum dy x, dx += dy D.
 
     Returns dict with dx, ddelta, dA, dB, dC and (when present) dD, dz, dh0.  With mag, also
-    ddelta_mag and dA_mag: per element the sum of the magnitudes of the terms it adds (over the
-    states for ddelta, over batch and time for dA), the scale of the float32 rounding a kernel
-    summing those terms can leave in it."""
+    ddelta_mag, dA_mag, dB_mag and dC_mag: per element the sum of the magnitudes of the terms it
+    adds (over the states for ddelta, over batch and time for dA, over the channels for dB and
+    dC), the
+    scale of the float32 rounding a kernel summing those terms can leave in it."""
     x, delta, A, Bm, Cm, dout = (np.asarray(v, np.float64) for v in (x, delta, A, Bm, Cm, dout))
     Bsz, L, Dm = x.shape
     N = A.shape[1]
@@ -254,7 +255,7 @@ def selective_scan_bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None,
         dx = dx + dy * Dv
     ddelta = np.zeros_like(delta)
     dA = np.zeros_like(A)
-    ddelta_mag, dA_mag = np.zeros_like(delta), np.zeros_like(A)
+    ddelta_mag, dA_mag, dB_mag, dC_mag = np.zeros_like(delta), np.zeros_like(A), np.zeros_like(Bm), np.zeros_like(Cm)
     dB = np.zeros_like(Bm)
     dC = np.zeros_like(Cm)
     dh = np.zeros((Bsz, Dm, N)) if dlast is None else np.asarray(dlast, np.float64).copy()
@@ -268,6 +269,8 @@ def selective_scan_bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None,
         Bt = Bm[:, t][:, None, :]                        # (B, 1, N)
         Ct = Cm[:, t][:, None, :]
         dC[:, t] = np.einsum("bd,bdn->bn", dyt, h_t)
+        if mag:
+            dC_mag[:, t] = np.einsum("bd,bdn->bn", np.abs(dyt), np.abs(h_t))
         dh = dh + dyt[..., None] * Ct
         zt = dt * A
         Bx = Bt * xt
@@ -283,14 +286,16 @@ def selective_scan_bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None,
             td, tA = da * A * a + dh * a * Bx, da * dt * a + dh * dt * dt * f * Bx
             ddelta[:, t] = np.sum(td, axis=2)
             dA += np.sum(tA, axis=0)
-            dB[:, t] = np.sum(dh * coef * xt, axis=1)
+            tB = dh * coef * xt
+            dB[:, t] = np.sum(tB, axis=1)
             dx[:, t] += np.sum(dh * coef * Bt, axis=2)
         elif method == "euler":
             a = np.exp(zt)
             td, tA = da * A * a + dh * Bx, da * dt * a
             ddelta[:, t] = np.sum(td, axis=2)
             dA += np.sum(tA, axis=0)
-            dB[:, t] = np.sum(dh * dt * xt, axis=1)
+            tB = dh * dt * xt
+            dB[:, t] = np.sum(tB, axis=1)
             dx[:, t] += np.sum(dh * dt * Bt, axis=2)
         elif method == "bilinear":
             u = 1.0 / (1.0 - 0.5 * zt)
@@ -299,17 +304,19 @@ def selective_scan_bwd(x, delta, A, Bm, Cm, dout, h0=None, method="zoh", D=None,
             td, tA = da * A * u2 + dh * u2 * Bx, da * dt * u2 + dh * 0.5 * dt * dt * u2 * Bx
             ddelta[:, t] = np.sum(td, axis=2)
             dA += np.sum(tA, axis=0)
-            dB[:, t] = np.sum(dh * dt * u * xt, axis=1)
+            tB = dh * dt * u * xt
+            dB[:, t] = np.sum(tB, axis=1)
             dx[:, t] += np.sum(dh * dt * u * Bt, axis=2)
         else:
             raise ValueError(f"unknown discretization {method!r}")
         if mag:
             ddelta_mag[:, t] = np.sum(np.abs(td), axis=2)
             dA_mag += np.sum(np.abs(tA), axis=0)
+            dB_mag[:, t] = np.sum(np.abs(tB), axis=1)
         dh = dh * a
     g.update(dx=dx, ddelta=ddelta, dA=dA, dB=dB, dC=dC)
     if mag:
-        g.update(ddelta_mag=ddelta_mag, dA_mag=dA_mag)
+        g.update(ddelta_mag=ddelta_mag, dA_mag=dA_mag, dB_mag=dB_mag, dC_mag=dC_mag)
     if h0 is not None:
         g["dh0"] = dh
     return g

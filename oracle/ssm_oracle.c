@@ -9,7 +9,9 @@
  * dB/dC are accumulated per thread and summed in thread order (deterministic).
  * It is pinned against scan_ref.py by tests/test_oracle_kat.py (test_c_oracle_matches_numpy_oracle).
  * The backward optionally reports, per ddelta element, the sum over states of the magnitudes of
- * the terms it adds (the scale of the float32 rounding a kernel can leave in that element).
+ * the terms it adds, per dA element the sum over batch and time and per dB and dC element the sum
+ * over channels of its terms' magnitudes (the scale of the float32 rounding a kernel can leave in
+ * that element).
  */
 #include <math.h>
 #include <stdint.h>
@@ -77,7 +79,8 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
                    const double *delta, const double *A, const double *Bm, const double *Cm,
                    const double *h0, const double *Dskip, const double *z, const double *dout,
                    const double *dlast, double *dx, double *ddelta, double *dA, double *dB,
-                   double *dC, double *dD, double *dz, double *dh0, double *ddelta_mag, int nthreads) {
+                   double *dC, double *dD, double *dz, double *dh0, double *ddelta_mag, double *dA_mag,
+                   double *dB_mag, double *dC_mag, int nthreads) {
   if (method < 0 || method > 2) return 1;
   int nt = 1;
 #ifdef _OPENMP
@@ -88,7 +91,13 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
   double *pB = (double *)calloc((size_t)nt * BLN, sizeof(double));
   double *pC = (double *)calloc((size_t)nt * BLN, sizeof(double));
   double *pA = (double *)calloc((size_t)B * D * N, sizeof(double));
-  if (!pB || !pC || !pA) { free(pB); free(pC); free(pA); return 2; }
+  double *pAm = (double *)calloc((size_t)B * D * N, sizeof(double));
+  double *pBm = dB_mag ? (double *)calloc((size_t)nt * BLN, sizeof(double)) : NULL;
+  double *pCm = dC_mag ? (double *)calloc((size_t)nt * BLN, sizeof(double)) : NULL;
+  if (!pB || !pC || !pA || !pAm || (dB_mag && !pBm) || (dC_mag && !pCm)) {
+    free(pB); free(pC); free(pA); free(pAm); free(pBm); free(pCm);
+    return 2;
+  }
 #pragma omp parallel
   {
     int tid = 0;
@@ -96,6 +105,7 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
     tid = omp_get_thread_num();
 #endif
     double *myB = pB + (int64_t)tid * BLN, *myC = pC + (int64_t)tid * BLN;
+    double *myBm = pBm ? pBm + (int64_t)tid * BLN : NULL, *myCm = pCm ? pCm + (int64_t)tid * BLN : NULL;
     double *hs = (double *)malloc(sizeof(double) * (L + 1) * N);
     double *dh = (double *)malloc(sizeof(double) * N);
 #pragma omp for schedule(static)
@@ -129,8 +139,9 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
           int64_t in = IDX3(b, t, n, L, N);
           double Av = A[d * N + n], Bv = Bm[in], h_t = hs[(t + 1) * N + n], hp = hs[t * N + n];
           myC[in] += dyv * h_t;
+          if (myCm) myCm[in] += fabs(dyv * h_t);
           dh[n] += dyv * Cm[in];
-          double zt = dt * Av, Bx = Bv * xv, da = dh[n] * hp, a;
+          double zt = dt * Av, Bx = Bv * xv, da = dh[n] * hp, a, tA, tB;
           if (method == 0) {
             a = exp(zt);
             double e = expm1(zt), coef = e / Av, f;
@@ -138,25 +149,29 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
             else f = (zt * a - e) / (zt * zt);
             ddt += da * Av * a + dh[n] * a * Bx;
             mag += fabs(da * Av * a + dh[n] * a * Bx);
-            pA[(b * D + d) * N + n] += da * dt * a + dh[n] * dt * dt * f * Bx;
-            myB[in] += dh[n] * coef * xv;
+            tA = da * dt * a + dh[n] * dt * dt * f * Bx;
+            tB = dh[n] * coef * xv;
             dxv += dh[n] * coef * Bv;
           } else if (method == 1) {
             a = exp(zt);
             ddt += da * Av * a + dh[n] * Bx;
             mag += fabs(da * Av * a + dh[n] * Bx);
-            pA[(b * D + d) * N + n] += da * dt * a;
-            myB[in] += dh[n] * dt * xv;
+            tA = da * dt * a;
+            tB = dh[n] * dt * xv;
             dxv += dh[n] * dt * Bv;
           } else {
             double u = 1.0 / (1.0 - 0.5 * zt), u2 = u * u;
             a = (1.0 + 0.5 * zt) * u;
             ddt += da * Av * u2 + dh[n] * u2 * Bx;
             mag += fabs(da * Av * u2 + dh[n] * u2 * Bx);
-            pA[(b * D + d) * N + n] += da * dt * u2 + dh[n] * 0.5 * dt * dt * u2 * Bx;
-            myB[in] += dh[n] * dt * u * xv;
+            tA = da * dt * u2 + dh[n] * 0.5 * dt * dt * u2 * Bx;
+            tB = dh[n] * dt * u * xv;
             dxv += dh[n] * dt * u * Bv;
           }
+          pA[(b * D + d) * N + n] += tA;
+          pAm[(b * D + d) * N + n] += fabs(tA);
+          myB[in] += tB;
+          if (myBm) myBm[in] += fabs(tB);
           dh[n] *= a;
         }
         dx[i3] = dxv;
@@ -175,11 +190,22 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
     for (int k = 0; k < nt; ++k) { sb += pB[(int64_t)k * BLN + i]; sc += pC[(int64_t)k * BLN + i]; }
     dB[i] = sb;
     dC[i] = sc;
+    if (dB_mag) {
+      double sm = 0.0;
+      for (int k = 0; k < nt; ++k) sm += pBm[(int64_t)k * BLN + i];
+      dB_mag[i] = sm;
+    }
+    if (dC_mag) {
+      double sm = 0.0;
+      for (int k = 0; k < nt; ++k) sm += pCm[(int64_t)k * BLN + i];
+      dC_mag[i] = sm;
+    }
   }
   for (int64_t dn = 0; dn < D * N; ++dn) {
-    double s = 0.0;
-    for (int64_t b = 0; b < B; ++b) s += pA[b * D * N + dn];
+    double s = 0.0, m = 0.0;
+    for (int64_t b = 0; b < B; ++b) s += pA[b * D * N + dn], m += pAm[b * D * N + dn];
     dA[dn] = s;
+    if (dA_mag) dA_mag[dn] = m;
   }
   if (dD) {
     for (int64_t d = 0; d < D; ++d) dD[d] = 0.0;
@@ -195,5 +221,8 @@ int ssm_oracle_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int method, const
   free(pB);
   free(pC);
   free(pA);
+  free(pAm);
+  free(pBm);
+  free(pCm);
   return 0;
 }

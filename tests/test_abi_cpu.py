@@ -154,11 +154,12 @@ def _bwd_args(B, L, D, N, segments):
 
 # (B, L, forward segments, backward segments) chosen automatically at D512 N16 float32 (128
 # wavefronts per batch row, 16-step chunks) by the library's cost model of resident rounds on
-# 1,024 SIMDs (3 forward / 2 backward wavefronts per SIMD); the counts are the segments the plan
-# actually walks (ceil(chunks / ceil(chunks / n))).
+# 1,024 SIMDs (3 forward / 2 backward wavefronts per SIMD), with walks of at most 128 chunks
+# preferred for one to three rows; the counts are the segments the plan actually walks
+# (ceil(chunks / ceil(chunks / n))).
 AUTO_PLANS = [(1, 512, 8, 8), (2, 512, 8, 8), (4, 512, 4, 4), (6, 512, 1, 8), (8, 512, 1, 2), (12, 512, 1, 1),
-              (16, 512, 1, 1), (1, 4096, 16, 16), (1, 16384, 24, 16), (1, 131072, 24, 16), (3, 16384, 8, 16),
-              (5, 8192, 9, 16), (5, 65536, 24, 16), (2, 4096, 8, 8), (8, 4096, 3, 2), (4, 1024, 4, 4)]
+              (16, 512, 1, 1), (1, 4096, 16, 16), (1, 16384, 24, 16), (1, 65536, 48, 32), (1, 131072, 72, 64),
+              (3, 16384, 8, 16), (5, 8192, 9, 16), (5, 65536, 24, 16), (2, 4096, 8, 8), (8, 4096, 3, 2), (4, 1024, 4, 4)]
 
 
 @pytest.mark.parametrize("B,L,nf,nb", AUTO_PLANS)

@@ -329,7 +329,7 @@ def test_c_oracle_matches_numpy_oracle(method, h0, gate):
 @pytest.mark.parametrize("method", R.DISCRETIZATIONS)
 def test_term_magnitudes_bound_values_and_add_over_rows(method):
     """The term magnitudes that scale the float32 cancellation bound of the GPU tests:
-    ddelta_mag equals the C oracle's (its own scalar loop), every magnitude bounds its value,
+    the ddelta, dA, dB and dC magnitudes equal the C oracle's (its own scalar loop), every magnitude bounds its value,
     an element of one term has magnitude |value|, and dA_mag adds over batch rows (so it is a
     sum of |terms|, not |sum|)."""
     ins = sel_inputs(B=3, L=40, D=7, N=6, seed=23, h0=True, gate=True)
@@ -338,7 +338,10 @@ def test_term_magnitudes_bound_values_and_add_over_rows(method):
     gm = R.selective_scan_bwd(*ins[:5], dout, ins[5], method, ins[6], ins[7], dl, mag=True)
     gc = c_oracle.bwd(*ins[:5], dout, ins[5], method, ins[6], ins[7], dl, mag=True)
     np.testing.assert_allclose(gm["ddelta_mag"], gc["ddelta_mag"], rtol=1e-11, atol=1e-12)
-    for k in ("ddelta", "dA"):
+    np.testing.assert_allclose(gm["dA_mag"], gc["dA_mag"], rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(gm["dB_mag"], gc["dB_mag"], rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(gm["dC_mag"], gc["dC_mag"], rtol=1e-11, atol=1e-12)
+    for k in ("ddelta", "dA", "dB", "dC"):
         assert np.all(gm[k + "_mag"] >= np.abs(gm[k]) * (1 - 1e-12)), k
         assert np.any(gm[k + "_mag"] > 1.5 * np.abs(gm[k])), k   # terms do cancel here
     x, delta, A, Bm, Cm, hz, Dv, z = ins
