@@ -399,8 +399,9 @@ int ssm_norm_bwd(const ssm_norm_args *args, void *stream);   /* autograd of :14-
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  Same arguments and results as ssm_fwd, except that args->workspace and
  * args->workspace_bytes are ignored: the long-sequence (segmented) path uses a fixed device
- * array of SSM_FWD_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, and a forward
- * whose ssm_fwd_workspace_bytes() exceeds it fails with SSM_ESPACE.  The stream must belong
+ * array of SSM_FWD_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.  With
+ * args->segments = 0 a plan whose ssm_fwd_workspace_bytes() exceeds the array runs the most
+ * segments that fit it; a forced count that exceeds it fails with SSM_ESPACE.  The stream must belong
  * to the current device.  Calls on one GPU share the array: calls that overlap on one GPU
  * race (serialize them, e.g. on one stream). */
 #define SSM_FWD_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024)

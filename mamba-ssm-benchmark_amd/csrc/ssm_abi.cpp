@@ -1096,7 +1096,16 @@ extern "C" {
 int ssm_fwd_noalloc(const ssm_fwd_args *a, void *stream) {
   int rc = ssm_fwd_check(a);
   if (rc) return rc;
-  const int64_t need = ssm_fwd_workspace_bytes(a);
+  ssm_fwd_args b = *a;
+  int64_t need = ssm_fwd_workspace_bytes(a);
+  if (need > (int64_t)SSM_FWD_NOALLOC_SCRATCH_BYTES && a->segments <= 0) {
+    // the automatic count lowered to the most segments whose three summary buffers fit the
+    // array (each buffer is B x nseg x D x NP states, rounded up to 256 bytes)
+    const FwdLayout f = fwd_layout(a->batch, a->seqlen, a->dim, a->dstate, a->dtype, has(a->z));
+    const int64_t per = a->batch * a->dim * f.np * state_size(a->dtype);
+    b.segments = (int32_t)std::max((int64_t)1, ((int64_t)SSM_FWD_NOALLOC_SCRATCH_BYTES / 3 - 255) / per);
+    need = ssm_fwd_workspace_bytes(&b);
+  }
   if (need > (int64_t)SSM_FWD_NOALLOC_SCRATCH_BYTES)
     return fail(SSM_ESPACE,
                 "ssm_fwd_noalloc: this forward needs %lld bytes of workspace, more than the fixed scratch of "
@@ -1105,7 +1114,6 @@ int ssm_fwd_noalloc(const ssm_fwd_args *a, void *stream) {
   void *ptr = nullptr;
   rc = scratch_address(stream, &ptr);
   if (rc) return rc;
-  ssm_fwd_args b = *a;
   b.workspace = ptr;
   b.workspace_bytes = SSM_FWD_NOALLOC_SCRATCH_BYTES;
   return ssm_fwd(&b, stream);

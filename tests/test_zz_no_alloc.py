@@ -102,3 +102,31 @@ def test_noalloc_forward_equals_ssm_fwd_on_consecutive_calls(dev):
                                       D=np64(Dv), z=np64(z))
         close(o2, rout, name="out")
         close(l2, rlast, name="last")
+
+
+@pytest.mark.gpu
+def test_noalloc_lowers_an_automatic_plan_to_the_scratch(dev):
+    """B3 L65536 D512 N16: the automatic plan's 32 segments need 9 MiB of workspace; with
+    segments = 0 ssm_fwd_noalloc runs the most that fit 8 MiB, (8 MiB / 3 - 255) // (3 x 512 x
+    16 x 4 B) = 28, and equals ssm_fwd forced to 28 segments bitwise (forced counts are
+    checked against the oracle elsewhere); no allocation."""
+    lib = _abi.lib()
+    B, L, D, N = 3, 65536, 512, 16
+    print(f"case B{B} L{L} D{D} N{N} automatic segments", flush=True)
+    _, ins = _case(dev, B, L, D, N, 0, "zoh", False)
+    out = torch.empty(B, L, D, device=dev)
+    a = _args(*ins, out, torch.empty(B, D, N, device=dev), hip_scan.METHODS["zoh"], 0)
+    assert lib.ssm_fwd_workspace_bytes(ctypes.byref(a)) > SCRATCH_BYTES
+    fit = (SCRATCH_BYTES // 3 - 255) // (B * D * N * 4)
+    assert fit == 28
+    o1, l1 = _call(lib, dev, ins, B, L, D, N, "zoh", fit, "ssm_fwd")
+    o2 = torch.empty(B, L, D, device=dev)
+    l2 = torch.empty(B, D, N, device=dev)
+    torch.cuda.synchronize()
+    before, free_before = torch.cuda.memory_allocated(dev), torch.cuda.mem_get_info(dev)[0]
+    a = _args(*ins, o2, l2, hip_scan.METHODS["zoh"], 0)
+    _abi.check(lib.ssm_fwd_noalloc(ctypes.byref(a), _abi.stream_handle(dev)), "ssm_fwd_noalloc")
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated(dev) == before
+    assert torch.cuda.mem_get_info(dev)[0] == free_before
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
