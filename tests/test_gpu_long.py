@@ -5,7 +5,8 @@ pass, carry over segment summaries, main pass) -- the structure of scan_chunked
 (models/scan.py:142-165) lifted to segments.  Checked here:
   * forced segment counts (incl. ragged last segments) at small shapes, forward and the
     backward that consumes the segmented forward's saved chunk states, all methods;
-  * the automatic choice at B1 D64 L8192;
+  * the automatic choice at B1 D64 L8192, and forward and backward planned apart (B6 L512
+    D512: the forward unsegmented, the backward in 8 segments);
   * BASELINE config 2 at its largest length, B1 L131072 D512 N16, float32 and bf16
     (rtol 1e-4 / atol 1e-5 float32; rtol 2e-2 / atol 1e-5 bf16), against the C fp64 oracle;
   * the backward at B1 L65536 D512 N16 (gate + D skip), walked in time segments, and with bf16
@@ -103,6 +104,25 @@ def test_automatic_segments_long_sequence(dev):
     ry, _, rlast = c_oracle.fwd(*(np64(v) for v in ins), np64(h0))
     close(y, ry, name="y")
     close(last, rlast, name="last")
+
+
+def test_forward_and_backward_plan_their_segments_apart(dev):
+    """B6 L512 D512 N16 with the gate and D skip: 768 wavefronts, so the automatic plan runs
+    the forward in one segment and the backward in 8 (it restarts from the forward's saved
+    chunk states, which do not depend on the forward's segments).  Every output and gradient
+    against the C float64 oracle at the bar; dA, dB, dC and ddelta under the cancellation rule
+    (at most 2 elements per tensor, each within float32 resolution of its terms' magnitudes)."""
+    t = baseline_inputs(6, 512, 512, 16, gate=True, with_dy=True)
+    ins = (t["u"], t["delta"], t["A"], t["Bm"], t["Cm"], None)
+    out, last, grads = run_seg(ins, dev, "zoh", None, D=t["D"], z=t["z"], dout=t["dy"])
+    rout, rlast, rg = oracle(ins, "zoh", D=t["D"], z=t["z"], dout=t["dy"], use_c=True, mag=True)
+    close(out, rout, name="out")
+    close(last, rlast, name="last")
+    for k, v in grads.items():
+        if k in ("dA", "dB", "dC", "ddelta"):
+            close_or_cancelled(v, rg[k], rg[k + "_mag"], k, allow=2)
+        else:
+            close(v, rg[k], name=k)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
