@@ -130,7 +130,7 @@ bool saved_rows_fit(const FwdLayout &f, int64_t L, int64_t D, int dtype) {
 // 0.874 ms; L65536 with (B, L, D) inputs: 48-64 segments 0.60-0.62 ms, 24 segments 0.66 ms;
 // backward 32 segments 1.168 ms, 16 segments 1.183 ms).  Segments are at least kSegMinChunks
 // chunks long; a positive `requested` overrides the choice (clamped to the valid range).
-constexpr int64_t kSimds = 1024, kSegMinChunks = 4, kSegLongChunks = 128;
+constexpr int64_t kSimds = 1024, kSegMinChunks = 4, kSegLongChunks = 128, kSyncSegChunks = 64;
 constexpr double kSegLongSlack = 1.1;
 
 struct PassModel {
@@ -324,6 +324,10 @@ int ssm_fwd(const ssm_fwd_args *a, void *stream) {
                   (long long)a->workspace_bytes, (long long)(3 * bb));
     p.nseg = sp.nseg;
     p.seg_chunks = sp.seg_chunks;
+    // (B, L, D) outputs over long segments: a workgroup barrier every 4 chunk pairs (B1 D512
+    // L65536, 48 segments of 86 chunks: forward 618 -> 575 us; no gain at 43 chunks, and 1-2 %
+    // slower with (B, D, L) outputs, whose 64-byte pieces each come from one wavefront)
+    if (sp.seg_chunks >= kSyncSegChunks && a->out.stride[2] == 1) p.sync_pairs = 4;
     p.seg_P = a->workspace;
     p.seg_E = (char *)a->workspace + bb;
     p.seg_hin = (char *)a->workspace + 2 * bb;

@@ -587,11 +587,17 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   if constexpr (UL) {
     // pairs of whole chunks strictly inside the segment, every lane's state and channel real
     const int kf = min(k1, L / CK);
-    if (p.N == NP && p.D % (WPB * CW) == 0)
+    if (p.N == NP && p.D % (WPB * CW) == 0) {
+      int pairs = 0;  // workgroup-uniform: every wavefront walks the same chunks
       for (; k + 1 < kf; k += 2) {
         iter(full, s1, T1, k, P0, P1);
         iter(full, s0, T0, k + 1, P1, P0);
+        if (!SUM && p.sync_pairs && ++pairs == p.sync_pairs) {
+          pairs = 0;
+          __syncthreads();
+        }
       }
+    }
   }
   for (; k <= k1; k += 2) {
     iter(ranged, s1, T1, k, P0, P1);

@@ -99,6 +99,11 @@ struct FwdParams {
   // at most kFoldSegs segments the float kernels' main pass folds seg_P / seg_E itself and no
   // carry pass runs.
   int nseg, seg_chunks;
+  // Chunk pairs between workgroup barriers in the float main pass (0: none).  A (B, L, D)
+  // output row takes 16 bytes per step from each of a workgroup's wavefronts; over long
+  // segments the wavefronts drift apart and the 64-byte pieces leave L2 before all four parts
+  // are written.  The barriers keep them in step.
+  int sync_pairs;
   void *seg_P, *seg_E, *seg_hin;
   KView x, dt, A, Bm, Cm, Dsk, z, bias, h0, out, last;
   // Low-rank delta: lowrank = R > 0 means delta = dtl (B, L, R) @ dtw (D, R)^T; dt then
