@@ -636,7 +636,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   const KView vg = with_layout<UL>(p.dout, p.x), vdz = p.dz;
   const KView vdx = with_layout<UL>(p.dx, p.x), vddt = with_layout<UL>(p.ddt, p.x);
   const KView vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
-  const bool xt = vx.s1 == 1, bt = vB.s1 == 1, ctt = vC.s1 == 1;
+  const bool bt = vB.s1 == 1, ctt = vC.s1 == 1;
   const KView vzl = p.has_z ? vz : vx;
   const float *ypre = (const float *)p.ypre;
   struct Tiles {
@@ -664,8 +664,9 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
   const RowRef rwB = flat_ref((const float *)p.ws_dB + wrow, p.L * NP * 4);
   const RowRef rwC = flat_ref((const float *)p.ws_dC + wrow, p.L * NP * 4);
   const uint32_t offK = (uint32_t)((dval ? d : 0) * NP + n) * 4u;
-  const uint32_t offY = (uint32_t)(ypre_index(!xt, 0, tj, dw + tc, p.L, p.D) * 4);
-  const uint32_t tstepY = (uint32_t)((xt ? 1 : (int)p.D) * CK * 4);
+  // the float forward saves the pre-gate output as (B, D, L)
+  const uint32_t offY = (uint32_t)(ypre_index(false, 0, tj, dw + tc, p.L, p.D) * 4);
+  const uint32_t tstepY = (uint32_t)(CK * 4);
   __amdgpu_buffer_rsrc_t rblr = empty;
   uint32_t offLR = 0, tstepLR = 0;
   bool rvLR = false;
@@ -708,7 +709,7 @@ __global__ void __launch_bounds__(kWave * bwdw_waves(NP)) k_bwdw(const BwdParams
       if constexpr (!SUM) T.B.load(vB, b, t0, L, 0, N, bt, lane);
       T.C.load(vC, b, t0, L, 0, N, ctt, lane);
       if constexpr (!SUM) {
-        T.yp.v = ypre ? ypre[ypre_index(!xt, b, min(t0 + tj, L - 1), min(dw + tc, D - 1), p.L, p.D)] : 0.0f;
+        T.yp.v = ypre ? ypre[ypre_index(false, b, min(t0 + tj, L - 1), min(dw + tc, D - 1), p.L, p.D)] : 0.0f;
         T.ck = ((const float *)p.ckpt)[((b * p.nchunks + (kc > 0 ? kc - 1 : 0)) * p.D + (dval ? d : 0)) * NP + n];
       }
     }

@@ -396,7 +396,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
 
   const KView vx = p.x, vdt = with_layout<UL>(p.dt, p.x), vz = p.z;  // z keeps its own strides
   const KView vout = with_layout<UL>(p.out, p.x), vB = p.Bm, vC = with_layout<UL>(p.Cm, p.Bm);
-  const bool xt = vx.s1 == 1, bt = vB.s1 == 1, ctt = vC.s1 == 1;
+  const bool bt = vB.s1 == 1, ctt = vC.s1 == 1;
   const bool zt = p.has_z && p.write_out && !SUM;
   const KView vzl = zt ? vz : vx;  // without a gate the z tile re-reads x (never used)
   struct Tiles {
@@ -429,8 +429,9 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
   const __amdgpu_buffer_rsrc_t rbk = flat_buffer(p.ckpt ? (const float *)p.ckpt + b * ckrow : p.x.p,
                                                  p.ckpt ? ckrow * 4 : 0);
   const uint32_t offO = RT::offset(vout, dw, lane);
-  const uint32_t offY = (uint32_t)(ypre_index(!xt, 0, tj, dw + tc, p.L, p.D) * 4);
-  const uint32_t tstepY = (uint32_t)((xt ? 1 : (int)p.D) * CK * 4);
+  // the saved pre-gate output is (B, D, L) whatever x's layout: 64-byte pieces per wavefront
+  const uint32_t offY = (uint32_t)(ypre_index(false, 0, tj, dw + tc, p.L, p.D) * 4);
+  const uint32_t tstepY = (uint32_t)(CK * 4);
   const uint32_t offK = (uint32_t)(((int64_t)d * NP + n) * 4);
   // Every load is unconditional (branch-free), two chunks ahead of the chunk being staged; past
   // the segment's end the prefetch re-reads its last chunk.
@@ -561,7 +562,7 @@ __global__ void __launch_bounds__(kWave * kFwdwWaves) k_fwdw(const FwdParams p) 
     } else {
       if (p.ckpt && dval && live) ((float *)p.ckpt)[((b * p.nchunks + kp) * p.D + d) * NP + n] = h;
       if (st) {
-        if (p.ypre) ((float *)p.ypre)[ypre_index(!xt, b, tg, dd, p.L, p.D)] = o0;
+        if (p.ypre) ((float *)p.ypre)[ypre_index(false, b, tg, dd, p.L, p.D)] = o0;
         if (p.write_out) Conv<IT>::store(vpw<IT>(vout) + b * vout.s0 + row_off<UL>(tg, dd, vout.s1, vout.s2), o);
       }
     }

@@ -112,12 +112,14 @@ struct FwdParams {
   KView dtl, dtw;
   int a_log;   // A holds A_log: the kernel uses -exp(A_log)
   void *ckpt;  // (B, nchunks, D, NP) state type: state at the end of each chunk
-  void *ypre;  // y + D x before the gate (iff gate and saving), state type; laid out
-               // (B, L, D) when x is D-contiguous, else (B, D, L) -- see ypre_index()
+  void *ypre;  // y + D x before the gate (iff gate and saving), state type; the float kernels
+               // lay it out (B, D, L), the float64 ones (B, L, D) when x is D-contiguous, else
+               // (B, D, L) -- see ypre_index()
 };
 
-// Index of (b, t, d) in the saved pre-gate output: it follows x's unit-stride axis so that
-// the forward's writes and the backward's reads are coalesced.
+// Index of (b, t, d) in the saved pre-gate output.  The float kernels always use (B, D, L)
+// (dfast = false): a wavefront's 16 steps x 4 channels are then four 64-byte pieces, where
+// (B, L, D) gives sixteen 16-byte ones.  The float64 kernels follow x's unit-stride axis.
 __host__ __device__ inline int64_t ypre_index(bool dfast, int64_t b, int64_t t, int64_t d, int64_t L, int64_t D) {
   return dfast ? (b * L + t) * D + d : (b * D + d) * L + t;
 }
