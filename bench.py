@@ -206,7 +206,7 @@ def time_steps(step, args, multi=False):
 def bench_c1(args, dev):
     import ssm_scan
     from ssm_scan.synthetic import baseline_inputs
-    B, L, D, N = 16, 512, 512, 16
+    B, L, D, N = args.batch, 512, 512, 16
     t = baseline_inputs(B, L, D, N, gate=True, with_dy=True)
     names = ("u", "delta", "A", "Bm", "Cm", "D", "z")
     leaves = [t[k].to(dev).requires_grad_() for k in names]
@@ -258,8 +258,9 @@ def bench_c1(args, dev):
         "ms_per_step": ms_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "config 1: fused selective-scan fwd+bwd, B16 L512 D512 N16 fp32, "
-                               "zoh, z gate + D skip, channel-major (B,D,L) storage",
+        "config": {"workload": f"config 1: fused selective-scan fwd+bwd, B{B} L512 D512 N16 fp32, "
+                               "zoh, z gate + D skip, channel-major (B,D,L) storage"
+                               + ("" if B == 16 else " (config 1 is B16; this is a batch sweep point)"),
                    "batch": B, "seqlen": L, "dim": D, "dstate": N, "method": "zoh"},
         "hbm_frac_step": (fb + bb) / (ms_step * 1e-3) / (HBM_PEAK_GBS * 1e9),
         "step_mode": step_mode,
@@ -268,7 +269,7 @@ def bench_c1(args, dev):
         "kernels_ms": {"ssm_fwd": fwd_ms, "ssm_bwd": bwd_ms, "ssm_fwd_cold": cold_f, "ssm_bwd_cold": cold_b},
         "kernels_ms_stats": kstats,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic("ssm_bwd_c1"),
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic("ssm_bwd_c1") if B == 16 else None,
                      "kernel": "ssm_bwd (k_bwdw + k_bwd_finalize)", "alg_bytes_per_launch": bb,
                      "fwd_achieved": fb / (fwd_ms * 1e-3) / 1e9},
     }
@@ -829,6 +830,8 @@ def parser():
     ap.add_argument("--seqlen", type=int, default=131072)
     ap.add_argument("--lengths", default="4096,16384,65536", help="long: the sequence lengths")
     ap.add_argument("--segments", type=int, default=0, help="forward time segments (0 = automatic)")
+    ap.add_argument("--batch", type=int, default=16,
+                    help="c1 only: batch rows (16 = config 1; other values are points of a batch sweep)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="report the eager step (no HIP-graph replay)")
     ap.add_argument("--no-extras", action="store_true",
